@@ -1,0 +1,250 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused add + RMSNorm + per-token int8 quantization path on one MI355X.
+
+Default workload: x and residual bf16 [8192, 8192] (1% of channels scaled x20
+as outliers), weight bf16 ~N(1, 0.1), eps 1e-5; output int8 [8192, 8192] + fp32 scales [8192, 1]
++ the bf16 residual written in place.  One step = one call of
+mcoplib_amd.custom_ops.rms_norm_dynamic_per_token_quant (one kernel launch) over one batch that
+is already resident in HBM; three input sets are rotated so consecutive steps do not hit the
+256 MB last-level cache.
+
+Prints ONE JSON line:  value = algorithmic GB/s of the whole job (bytes = every input read once
++ every output written once, 7*T*H + 2*H + 4*T for config 3), plus `roofline` (the kernel's
+average launch duration from HIP events recorded around every launch inside the timed region)
+and `cpu_baseline` (the C oracle on a bounded row sample on this host's cores).
+
+  python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--workload cfg3]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+HBM_PEAK_GBS = 8000.0
+METRIC = "HBM GB/s & % of peak: fused add-RMSNorm+per-token int8 quant, 8192x8192"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="cfg3",
+                    choices=["cfg2", "cfg3", "cfg4", "cfg5-large", "cfg5-decode1",
+                             "cfg5-decode4", "cfg5-decode16", "cfg5-decode64"])
+    ap.add_argument("--sets", type=int, default=3, help="rotated input sets")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+# ------------------------------------------------------------------------------ workloads
+class Workload:
+    """Inputs, a launcher and the byte model of one BASELINE configuration."""
+
+    def __init__(self, name, T, H, eps, kind):
+        self.name, self.T, self.H, self.eps, self.kind = name, T, H, eps, kind
+
+    @property
+    def bytes(self) -> int:
+        T, H = self.T, self.H
+        if self.kind == "add_norm_int8":   # read x, r (2H each), w; write r (2H), q (H), s
+            return 7 * T * H + 2 * H + 4 * T
+        if self.kind == "fused_add":       # read x, r; write x, r; read w
+            return 8 * T * H + 2 * H
+        if self.kind == "smooth_fp8":      # read x; write q, after_res, after_norm; w, smooth, s
+            return 2 * T * H + T * H + 4 * T * H + 2 * H + 4 * H + 4 * T
+        raise ValueError(self.kind)
+
+    def make(self, torch, dev, seed):
+        T, H = self.T, self.H
+        g = torch.Generator(device=dev).manual_seed(seed)
+        x = torch.randn(T, H, generator=g, device=dev)
+        if self.name == "cfg3":
+            idx = torch.randperm(H, generator=torch.Generator().manual_seed(3))[: round(0.01 * H)]
+            x[:, idx.to(dev)] *= 20.0
+        x = x.to(torch.bfloat16)
+        w = (1 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
+        d = {"x": x, "w": w}
+        if self.kind in ("add_norm_int8", "fused_add"):
+            d["r"] = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
+        if self.kind == "add_norm_int8":
+            d["q"] = torch.empty(T, H, dtype=torch.int8, device=dev)
+            d["s"] = torch.empty(T, 1, dtype=torch.float32, device=dev)
+        if self.kind == "smooth_fp8":
+            d["sm"] = 0.5 + 1.5 * torch.rand(H, generator=g, device=dev)
+            d["q"] = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=dev)
+            d["s"] = torch.empty(T, dtype=torch.float32, device=dev)
+            d["ar"] = torch.empty_like(x)
+            d["an"] = torch.empty_like(x)
+        return d
+
+    def launcher(self, torch, d):
+        from mcoplib_amd import op
+        import mcoplib_amd._C  # noqa: F401
+        if self.kind == "add_norm_int8":
+            return lambda: op.rms_norm_dynamic_per_token_quant_custom(
+                d["q"], d["x"], d["w"], d["s"], self.eps, None, d["r"])
+        if self.kind == "fused_add":
+            return lambda: torch.ops._C.fused_add_rms_norm(d["x"], d["r"], d["w"], self.eps)
+        return lambda: op.rms_norm_dynamic_per_token_quant(
+            d["q"], d["x"], d["w"], d["sm"], d["s"], self.eps, d["ar"], d["an"], None)
+
+
+WORKLOADS = {
+    "cfg2": Workload("cfg2", 4096, 4096, 1e-6, "fused_add"),
+    "cfg3": Workload("cfg3", 8192, 8192, 1e-5, "add_norm_int8"),
+    "cfg4": Workload("cfg4", 16384, 7168, 1e-6, "smooth_fp8"),
+    "cfg5-large": Workload("cfg5-large", 32768, 16384, 1e-6, "add_norm_int8"),
+    **{f"cfg5-decode{t}": Workload(f"cfg5-decode{t}", t, 5120, 1e-6, "add_norm_int8")
+       for t in (1, 4, 16, 64)},
+}
+KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "fused_add": "k_fused_add_rms_norm",
+               "smooth_fp8": "k_rms_norm_smooth_quant"}
+
+
+# ------------------------------------------------------------------------------ pieces
+def traffic_from_profiles(wl: Workload):
+    """HBM bytes per dispatch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by
+    a copy kernel's reading), from the committed summary, or None."""
+    p = ROOT / "profiles" / f"{KERNEL_NAME[wl.kind]}_{wl.name}_pmc.txt"
+    if not p.exists():
+        return None
+    m = re.search(r"^hbm_bytes_per_dispatch:\s*([0-9.eE+]+)", p.read_text(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(wl: Workload, seconds: float) -> dict:
+    """The C oracle (oracle/mcop_oracle.c, OpenMP over rows) on a bounded row sample of the same
+    workload, on this host's cores; reported in the metric's unit."""
+    import torch
+    import oracle  # CPU baseline leg only
+
+    cores = len(os.sched_getaffinity(0))
+    oracle.set_threads(cores)
+    rows = min(wl.T, 1024)
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(rows, wl.H, generator=g).to(torch.bfloat16)
+    r = torch.randn(rows, wl.H, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(wl.H, generator=g)).to(torch.bfloat16)
+    sm = 0.5 + 1.5 * torch.rand(wl.H, generator=g)
+
+    def run():
+        if wl.kind == "add_norm_int8":
+            oracle.rms_norm_dynamic_per_token_quant(x, w, wl.eps, torch.int8, residual=r)
+        elif wl.kind == "fused_add":
+            oracle.fused_add_rms_norm(x, r, w, wl.eps)
+        else:
+            oracle.rms_norm_smooth_quant(x, w, sm, wl.eps, torch.float8_e4m3fn)
+
+    run()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 5:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    sample_bytes = Workload(wl.name, rows, wl.H, wl.eps, wl.kind).bytes
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "kind": "port",
+            "sample": f"{rows} of {wl.T} rows x {wl.H} (same byte model), median of {len(times)} "
+                      f"runs over ~{seconds:.0f} s, oracle/mcop_oracle.c with {cores} OpenMP "
+                      f"threads, {cpu_model}",
+            "tokens_per_s": round(rows / med, 1)}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "rows are independent, so N GPUs would each run this kernel on T/N rows with no "
+              "communication -- run with --gpus 1", file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+    sys.path.insert(0, str(ROOT))
+    import mcoplib_amd  # noqa: F401  (fails loudly if libmcop_norm.so is missing)
+
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    wl = WORKLOADS[args.workload]
+    sets = [wl.make(torch, dev, 100 + i) for i in range(max(1, args.sets))]
+    launches = [wl.launcher(torch, d) for d in sets]
+    for i in range(args.warmup):
+        launches[i % len(launches)]()
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(K)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(K):
+        ev[i][0].record()
+        launches[i % len(launches)]()
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_launch_ms = [a.elapsed_time(b) for a, b in ev]
+    total_ms = ev[0][0].elapsed_time(ev[-1][1])
+    ms_per_step = total_ms / K
+    kernel_ms = statistics.mean(per_launch_ms)
+
+    value = wl.bytes / (ms_per_step * 1e-3) / 1e9
+    achieved = wl.bytes / (kernel_ms * 1e-3) / 1e9
+    traffic = traffic_from_profiles(wl)
+    out = {
+        "metric": METRIC if wl.name == "cfg3" else f"HBM GB/s: {wl.name} ({wl.kind}, {wl.T}x{wl.H})",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{wl.name}: {wl.kind} T={wl.T} H={wl.H} bf16 in, "
+                               f"eps={wl.eps}" + (", 1% outlier channels x20" if wl.name == "cfg3" else ""),
+                   "tokens": wl.T, "hidden": wl.H, "io": "bf16 -> int8/fp8 + fp32 scales",
+                   "rotated_input_sets": len(sets)},
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "tokens_per_s": round(wl.T / (ms_per_step * 1e-3), 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic,
+                     "kernel": KERNEL_NAME[wl.kind],
+                     "kernel_avg_us": round(kernel_ms * 1e3, 3),
+                     "algorithmic_bytes_per_launch": wl.bytes},
+        "host_wall_s": round(wall, 4),
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

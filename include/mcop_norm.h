@@ -1,0 +1,137 @@
+/*
+ * mcop_norm.h -- C ABI of libmcop_norm.so, the gfx950 (MI355X) implementation of the fused
+ * RMSNorm + per-token quantization operators of MetaX-MACA/mcoplib.
+ *
+ * Conventions shared by every entry point
+ *   - All tensor arguments are raw device pointers (HIP global memory on the calling device).
+ *     Rows are `hidden_size` elements long and contiguous unless a row stride is given.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the legacy default stream). Every call
+ *     is asynchronous: it only enqueues kernels on `stream` and never synchronizes.
+ *   - The device is the one current on the calling host thread (hipSetDevice); callers that
+ *     hold tensors on another device make it current first.
+ *   - Return value: MCOP_OK (0) or a negative MCOP_E_* code. The message of the last failure on
+ *     the calling thread is returned by mcop_last_error(). Nothing is allocated, no state is
+ *     kept between calls (apart from the tuning override below), and calls are re-entrant.
+ *   - Floating-point inputs may be bf16, fp16 or fp32 (mcop_dtype). Quantized outputs are int8
+ *     or OCP fp8-e4m3fn. Per-token scales are fp32, one per row.
+ *   - Results do not depend on the launch configuration: the row sum of squares is accumulated
+ *     in fp64 and rounded once to fp32, and every other step is a correctly rounded fp32
+ *     operation, so any split of a row over lanes gives the same bits.
+ */
+#ifndef MCOP_NORM_H
+#define MCOP_NORM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  MCOP_BF16 = 0,
+  MCOP_F16 = 1,
+  MCOP_F32 = 2,
+  MCOP_I8 = 3,
+  MCOP_FP8_E4M3FN = 4
+} mcop_dtype;
+
+enum {
+  MCOP_OK = 0,
+  MCOP_E_INVALID = -1,  /* bad argument: null pointer, size, dtype combination */
+  MCOP_E_UNSUPPORTED = -2, /* valid request this build does not implement (e.g. hidden_size too large) */
+  MCOP_E_LAUNCH = -3    /* the HIP runtime rejected the kernel launch */
+};
+
+/* Flags of mcop_rms_norm_smooth_quant. */
+enum {
+  /* Default (bit clear): the reference's literal normalisation u = (a / rho) * w with
+     rho = 1/sqrt(mean(a^2)+eps), i.e. multiplication by sqrt(mean(a^2)+eps)
+     (op/fused_rms_norm_dq.cu:94,139,179). Bit set: the textbook u = (a * rho) * w. */
+  MCOP_SQ_STANDARD_NORM = 1u << 0
+};
+
+/* H1. In-place residual add + RMSNorm (vLLM `_C::fused_add_rms_norm`).
+ *   residual[t,:] <- z = round(input + residual);  input[t,:] <- round(round(z * rho) * weight)
+ *   with rho = 1/sqrt(sum(z^2)/H + eps) computed on the rounded z.
+ * `input_row_stride` is the element stride between rows of `input` (>= hidden_size);
+ * `residual` is contiguous. input, residual and weight share `dtype`.
+ * Replaces fused_add_rms_norm(), op/vllm/layernorm_kernels.cu:243-292
+ * (schema op/vllm/torch_bindings.cpp:161-164). */
+int mcop_fused_add_rms_norm(void* input, int64_t input_row_stride, void* residual,
+                            const void* weight, int64_t num_tokens, int64_t hidden_size,
+                            mcop_dtype dtype, float epsilon, void* stream);
+
+/* H2 / H3. (Residual add +) RMSNorm + dynamic per-token quantization.
+ *   a = input (+ residual); if residual: residual <- round(a)
+ *   rho = 1/sqrt(sum(a^2)/H + eps);  y = round(round(a * rho) * weight)
+ *   A = max|y| (A = min(A, *scale_ub) when scale_ub != NULL)
+ *   int8: s = max(A/127, FLT_EPSILON), q = sat[-128,127](rne(y * (1/s)))
+ *   fp8 : s = max(A/448, 1/(448*512)), q = e4m3fn(clamp(y / s, -448, 448))
+ *   scales[t] = s
+ * `out_dtype` is MCOP_I8 or MCOP_FP8_E4M3FN; input, weight and residual share `in_dtype`;
+ * `scale_ub` is a device pointer to one fp32 value or NULL; `residual` may be NULL.
+ * Replaces rms_norm_dynamic_per_token_quant(),
+ * op/vllm/quantization/fused_kernels/fused_layernorm_dynamic_per_token_quant.cu:163-192
+ * (schema op/vllm/torch_bindings.cpp:216-221), and
+ * rms_norm_dynamic_per_token_quant_custom(), op/rms_norm_dynamic_per_token_quant.cu:266-285
+ * (pybind op/pybind.cpp:55, declaration include/rms_norm_dynamic_per_token_quant.h:2-8). */
+int mcop_rms_norm_dynamic_per_token_quant(void* out, mcop_dtype out_dtype, float* scales,
+                                          const void* input, const void* weight,
+                                          const float* scale_ub, void* residual,
+                                          int64_t num_tokens, int64_t hidden_size,
+                                          mcop_dtype in_dtype, float epsilon, void* stream);
+
+/* H4. SmoothQuant (residual add +) RMSNorm + dynamic per-token quantization
+ * (mcoplib.op.rms_norm_dynamic_per_token_quant, "fused_rms_norm_dq").
+ *   a = input (+ residual, read only); after_res <- round(a)
+ *   rho = 1/sqrt(sum(a^2)/H + eps) on the unrounded a;  a~ = round(a)
+ *   u = (a~ / rho) * w   (or (a~ * rho) * w with MCOP_SQ_STANDARD_NORM); after_norm <- round(u)
+ *   v = u * smooth;  A = max|v|
+ *   int8: s = A/127, q = sat[-127,127](rne(v * (1/s)));  fp8: s = A/448,
+ *   q = e4m3fn(clamp(v * (1/s), -448, 448));  A == 0 gives s = 0 and q = 0.
+ * `weight_dtype` and `smooth_dtype` are each `in_dtype` or MCOP_F32. after_res, after_norm and
+ * residual may be NULL.
+ * Replaces rms_norm_dynamic_per_token_quant(), op/fused_rms_norm_dq.cu:646-667
+ * (pybind op/pybind.cpp:42, declaration include/fused_rms_norm_dq.h:3-12). */
+int mcop_rms_norm_smooth_quant(void* out, mcop_dtype out_dtype, float* scales,
+                               const void* input, const void* weight, mcop_dtype weight_dtype,
+                               const void* smooth, mcop_dtype smooth_dtype, void* after_res,
+                               void* after_norm, const void* residual, int64_t num_tokens,
+                               int64_t hidden_size, mcop_dtype in_dtype, float epsilon,
+                               uint32_t flags, void* stream);
+
+/* H5. Smooth-scale multiply + dynamic per-token int8 quantization, no normalisation.
+ *   v = input * smooth;  A = max|v|;  scales[t] = A * 0.00787401574803f
+ *   q = sat[-128,127](rne(v * (127/A)));  A == 0 gives q = 0.
+ * input is bf16, smooth fp32 [hidden_size], out int8, scales fp32 [num_tokens].
+ * Replaces scale_dynamic_quant(), op/scale_dynamic_quant.cu:127-153
+ * (pybind op/pybind.cpp:51, declaration include/scale_dynamic_quant.h:6-10). */
+int mcop_scale_dynamic_quant(int8_t* out, float* scales, const void* input, const float* smooth,
+                             int64_t num_tokens, int64_t hidden_size, void* stream);
+
+/* The clamp-and-convert step shared by every fp8 epilogue, elementwise:
+ *   out[i] = e4m3fn(clamp(in[i] * mul, -448, 448))   (RNE; clamp with fmin/fmax semantics)
+ * No reference counterpart as an entry point (the step is float_to_fp8,
+ * op/vllm/quantization/fused_kernels/quant_conversions.cuh:23-28); exported so the hardware
+ * conversion can be checked bit for bit against the OCP fp8 definition. */
+int mcop_fp8_e4m3fn_from_f32(uint8_t* out, const float* in, int64_t n, float mul, void* stream);
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* mcop_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int mcop_abi_version(void);
+#define MCOP_ABI_VERSION 1
+
+/* Launch-shape override for the row kernels (no reference counterpart; used by the tuning sweep
+ * and by the tests that check results do not depend on the launch shape).
+ * vectors_per_lane in {0,1,2,4,8}, lanes_per_row in {0} or a multiple of 64 up to 1024;
+ * 0 restores the automatic choice. A request the row does not fit falls back to automatic.
+ * Process-wide; not meant to be changed while other threads launch. */
+int mcop_set_launch_override(int vectors_per_lane, int lanes_per_row);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MCOP_NORM_H */

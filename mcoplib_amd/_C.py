@@ -1,0 +1,109 @@
+"""``torch.ops._C`` surface (the vLLM operator library that mcoplib builds as ``mcoplib._C``).
+
+Importing this module registers, in the ``_C`` torch.library namespace, the schemas of
+op/vllm/torch_bindings.cpp:161-164 (``fused_add_rms_norm``) and :216-221
+(``rms_norm_dynamic_per_token_quant``) with implementations for the CUDA (HIP) dispatch key that
+call libmcop_norm.so.  If another library (vLLM's own ``_C``) already defined a schema, only the
+CUDA implementation is registered over it.  There is no CPU implementation: calling these ops on
+CPU tensors raises, as the reference does.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._checks import dispatch_check, numel_check, on_cuda, rows_of, torch_check
+from .op import _norm_quant
+
+SCHEMAS = {
+    "fused_add_rms_norm":
+        "fused_add_rms_norm(Tensor! input, Tensor! residual, Tensor weight, float epsilon) -> ()",
+    "rms_norm_dynamic_per_token_quant":
+        "rms_norm_dynamic_per_token_quant(Tensor! result, Tensor input, Tensor weight, "
+        "Tensor! scale, float epsilon, Tensor? scale_ub, Tensor!? residual) -> ()",
+}
+
+
+def fused_add_rms_norm(input: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                       epsilon: float) -> None:
+    """In place: residual <- input + residual; input <- RMSNorm(residual) * weight
+    (reference host function op/vllm/layernorm_kernels.cu:243-292)."""
+    name = "fused_add_rms_norm"
+    torch_check(weight.dtype == input.dtype, "weight.scalar_type() == input.scalar_type()")
+    torch_check(input.dtype == residual.dtype, "input.scalar_type() == residual.scalar_type()")
+    torch_check(residual.is_contiguous(), "residual.is_contiguous()")
+    torch_check(weight.is_contiguous(), "weight.is_contiguous()")
+    dispatch_check(input.dtype, "fused_add_rms_norm_kernel")
+    on_cuda(name, input, residual, weight)
+    T, H = rows_of(input)
+    numel_check(name, "residual", residual, T * H)
+    numel_check(name, "weight", weight, H)
+    # Rows of `input` are addressed as row * stride(-2) (the reference's input_stride), which
+    # needs a unit last-dimension stride and uniformly strided rows.
+    if input.dim() >= 2 and T > 1:
+        if input.stride(-1) != 1:
+            raise RuntimeError(f"{name}: input must be contiguous in its last dimension")
+        for d in range(input.dim() - 2):
+            if input.size(d) > 1 and input.stride(d) != input.stride(d + 1) * input.size(d + 1):
+                raise RuntimeError(f"{name}: input rows must be uniformly strided")
+        row_stride = input.stride(-2)
+    else:
+        row_stride = H
+    with _lib.device_of(input):
+        _lib.check(_lib.lib.mcop_fused_add_rms_norm(
+            input.data_ptr(), row_stride, residual.data_ptr(), weight.data_ptr(), T, H,
+            _lib.DTYPE_CODE[input.dtype], float(epsilon), _lib.stream_of(input)))
+
+
+def rms_norm_dynamic_per_token_quant(result: torch.Tensor, input: torch.Tensor,
+                                     weight: torch.Tensor, scale: torch.Tensor, epsilon: float,
+                                     scale_ub: Optional[torch.Tensor] = None,
+                                     residual: Optional[torch.Tensor] = None) -> None:
+    """(Residual add +) RMSNorm + dynamic per-token int8 / fp8-e4m3fn quantization (reference
+    host function
+    op/vllm/quantization/fused_kernels/fused_layernorm_dynamic_per_token_quant.cu:163-192)."""
+    fp8 = torch.float8_e4m3fn
+    torch_check(result.dtype in (fp8, torch.int8),
+                "out.dtype() == kFp8Type || out.dtype() == torch::kInt8")
+    torch_check(result.is_contiguous() and input.is_contiguous(),
+                "out.is_contiguous() && input.is_contiguous()")
+    if scale_ub is not None:
+        torch_check(result.dtype == fp8, "out.dtype() == kFp8Type")
+    torch_check(weight.dtype == input.dtype, "weight.dtype() == input.dtype()")
+    torch_check(scale.dtype == torch.float32, "scales.dtype() == torch::kFloat32")
+    if residual is not None:
+        torch_check(residual.dtype == input.dtype,
+                    "residual->scalar_type() == input.scalar_type()")
+    dispatch_check(input.dtype, "rms_norm_dynamic_per_token_quant_dispatch")
+    _norm_quant("rms_norm_dynamic_per_token_quant", result, input, weight, scale, epsilon,
+                scale_ub, residual)
+
+
+_IMPLS = {
+    "fused_add_rms_norm": fused_add_rms_norm,
+    "rms_norm_dynamic_per_token_quant": rms_norm_dynamic_per_token_quant,
+}
+
+_library = torch.library.Library("_C", "FRAGMENT")
+
+
+def _defined(name: str) -> bool:
+    try:
+        getattr(torch.ops._C, name)
+        return True
+    except (AttributeError, RuntimeError):
+        return False
+
+
+def _meta(*args, **kwargs) -> None:  # mutating ops with no return: nothing to compute
+    return None
+
+
+for _name, _schema in SCHEMAS.items():
+    if not _defined(_name):
+        _library.define(_schema)
+        _library.impl(_name, _meta, "Meta")
+    _library.impl(_name, _IMPLS[_name], "CUDA")

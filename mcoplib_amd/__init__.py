@@ -1,0 +1,19 @@
+"""mcoplib_amd -- MI355X (gfx950) implementation of MetaX-MACA/mcoplib's fused RMSNorm +
+per-token quantization path.
+
+Surfaces (same names, argument order and in-place conventions as the reference):
+  mcoplib_amd.op          -- mcoplib.op: rms_norm_dynamic_per_token_quant (fused_rms_norm_dq),
+                             rms_norm_dynamic_per_token_quant_custom, scale_dynamic_quant
+  mcoplib_amd.custom_ops  -- mcoplib.custom_ops.rms_norm_dynamic_per_token_quant
+  mcoplib_amd._C          -- registers torch.ops._C.fused_add_rms_norm and
+                             torch.ops._C.rms_norm_dynamic_per_token_quant
+
+All of them call libmcop_norm.so (hand-written HIP kernels, C ABI in include/mcop_norm.h).
+Importing the package fails if that library is not built: there is no other implementation.
+"""
+
+from . import _lib  # noqa: F401  (loads libmcop_norm.so; raises ImportError if missing)
+from . import op, custom_ops  # noqa: F401
+
+__version__ = "0.1.0"
+LIBRARY_PATH = str(_lib.LIB_PATH)

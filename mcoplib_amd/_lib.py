@@ -1,0 +1,104 @@
+"""ctypes binding of libmcop_norm.so (the gfx950 kernels and their C ABI, include/mcop_norm.h).
+
+The library is loaded once at import.  There is no fallback: if the library is missing or does
+not export the expected ABI, importing this module raises ImportError, and every operator of the
+package therefore fails loudly instead of computing anything elsewhere.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libmcop_norm.so"
+ABI_VERSION = 1
+
+# mcop_dtype codes (include/mcop_norm.h)
+BF16, F16, F32, I8, FP8_E4M3FN = 0, 1, 2, 3, 4
+DTYPE_CODE = {
+    torch.bfloat16: BF16,
+    torch.float16: F16,
+    torch.float32: F32,
+    torch.int8: I8,
+    torch.float8_e4m3fn: FP8_E4M3FN,
+}
+SQ_STANDARD_NORM = 1
+
+
+def _load() -> ctypes.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is not built; run `python -m mcoplib_amd._build` (hipcc, gfx950)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    P, I64, F, I, U32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int, ctypes.c_uint32
+    lib.mcop_fused_add_rms_norm.argtypes = [P, I64, P, P, I64, I64, I, F, P]
+    lib.mcop_rms_norm_dynamic_per_token_quant.argtypes = [P, I, P, P, P, P, P, I64, I64, I, F, P]
+    lib.mcop_rms_norm_smooth_quant.argtypes = [P, I, P, P, P, I, P, I, P, P, P, I64, I64, I, F,
+                                               U32, P]
+    lib.mcop_scale_dynamic_quant.argtypes = [P, P, P, P, I64, I64, P]
+    lib.mcop_fp8_e4m3fn_from_f32.argtypes = [P, P, I64, F, P]
+    lib.mcop_set_launch_override.argtypes = [I, I]
+    for fn in ("mcop_fused_add_rms_norm", "mcop_rms_norm_dynamic_per_token_quant",
+               "mcop_rms_norm_smooth_quant", "mcop_scale_dynamic_quant",
+               "mcop_fp8_e4m3fn_from_f32", "mcop_set_launch_override", "mcop_abi_version"):
+        getattr(lib, fn).restype = I
+    lib.mcop_last_error.restype = ctypes.c_char_p
+    lib.mcop_last_error.argtypes = []
+    got = lib.mcop_abi_version()
+    if got != ABI_VERSION:
+        raise ImportError(f"{LIB_PATH}: ABI version {got}, expected {ABI_VERSION}")
+    return lib
+
+
+lib = _load()
+
+
+def check(rc: int) -> None:
+    """Raise RuntimeError with the library's message on a non-zero status."""
+    if rc != 0:
+        msg = lib.mcop_last_error().decode("utf-8", "replace")
+        raise RuntimeError(msg or f"libmcop_norm status {rc}")
+
+
+try:  # raw hipStream_t of the current torch stream without building a Stream object
+    _raw_stream = torch._C._cuda_getCurrentRawStream  # type: ignore[attr-defined]
+except AttributeError:  # pragma: no cover
+    _raw_stream = None
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """hipStream_t (as an int) of torch's current stream on t's device."""
+    idx = t.device.index if t.device.index is not None else torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(idx)
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+class device_of:
+    """Make t's device current for the duration of a call (the reference's device guard)."""
+
+    __slots__ = ("idx", "prev")
+
+    def __init__(self, t: torch.Tensor):
+        self.idx = t.device.index
+        self.prev = None
+
+    def __enter__(self):
+        if self.idx is not None:
+            cur = torch.cuda.current_device()
+            if cur != self.idx:
+                self.prev = cur
+                torch.cuda.set_device(self.idx)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+def set_launch_override(vectors_per_lane: int = 0, lanes_per_row: int = 0) -> None:
+    """Force the row kernels' launch shape (0, 0 = automatic). Results do not change."""
+    check(lib.mcop_set_launch_override(int(vectors_per_lane), int(lanes_per_row)))

@@ -1,0 +1,150 @@
+// fused_add_rms_norm.hip -- in-place residual add + RMSNorm (vLLM `_C::fused_add_rms_norm`).
+//
+// Semantics (per row, b() = round to the dtype), following op/vllm/layernorm_kernels.cu:92-144
+// and op/vllm/type_convert.cuh:104-165 of the reference:
+//   z = b(x + r);  residual <- z                     (packed add, :118-125)
+//   rho = 1/sqrt(sum(z^2)/H + eps)  on the rounded z  (:122, :127-133; fp64 sum here)
+//   x <- b(b(z * rho) * w)                            (:136-143: scale then weight multiply)
+// One pass over HBM: x, residual and weight are loaded once into VGPRs, residual is written
+// from registers before the reduction, x after it (8*H bytes per bf16 row, plus the weight).
+#include <hip/hip_runtime.h>
+
+#include "../../include/mcop_norm.h"
+#include "rowkern.h"
+
+namespace mcop {
+
+template <class E, int VEC, int NV>
+__global__ void __launch_bounds__(max_tpr(VEC, NV))
+k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
+                     typename E::S* __restrict__ res, const typename E::S* __restrict__ w,
+                     int64_t rows, int hidden, int tpr, float eps) {
+  using S = typename E::S;
+  __shared__ double red_sum[16];
+  const RowPos p = row_pos(rows, tpr);
+  const int nvec = hidden / VEC;
+  const int64_t xbase = p.row * x_stride, xlbase = p.lrow * x_stride;
+  const int64_t rbase = p.row * (int64_t)hidden, rlbase = p.lrow * (int64_t)hidden;
+
+  Pack<S, VEC> xv[NV], rv[NV], wv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
+    xv[v] = ld<S, VEC>(x + xlbase + lj);
+    rv[v] = ld<S, VEC>(res + rlbase + lj);
+    wv[v] = ld<S, VEC>(w + lj);
+  }
+
+  float z[NV][VEC];
+  double ss = 0.0;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int j = vec_index(v, tpr, p.lt);
+    const bool in = j < nvec;
+    Pack<S, VEC> o;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      o.v[e] = E::from_f(E::to_f(xv[v].v[e]) + E::to_f(rv[v].v[e]));
+      const float t = in ? E::to_f(o.v[e]) : 0.0f;
+      z[v][e] = t;
+      const double d = (double)t;
+      ss = __builtin_fma(d, d, ss);
+    }
+    if (p.live && in) st<S, VEC>(res + rbase + (int64_t)j * VEC, o);
+  }
+
+  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int j = vec_index(v, tpr, p.lt);
+    if (p.live && j < nvec) {
+      Pack<S, VEC> o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        o.v[e] = E::from_f(rnd<E>(z[v][e] * rho) * E::to_f(wv[v].v[e]));
+      }
+      st<S, VEC>(x + xbase + (int64_t)j * VEC, o);
+    }
+  }
+}
+
+template <class E, int VEC>
+static void launch_nv(const Geometry& g, void* x, int64_t xs, void* res, const void* w,
+                      int64_t rows, int hidden, float eps, hipStream_t st) {
+  using S = typename E::S;
+  const dim3 grid((unsigned)g.blocks), block((unsigned)(g.tpr * g.rpb));
+  auto* xp = static_cast<S*>(x);
+  auto* rp = static_cast<S*>(res);
+  auto* wp = static_cast<const S*>(w);
+#define MCOP_LAUNCH(NVV)                                                                    \
+  hipLaunchKernelGGL((k_fused_add_rms_norm<E, VEC, NVV>), grid, block, 0, st, xp, xs, rp, wp, \
+                     rows, hidden, g.tpr, eps)
+  if constexpr (VEC == 1) {
+    if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
+  } else {
+    switch (g.nv) {
+      case 1: MCOP_LAUNCH(1); break;
+      case 2: MCOP_LAUNCH(2); break;
+      case 4: MCOP_LAUNCH(4); break;
+      default: MCOP_LAUNCH(8); break;
+    }
+  }
+#undef MCOP_LAUNCH
+}
+
+template <class E>
+static int dispatch(void* x, int64_t xs, void* res, const void* w, int64_t rows, int64_t hidden,
+                    float eps, hipStream_t st) {
+  constexpr int V = E::VEC;
+  const bool vec_ok = hidden % V == 0 && xs % V == 0 && aligned(16, x, res, w);
+  Geometry g;
+  if (!choose_geometry(rows, hidden, vec_ok ? V : 1, &g)) {
+    return set_error(MCOP_E_UNSUPPORTED,
+                     "fused_add_rms_norm: hidden_size %lld is larger than the register-resident "
+                     "kernels support",
+                     (long long)hidden);
+  }
+  if (g.vec == 1) {
+    launch_nv<E, 1>(g, x, xs, res, w, rows, (int)hidden, eps, st);
+  } else {
+    launch_nv<E, V>(g, x, xs, res, w, rows, (int)hidden, eps, st);
+  }
+  return check_launch("fused_add_rms_norm");
+}
+
+}  // namespace mcop
+
+extern "C" int mcop_fused_add_rms_norm(void* input, int64_t input_row_stride, void* residual,
+                                       const void* weight, int64_t num_tokens,
+                                       int64_t hidden_size, mcop_dtype dtype, float epsilon,
+                                       void* stream) {
+  using namespace mcop;
+  if (num_tokens < 0 || hidden_size <= 0 || hidden_size > INT32_MAX ||
+      input_row_stride < hidden_size) {
+    return set_error(MCOP_E_INVALID,
+                     "fused_add_rms_norm: bad shape num_tokens=%lld hidden_size=%lld "
+                     "input_row_stride=%lld",
+                     (long long)num_tokens, (long long)hidden_size, (long long)input_row_stride);
+  }
+  if (num_tokens == 0) return MCOP_OK;
+  if (!input || !residual || !weight) {
+    return set_error(MCOP_E_INVALID, "fused_add_rms_norm: null pointer");
+  }
+  auto st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MCOP_BF16:
+      return dispatch<BF16>(input, input_row_stride, residual, weight, num_tokens, hidden_size,
+                            epsilon, st);
+    case MCOP_F16:
+      return dispatch<F16>(input, input_row_stride, residual, weight, num_tokens, hidden_size,
+                           epsilon, st);
+    case MCOP_F32:
+      return dispatch<F32>(input, input_row_stride, residual, weight, num_tokens, hidden_size,
+                           epsilon, st);
+    default:
+      return set_error(MCOP_E_INVALID, "fused_add_rms_norm: dtype %d is not bf16/fp16/fp32",
+                       (int)dtype);
+  }
+}

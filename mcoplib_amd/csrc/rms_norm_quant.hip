@@ -1,0 +1,216 @@
+// rms_norm_quant.hip -- (residual add +) RMSNorm + dynamic per-token int8 / fp8-e4m3fn
+// quantization, one pass over HBM.
+//
+// Semantics (per row, a = x [+ r] in fp32, b() = round to the input dtype):
+//   residual <- b(a)                                   fused_..._quant.cu / layernorm_utils.cuh:503-508
+//   rho = 1/sqrt(sum(a^2)/H + eps)                     layernorm_utils.cuh:245-276 (order: fp64 sum)
+//   y = b(b(a*rho) * w)                                layernorm_utils.cuh:436,531
+//   A = max|y|, min(A, *scale_ub)                      layernorm_utils.cuh:440-445
+//   int8: s = max(A/127, FLT_EPSILON); q = sat[-128,127](rne(y * (1/s)))
+//                                                      utils.cuh:46-51, fused_..._quant.cu:37
+//   fp8 : s = max(A/448, 1/(448*512)); q = e4m3fn(clamp(y / s, +-448))  quant_conversions.cuh:23-28
+// (paths relative to op/vllm/quantization/fused_kernels/ and op/vllm/quantization/ of the
+// reference).
+//
+// One pass: every lane loads all of its vectors of x, residual and weight before the first
+// reduction and keeps the row in VGPRs; the residual is written back from registers, the codes
+// are produced from registers, so HBM sees x and residual read once, residual and the codes
+// written once (7*H + 4 bytes per bf16 row with residual).
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+
+#include "../../include/mcop_norm.h"
+#include "rowkern.h"
+
+namespace mcop {
+
+template <class E, int VEC, int NV, bool FP8, bool RES>
+__global__ void __launch_bounds__(max_tpr(VEC, NV))
+k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
+                 const typename E::S* __restrict__ x, const typename E::S* __restrict__ w,
+                 const float* __restrict__ scale_ub, typename E::S* __restrict__ res,
+                 int64_t rows, int hidden, int tpr, float eps) {
+  using S = typename E::S;
+  __shared__ double red_sum[16];
+  __shared__ float red_max[16];
+  const RowPos p = row_pos(rows, tpr);
+  const int nvec = hidden / VEC;
+  const int64_t base = p.row * (int64_t)hidden;
+  const int64_t lbase = p.lrow * (int64_t)hidden;
+
+  // All loads first, unconditionally (out-of-row lanes re-read vector 0 of their row).
+  Pack<S, VEC> xv[NV], rv[NV], wv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
+    xv[v] = ld<S, VEC>(x + lbase + lj);
+    if constexpr (RES) rv[v] = ld<S, VEC>(res + lbase + lj);
+    wv[v] = ld<S, VEC>(w + lj);
+  }
+
+  float a[NV][VEC];
+  double ss = 0.0;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int j = vec_index(v, tpr, p.lt);
+    const bool in = j < nvec;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float t = E::to_f(xv[v].v[e]);
+      if constexpr (RES) t += E::to_f(rv[v].v[e]);
+      t = in ? t : 0.0f;
+      a[v][e] = t;
+      const double d = (double)t;
+      ss = __builtin_fma(d, d, ss);
+    }
+    if constexpr (RES) {
+      if (p.live && in) {
+        Pack<S, VEC> o;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(a[v][e]);
+        st<S, VEC>(res + base + (int64_t)j * VEC, o);
+      }
+    }
+  }
+
+  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+
+  float amax = 0.0f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      // Lanes past the row end hold a == 0, hence y == +-0: no effect on the max.
+      const float y = rnd<E>(rnd<E>(a[v][e] * rho) * E::to_f(wv[v].v[e]));
+      a[v][e] = y;
+      amax = __builtin_fmaxf(amax, __builtin_fabsf(y));
+    }
+  }
+  amax = row_reduce(amax, red_max, tpr, MaxOp());
+
+  float A = amax;
+  if (scale_ub != nullptr) A = __builtin_fminf(A, *scale_ub);
+  const float s = FP8 ? __builtin_fmaxf(mcop_div_rn(A, 448.0f), 1.0f / 229376.0f)
+                      : __builtin_fmaxf(mcop_div_rn(A, 127.0f), FLT_EPSILON);
+  if (p.live && p.lt == 0) scales[p.row] = s;
+  const float inv = mcop_div_rn(1.0f, s);
+  const bool s_ok = mcop_divisor_ok(s);
+
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int j = vec_index(v, tpr, p.lt);
+    if (p.live && j < nvec) {
+      Pack<uint8_t, VEC> q;
+      if constexpr (FP8) {
+        float c[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) c[e] = clamp_fp8(mcop_fdiv_const(a[v][e], s, inv, s_ok));
+        q = cvt_fp8<VEC>(c);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(a[v][e] * inv);
+      }
+      st<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
+    }
+  }
+}
+
+template <class E, int VEC, bool FP8, bool RES>
+static void launch_nv(const Geometry& g, void* out, float* scales, const void* x, const void* w,
+                      const float* scale_ub, void* res, int64_t rows, int hidden, float eps,
+                      hipStream_t st) {
+  using S = typename E::S;
+  const dim3 grid((unsigned)g.blocks), block((unsigned)(g.tpr * g.rpb));
+  auto* o = static_cast<uint8_t*>(out);
+  auto* xp = static_cast<const S*>(x);
+  auto* wp = static_cast<const S*>(w);
+  auto* rp = static_cast<S*>(res);
+#define MCOP_LAUNCH(NVV)                                                                   \
+  hipLaunchKernelGGL((k_rms_norm_quant<E, VEC, NVV, FP8, RES>), grid, block, 0, st, o,     \
+                     scales, xp, wp, scale_ub, rp, rows, hidden, g.tpr, eps)
+  if constexpr (VEC == 1) {
+    if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
+  } else {
+    switch (g.nv) {
+      case 1: MCOP_LAUNCH(1); break;
+      case 2: MCOP_LAUNCH(2); break;
+      case 4: MCOP_LAUNCH(4); break;
+      default: MCOP_LAUNCH(8); break;
+    }
+  }
+#undef MCOP_LAUNCH
+}
+
+template <class E, bool FP8>
+static int dispatch(void* out, float* scales, const void* x, const void* w,
+                    const float* scale_ub, void* res, int64_t rows, int64_t hidden, float eps,
+                    hipStream_t st) {
+  constexpr int V = E::VEC;
+  const bool vec_ok = hidden % V == 0 && aligned(16, x, w, res) && aligned(V, out);
+  Geometry g;
+  if (!choose_geometry(rows, hidden, vec_ok ? V : 1, &g)) {
+    return set_error(MCOP_E_UNSUPPORTED,
+                     "rms_norm_dynamic_per_token_quant: hidden_size %lld is larger than the "
+                     "register-resident kernels support",
+                     (long long)hidden);
+  }
+  const int h = (int)hidden;
+  if (g.vec == 1) {
+    if (res) launch_nv<E, 1, FP8, true>(g, out, scales, x, w, scale_ub, res, rows, h, eps, st);
+    else launch_nv<E, 1, FP8, false>(g, out, scales, x, w, scale_ub, res, rows, h, eps, st);
+  } else {
+    if (res) launch_nv<E, V, FP8, true>(g, out, scales, x, w, scale_ub, res, rows, h, eps, st);
+    else launch_nv<E, V, FP8, false>(g, out, scales, x, w, scale_ub, res, rows, h, eps, st);
+  }
+  return check_launch("rms_norm_dynamic_per_token_quant");
+}
+
+}  // namespace mcop
+
+extern "C" int mcop_rms_norm_dynamic_per_token_quant(void* out, mcop_dtype out_dtype,
+                                                     float* scales, const void* input,
+                                                     const void* weight, const float* scale_ub,
+                                                     void* residual, int64_t num_tokens,
+                                                     int64_t hidden_size, mcop_dtype in_dtype,
+                                                     float epsilon, void* stream) {
+  using namespace mcop;
+  if (num_tokens < 0 || hidden_size <= 0 || hidden_size > INT32_MAX) {
+    return set_error(MCOP_E_INVALID,
+                     "rms_norm_dynamic_per_token_quant: bad shape num_tokens=%lld "
+                     "hidden_size=%lld",
+                     (long long)num_tokens, (long long)hidden_size);
+  }
+  if (num_tokens == 0) return MCOP_OK;
+  if (!out || !scales || !input || !weight) {
+    return set_error(MCOP_E_INVALID, "rms_norm_dynamic_per_token_quant: null pointer");
+  }
+  if (out_dtype != MCOP_I8 && out_dtype != MCOP_FP8_E4M3FN) {
+    return set_error(MCOP_E_INVALID, "rms_norm_dynamic_per_token_quant: out dtype %d is not int8 "
+                     "or fp8_e4m3fn", (int)out_dtype);
+  }
+  const bool fp8 = out_dtype == MCOP_FP8_E4M3FN;
+  auto st = static_cast<hipStream_t>(stream);
+  switch (in_dtype) {
+    case MCOP_BF16:
+      return fp8 ? dispatch<BF16, true>(out, scales, input, weight, scale_ub, residual,
+                                        num_tokens, hidden_size, epsilon, st)
+                 : dispatch<BF16, false>(out, scales, input, weight, scale_ub, residual,
+                                         num_tokens, hidden_size, epsilon, st);
+    case MCOP_F16:
+      return fp8 ? dispatch<F16, true>(out, scales, input, weight, scale_ub, residual,
+                                       num_tokens, hidden_size, epsilon, st)
+                 : dispatch<F16, false>(out, scales, input, weight, scale_ub, residual,
+                                        num_tokens, hidden_size, epsilon, st);
+    case MCOP_F32:
+      return fp8 ? dispatch<F32, true>(out, scales, input, weight, scale_ub, residual,
+                                       num_tokens, hidden_size, epsilon, st)
+                 : dispatch<F32, false>(out, scales, input, weight, scale_ub, residual,
+                                        num_tokens, hidden_size, epsilon, st);
+    default:
+      return set_error(MCOP_E_INVALID,
+                       "rms_norm_dynamic_per_token_quant: input dtype %d is not bf16/fp16/fp32",
+                       (int)in_dtype);
+  }
+}

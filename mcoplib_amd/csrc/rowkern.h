@@ -1,0 +1,206 @@
+// rowkern.h -- building blocks of the gfx950 row kernels (device code) and their launch
+// geometry (host code).
+//
+// Layout model: a row of `hidden` elements is split into vectors of VEC elements (16 bytes on
+// the vector path, one element on the scalar path).  Lane `lt` of a row owns vectors
+// lt, lt + tpr, lt + 2*tpr, ... (NV of them), so every load/store instruction of a wave covers
+// 64 consecutive vectors (1 KiB of bf16 for 16-byte vectors).  A workgroup holds
+// `blockDim.x / tpr` rows; tpr (lanes per row) is a multiple of 64, so a row is a whole number
+// of waves and the row reductions never mix rows inside a wave.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "numerics.h"
+
+namespace mcop {
+
+// ---------------------------------------------------------------------------------------------
+// Element types.  S is the storage type; to_f widens exactly; from_f rounds to nearest even.
+struct BF16 {
+  using S = uint16_t;
+  static constexpr int VEC = 8;
+  static __device__ __forceinline__ float to_f(S s) {
+    return __builtin_bit_cast(float, (uint32_t)s << 16);
+  }
+  static __device__ __forceinline__ S from_f(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);  // v_cvt_pk_bf16_f32, RNE
+  }
+};
+struct F16 {
+  using S = uint16_t;
+  static constexpr int VEC = 8;
+  static __device__ __forceinline__ float to_f(S s) {
+    return (float)__builtin_bit_cast(_Float16, s);
+  }
+  static __device__ __forceinline__ S from_f(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32, RNE
+  }
+};
+struct F32 {
+  using S = float;
+  static constexpr int VEC = 4;
+  static __device__ __forceinline__ float to_f(S s) { return s; }
+  static __device__ __forceinline__ S from_f(float f) { return f; }
+};
+
+// Round an fp32 value to the storage type and widen it back.
+template <class E>
+__device__ __forceinline__ float rnd(float f) {
+  return E::to_f(E::from_f(f));
+}
+
+// N elements of type T as one aligned register block, so that a 4-, 8- or 16-byte block is one
+// global load or store instruction (blocks of 32 bytes become two).
+template <class T, int N>
+struct alignas(sizeof(T) * N) Pack {
+  T v[N];
+};
+
+template <class T, int N>
+__device__ __forceinline__ Pack<T, N> ld(const T* p) {
+  return *reinterpret_cast<const Pack<T, N>*>(p);
+}
+template <class T, int N>
+__device__ __forceinline__ void st(T* p, const Pack<T, N>& v) {
+  *reinterpret_cast<Pack<T, N>*>(p) = v;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Quantizers.
+
+// rne(v) converted to int32 by the hardware conversion, whose results are defined for every
+// input: NaN -> 0, out-of-range values saturate.  Inline VALU asm keeps that definition (a C++
+// cast of NaN is undefined behaviour the compiler may exploit).
+__device__ __forceinline__ int cvt_rne_i32(float v) {
+  int r;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(__builtin_rintf(v)));
+  return r;
+}
+
+// int8 code of v: saturate(rne(v)) to [LO, 127]; NaN -> 0.
+template <int LO>
+__device__ __forceinline__ uint8_t q_i8(float v) {
+  const int i = cvt_rne_i32(v);
+  return (uint8_t)(i < LO ? LO : (i > 127 ? 127 : i));
+}
+
+// OCP fp8 e4m3fn codes of N values already clamped to [-448, 448] (v_cvt_pk_fp8_f32: RNE).
+template <int N>
+__device__ __forceinline__ Pack<uint8_t, N> cvt_fp8(const float* c) {
+  Pack<uint8_t, N> p;
+  if constexpr (N == 1) {
+    const int r = __builtin_amdgcn_cvt_pk_fp8_f32(c[0], c[0], 0, false);
+    p.v[0] = (uint8_t)(r & 0xff);
+  } else {
+    static_assert(N % 4 == 0, "fp8 packs are built 4 codes per dword");
+#pragma unroll
+    for (int d = 0; d < N / 4; ++d) {
+      int r = __builtin_amdgcn_cvt_pk_fp8_f32(c[4 * d + 0], c[4 * d + 1], 0, false);
+      r = __builtin_amdgcn_cvt_pk_fp8_f32(c[4 * d + 2], c[4 * d + 3], r, true);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) p.v[4 * d + k] = (uint8_t)((uint32_t)r >> (8 * k));
+    }
+  }
+  return p;
+}
+
+// clamp(v, -448, 448) with fmin/fmax semantics (a NaN operand yields the other operand), as
+// the reference's float_to_fp8 does before its conversion.
+__device__ __forceinline__ float clamp_fp8(float v) {
+  return __builtin_fmaxf(-448.0f, __builtin_fminf(v, 448.0f));
+}
+
+// ---------------------------------------------------------------------------------------------
+// Row reductions.  Every thread of the workgroup must call them (they may contain a barrier).
+// `lds` holds one slot per wave of the workgroup (at most 16).  The sum is of fp64 partials;
+// its result is independent of the order up to fp64 rounding, which the single rounding to
+// fp32 afterwards absorbs.
+
+struct SumOp {
+  __device__ __forceinline__ double operator()(double a, double b) const { return a + b; }
+};
+struct MaxOp {
+  __device__ __forceinline__ float operator()(float a, float b) const {
+    return __builtin_fmaxf(a, b);
+  }
+};
+
+template <class T, class Op>
+__device__ __forceinline__ T wave_reduce(T v, Op op) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = op(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+template <class T, class Op>
+__device__ __forceinline__ T row_reduce(T v, T* lds, int tpr, Op op) {
+  v = wave_reduce(v, op);
+  if (tpr == 64) return v;  // the row is one wave
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) lds[wave] = v;
+  __syncthreads();
+  const int wpr = tpr >> 6;
+  const int first = (wave / wpr) * wpr;
+  T t = lds[first];
+  for (int i = 1; i < wpr; ++i) t = op(t, lds[first + i]);
+  return t;
+}
+
+// Position of this thread: its row and its lane within the row.  `lrow` is the row its loads
+// use: the last row for lanes of a workgroup's trailing rows past the end, so that every load
+// of the kernel is unconditional (no branch, hence no wait, between the loads of a lane); such
+// lanes store nothing.
+struct RowPos {
+  int64_t row;
+  int64_t lrow;
+  int lt;
+  bool live;
+};
+__device__ __forceinline__ RowPos row_pos(int64_t num_rows, int tpr) {
+  const int rpb = blockDim.x / tpr;
+  RowPos p;
+  p.row = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
+  p.lt = threadIdx.x % tpr;
+  p.live = p.row < num_rows;
+  p.lrow = p.live ? p.row : num_rows - 1;
+  return p;
+}
+
+// Vector index of a lane's v-th vector, and the index its loads use (0 when past the row end,
+// so the load stays inside the row and is discarded).
+__device__ __forceinline__ int vec_index(int v, int tpr, int lt) { return v * tpr + lt; }
+__device__ __forceinline__ int load_index(int j, int nvec) { return j < nvec ? j : 0; }
+
+// Largest lanes-per-row a kernel with NV vectors of VEC elements per lane is compiled for:
+// 1024 keeps at most 128 VGPRs per lane, which rows of 4 or 8 16-byte vectors per lane exceed,
+// so those are compiled for 512 lanes (256 VGPRs).
+__host__ __device__ constexpr int max_tpr(int vec, int nv) { return (vec > 1 && nv >= 4) ? 512 : 1024; }
+
+}  // namespace mcop
+
+// ---------------------------------------------------------------------------------------------
+// Host side: launch geometry and error reporting shared by the entry points.
+namespace mcop {
+
+struct Geometry {
+  int vec;     // elements per vector (1 = scalar path)
+  int nv;      // vectors per lane
+  int tpr;     // lanes per row (multiple of 64, <= 1024)
+  int rpb;     // rows per workgroup
+  int64_t blocks;
+};
+
+// Picks the launch shape of a row kernel. `vec` is 1 or the 16-byte vector width; returns false
+// when the row does not fit (hidden too large for the register-resident kernels).
+bool choose_geometry(int64_t rows, int64_t hidden, int vec, Geometry* g);
+
+// True when every non-null pointer is aligned to `bytes`.
+bool aligned(int bytes, const void* p0, const void* p1 = nullptr, const void* p2 = nullptr,
+             const void* p3 = nullptr, const void* p4 = nullptr, const void* p5 = nullptr);
+
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+}  // namespace mcop

@@ -1,0 +1,150 @@
+"""``mcoplib.op`` surface of the fused norm/quant path, backed by libmcop_norm.so (gfx950).
+
+Functions keep the reference pybind signatures (op/pybind.cpp:42, 51, 55; declarations in
+include/fused_rms_norm_dq.h:3-12, include/rms_norm_dynamic_per_token_quant.h:2-8,
+include/scale_dynamic_quant.h:6-10), their positional argument order, in-place outputs and
+error behaviour.  Every call enqueues one kernel on torch's current stream of the tensors'
+device and returns without synchronizing.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._checks import (contiguous_check, dispatch_check, numel_check, on_cuda, rows_of,
+                      torch_check)
+
+__all__ = [
+    "rms_norm_dynamic_per_token_quant",
+    "rms_norm_dynamic_per_token_quant_custom",
+    "scale_dynamic_quant",
+]
+
+
+def rms_norm_dynamic_per_token_quant(out: torch.Tensor, input: torch.Tensor,
+                                     weight: torch.Tensor, smooth_scale: torch.Tensor,
+                                     scales: torch.Tensor, var_epsilon: float,
+                                     after_res: torch.Tensor, after_norm: torch.Tensor,
+                                     residual: Optional[torch.Tensor] = None,
+                                     standard_norm: bool = False) -> None:
+    """SmoothQuant (residual add +) RMSNorm + dynamic per-token quantization
+    ("fused_rms_norm_dq"; reference entry op/fused_rms_norm_dq.cu:646-667).
+
+    after_res <- input (+ residual); after_norm <- after_res / rsqrt(mean(after_res^2) + eps)
+    * weight (the reference's literal form; ``standard_norm=True`` multiplies by the rsqrt
+    instead); out <- per-token quantization of after_norm * smooth_scale; scales[t] <- absmax/127
+    (int8) or absmax/448 (fp8-e4m3fn, an extension: the reference accepts int8 only).
+    ``residual`` is read, not updated.  weight and smooth_scale are each the input dtype or fp32.
+    """
+    name = "rms_norm_dynamic_per_token_quant"
+    torch_check(out.dtype in (torch.int8, torch.float8_e4m3fn),
+                "out.dtype() == torch::kInt8 || out.dtype() == torch::kFloat8_e4m3fn")
+    torch_check(out.is_contiguous() and input.is_contiguous(),
+                "out.is_contiguous() && input.is_contiguous()")
+    torch_check(scales.dtype == torch.float32, "scales.dtype() == torch::kFloat32")
+    dispatch_check(input.dtype, "rms_norm_dynamic_per_token_quant_dispatch")
+    on_cuda(name, out, input, weight, smooth_scale, scales, after_res, after_norm, residual)
+    T, H = rows_of(input)
+    numel_check(name, "out", out, T * H)
+    numel_check(name, "weight", weight, H)
+    numel_check(name, "smooth_scale", smooth_scale, H)
+    numel_check(name, "scales", scales, T)
+    for what, t in (("weight", weight), ("smooth_scale", smooth_scale), ("scales", scales),
+                    ("after_res", after_res), ("after_norm", after_norm)):
+        contiguous_check(name, what, t)
+    for what, t in (("after_res", after_res), ("after_norm", after_norm)):
+        numel_check(name, what, t, T * H)
+        if t.dtype != input.dtype:
+            raise RuntimeError(f"{name}: {what} must have the input dtype {input.dtype}")
+    if residual is not None:
+        if residual.dtype != input.dtype:
+            raise RuntimeError(f"{name}: residual must have the input dtype {input.dtype}")
+        contiguous_check(name, "residual", residual)
+        numel_check(name, "residual", residual, T * H)
+    for what, t in (("weight", weight), ("smooth_scale", smooth_scale)):
+        if t.dtype not in (input.dtype, torch.float32):
+            raise RuntimeError(f"{name}: {what} must be {input.dtype} or float32, got {t.dtype}")
+    with _lib.device_of(input):
+        _lib.check(_lib.lib.mcop_rms_norm_smooth_quant(
+            out.data_ptr(), _lib.DTYPE_CODE[out.dtype], scales.data_ptr(), input.data_ptr(),
+            weight.data_ptr(), _lib.DTYPE_CODE[weight.dtype], smooth_scale.data_ptr(),
+            _lib.DTYPE_CODE[smooth_scale.dtype], after_res.data_ptr(), after_norm.data_ptr(),
+            None if residual is None else residual.data_ptr(), T, H,
+            _lib.DTYPE_CODE[input.dtype], float(var_epsilon),
+            _lib.SQ_STANDARD_NORM if standard_norm else 0, _lib.stream_of(input)))
+
+
+def rms_norm_dynamic_per_token_quant_custom(out: torch.Tensor, input: torch.Tensor,
+                                            weight: torch.Tensor, scales: torch.Tensor,
+                                            var_epsilon: float,
+                                            scale_ub: Optional[torch.Tensor] = None,
+                                            residual: Optional[torch.Tensor] = None) -> None:
+    """(Residual add +) RMSNorm + dynamic per-token int8 quantization (reference entry
+    op/rms_norm_dynamic_per_token_quant.cu:266-285).  ``residual`` is updated in place to
+    input + residual; out and scales ([T] or [T, 1] fp32) are written."""
+    name = "rms_norm_dynamic_per_token_quant_custom"
+    torch_check(out.dtype == torch.int8, "out.dtype() == torch::kInt8")
+    torch_check(out.is_contiguous() and input.is_contiguous(),
+                "out.is_contiguous() && input.is_contiguous()")
+    torch_check(scales.dtype == torch.float32, "scales.dtype() == torch::kFloat32")
+    dispatch_check(input.dtype, " rms_norm_dynamic_per_token_quant_dispatch_")
+    _norm_quant(name, out, input, weight, scales, var_epsilon, scale_ub, residual)
+
+
+def _norm_quant(name: str, out: torch.Tensor, input: torch.Tensor, weight: torch.Tensor,
+                scales: torch.Tensor, eps: float, scale_ub: Optional[torch.Tensor],
+                residual: Optional[torch.Tensor]) -> None:
+    """Shared launcher of the (residual add +) RMSNorm + per-token quant kernel."""
+    on_cuda(name, out, input, weight, scales, scale_ub, residual)
+    T, H = rows_of(input)
+    numel_check(name, "out", out, T * H)
+    numel_check(name, "weight", weight, H)
+    numel_check(name, "scales", scales, T)
+    contiguous_check(name, "weight", weight)
+    contiguous_check(name, "scales", scales)
+    if weight.dtype != input.dtype:
+        raise RuntimeError(f"{name}: weight must have the input dtype {input.dtype}")
+    if residual is not None:
+        if residual.dtype != input.dtype:
+            raise RuntimeError(f"{name}: residual must have the input dtype {input.dtype}")
+        contiguous_check(name, "residual", residual)
+        numel_check(name, "residual", residual, T * H)
+    if scale_ub is not None:
+        if scale_ub.dtype != torch.float32 or scale_ub.numel() < 1:
+            raise RuntimeError(f"{name}: scale_ub must be a float32 tensor with one element")
+    with _lib.device_of(input):
+        _lib.check(_lib.lib.mcop_rms_norm_dynamic_per_token_quant(
+            out.data_ptr(), _lib.DTYPE_CODE[out.dtype], scales.data_ptr(), input.data_ptr(),
+            weight.data_ptr(), None if scale_ub is None else scale_ub.data_ptr(),
+            None if residual is None else residual.data_ptr(), T, H,
+            _lib.DTYPE_CODE[input.dtype], float(eps), _lib.stream_of(input)))
+
+
+def scale_dynamic_quant(hidden_states: torch.Tensor, smooth_scales: torch.Tensor,
+                        dst_dtype: torch.dtype = torch.int8
+                        ) -> tuple[torch.Tensor, torch.Tensor]:
+    """Smooth-scale multiply + dynamic per-token int8 quantization (reference entry
+    op/scale_dynamic_quant.cu:127-153).  Returns new (codes shaped like hidden_states,
+    scales [T] fp32)."""
+    torch_check(hidden_states.is_cuda, "hidden_states.is_cuda()")
+    torch_check(smooth_scales.is_cuda, "smooth_scales.is_cuda()")
+    T, H = rows_of(hidden_states)
+    output = torch.empty_like(hidden_states, dtype=dst_dtype)
+    scales = torch.empty((T,), dtype=smooth_scales.dtype, device=smooth_scales.device)
+    if not (hidden_states.dtype == torch.bfloat16 and dst_dtype == torch.int8):
+        raise RuntimeError("Only support bfloat16")
+    name = "scale_dynamic_quant"
+    on_cuda(name, hidden_states, smooth_scales)
+    contiguous_check(name, "hidden_states", hidden_states)
+    contiguous_check(name, "smooth_scales", smooth_scales)
+    numel_check(name, "smooth_scales", smooth_scales, H)
+    if smooth_scales.dtype != torch.float32:
+        raise RuntimeError(f"{name}: smooth_scales must be float32")
+    with _lib.device_of(hidden_states):
+        _lib.check(_lib.lib.mcop_scale_dynamic_quant(
+            output.data_ptr(), scales.data_ptr(), hidden_states.data_ptr(),
+            smooth_scales.data_ptr(), T, H, _lib.stream_of(hidden_states)))
+    return output, scales

@@ -1,0 +1,135 @@
+"""The C-ABI library and the Python surfaces, without a GPU: the library loads, exports every
+entry point include/mcop_norm.h declares, and rejects bad arguments before touching the device;
+the Python surfaces reproduce the reference's argument checks."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import mcoplib_amd
+from mcoplib_amd import _lib, op, custom_ops
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "mcop_norm.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(mcop_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    names = _declared()
+    assert "mcop_rms_norm_dynamic_per_token_quant" in names and len(names) >= 8
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in {HEADER.name} but not exported"
+
+
+def test_abi_version_and_error_channel():
+    assert _lib.lib.mcop_abi_version() == 1
+    assert mcoplib_amd.LIBRARY_PATH.endswith("libmcop_norm.so")
+
+
+def _err():
+    return _lib.lib.mcop_last_error().decode()
+
+
+def test_c_abi_rejects_bad_arguments_without_a_device():
+    L = _lib.lib
+    # zero rows: nothing to do
+    assert L.mcop_rms_norm_dynamic_per_token_quant(None, 3, None, None, None, None, None, 0, 64,
+                                                   0, 1e-6, None) == 0
+    assert L.mcop_fused_add_rms_norm(None, 64, None, None, 0, 64, 0, 1e-6, None) == 0
+    # bad shapes
+    assert L.mcop_rms_norm_dynamic_per_token_quant(None, 3, None, None, None, None, None, 4, 0,
+                                                   0, 1e-6, None) == -1
+    assert "bad shape" in _err()
+    assert L.mcop_fused_add_rms_norm(None, 32, None, None, 4, 64, 0, 1e-6, None) == -1
+    assert "input_row_stride" in _err()
+    assert L.mcop_scale_dynamic_quant(None, None, None, None, -1, 8, None) == -1
+    # null pointers
+    assert L.mcop_rms_norm_dynamic_per_token_quant(None, 3, None, None, None, None, None, 4, 64,
+                                                   0, 1e-6, None) == -1
+    assert "null pointer" in _err()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    # output dtype must be int8 / fp8
+    assert L.mcop_rms_norm_dynamic_per_token_quant(p, 0, p, p, p, None, None, 4, 64, 0, 1e-6,
+                                                   None) == -1
+    assert "out dtype" in _err()
+    # input dtype must be bf16 / fp16 / fp32
+    assert L.mcop_rms_norm_dynamic_per_token_quant(p, 3, p, p, p, None, None, 4, 64, 3, 1e-6,
+                                                   None) == -1
+    assert "input dtype" in _err()
+    assert L.mcop_fused_add_rms_norm(p, 64, p, p, 4, 64, 4, 1e-6, None) == -1
+    # smooth quant: weight / smooth dtype combinations
+    assert L.mcop_rms_norm_smooth_quant(p, 3, p, p, p, 1, p, 2, None, None, None, 4, 64, 0, 1e-6,
+                                        0, None) == -1
+    assert "weight dtype" in _err()
+    assert L.mcop_rms_norm_smooth_quant(p, 3, p, p, p, 0, p, 2, None, None, None, 4, 64, 2, 1e-6,
+                                        0, None) == -1
+    assert "fp32 input" in _err()
+    # launch override validation
+    assert L.mcop_set_launch_override(2, 100) == -1
+    assert L.mcop_set_launch_override(0, 0) == 0
+
+
+def test_reference_checks_on_the_python_surfaces():
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    w = torch.ones(64, dtype=torch.bfloat16)
+    s = torch.zeros(4, 1)
+    with pytest.raises(RuntimeError, match=r"Expected out.dtype\(\) == torch::kInt8"):
+        op.rms_norm_dynamic_per_token_quant_custom(torch.empty(4, 64, dtype=torch.float16), x, w,
+                                                   s, 1e-6)
+    with pytest.raises(RuntimeError, match="scales.dtype"):
+        op.rms_norm_dynamic_per_token_quant_custom(torch.empty(4, 64, dtype=torch.int8), x, w,
+                                                   s.double(), 1e-6)
+    with pytest.raises(RuntimeError, match="is_contiguous"):
+        op.rms_norm_dynamic_per_token_quant_custom(torch.empty(64, 4, dtype=torch.int8).t(), x,
+                                                   w, s, 1e-6)
+    with pytest.raises(RuntimeError, match="not implemented for 'Int'"):
+        op.rms_norm_dynamic_per_token_quant_custom(torch.empty(4, 64, dtype=torch.int8),
+                                                   x.int(), w, s, 1e-6)
+    # CPU tensors never reach the library
+    with pytest.raises(RuntimeError, match="CUDA"):
+        op.rms_norm_dynamic_per_token_quant_custom(torch.empty(4, 64, dtype=torch.int8), x, w, s,
+                                                   1e-6)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        custom_ops.rms_norm_dynamic_per_token_quant(x, w, 1e-6, torch.int8)
+    with pytest.raises(RuntimeError):
+        op.scale_dynamic_quant(x, torch.ones(64), torch.int8)
+    sm = torch.ones(64)
+    with pytest.raises(RuntimeError, match=r"out.dtype\(\) == torch::kInt8"):
+        op.rms_norm_dynamic_per_token_quant(torch.empty(4, 64), x, w, sm, torch.zeros(4), 1e-6,
+                                            torch.empty_like(x), torch.empty_like(x))
+
+
+def test_torch_library_schemas_registered():
+    import mcoplib_amd._C  # noqa: F401
+
+    fa = torch.ops._C.fused_add_rms_norm.default._schema
+    assert [a.name for a in fa.arguments] == ["input", "residual", "weight", "epsilon"]
+    assert [a.alias_info is not None and a.alias_info.is_write for a in fa.arguments] == [
+        True, True, False, False]
+    assert len(fa.returns) == 0
+    rq = torch.ops._C.rms_norm_dynamic_per_token_quant.default._schema
+    assert [a.name for a in rq.arguments] == ["result", "input", "weight", "scale", "epsilon",
+                                              "scale_ub", "residual"]
+    assert [a.alias_info is not None and a.alias_info.is_write for a in rq.arguments] == [
+        True, False, False, True, False, False, True]
+    assert len(rq.returns) == 0
+    # no CPU implementation: the dispatcher refuses CPU tensors
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        torch.ops._C.fused_add_rms_norm(x, x.clone(), torch.ones(64, dtype=torch.bfloat16), 1e-6)
+    # the CUDA implementations apply the reference's checks before any device work
+    from mcoplib_amd import _C
+    with pytest.raises(RuntimeError, match="weight.scalar_type"):
+        _C.fused_add_rms_norm(x, x.clone(), torch.ones(64), 1e-6)
+    with pytest.raises(RuntimeError, match="kFp8Type"):
+        _C.rms_norm_dynamic_per_token_quant(
+            torch.empty(4, 64, dtype=torch.int8), x, torch.ones(64, dtype=torch.bfloat16),
+            torch.zeros(4, 1), 1e-6, torch.ones(1), None)
