@@ -40,7 +40,8 @@ def parse():
     ap.add_argument("--workload", default="cfg3",
                     choices=["cfg2", "cfg3", "cfg4", "cfg5-large", "cfg5-decode1",
                              "cfg5-decode4", "cfg5-decode16", "cfg5-decode64"])
-    ap.add_argument("--sets", type=int, default=3, help="rotated input sets")
+    ap.add_argument("--sets", type=int, default=0,
+                    help="rotated input sets (default: enough for > 1 GiB, at least 3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     return ap.parse_args()
@@ -188,26 +189,42 @@ def main() -> int:
     dev = "cuda:0"
     torch.cuda.set_device(0)
     wl = WORKLOADS[args.workload]
-    sets = [wl.make(torch, dev, 100 + i) for i in range(max(1, args.sets))]
+    n_sets = args.sets or max(3, -(-(1 << 30) // wl.bytes))
+    sets = [wl.make(torch, dev, 100 + i) for i in range(n_sets)]
     launches = [wl.launcher(torch, d) for d in sets]
-    for i in range(args.warmup):
+    # warm-up: the requested steps, continued until the GPU has been busy for ~2 s so that
+    # clocks and power state have settled before the timed region
+    i, t_w = 0, time.perf_counter()
+    while i < args.warmup or time.perf_counter() - t_w < 2.0:
         launches[i % len(launches)]()
+        i += 1
+        if i % 64 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
 
     K = args.steps
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(K)]
+    # (1) whole-job throughput: K back-to-back steps between two events
+    t_start, t_stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    t_start.record()
+    for i in range(K):
+        launches[i % len(launches)]()
+    t_stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = t_start.elapsed_time(t_stop)
+    ms_per_step = total_ms / K
+    # (2) the kernel's average launch duration: the same K steps with an event pair around
+    # every launch (on torch's current stream, the stream the kernel is launched on)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(K)]
     for i in range(K):
         ev[i][0].record()
         launches[i % len(launches)]()
         ev[i][1].record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     per_launch_ms = [a.elapsed_time(b) for a, b in ev]
-    total_ms = ev[0][0].elapsed_time(ev[-1][1])
-    ms_per_step = total_ms / K
     kernel_ms = statistics.mean(per_launch_ms)
 
     value = wl.bytes / (ms_per_step * 1e-3) / 1e9

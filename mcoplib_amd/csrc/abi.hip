@@ -45,7 +45,7 @@ bool aligned(int bytes, const void* p0, const void* p1, const void* p2, const vo
   return true;
 }
 
-// Vector path: vectors per lane nv in {1,2,4,8}; the default is two 16-byte vectors per tensor
+// Vector path: vectors per lane nv in {1,2,4,8,16}; the default is two 16-byte vectors per tensor
 // per lane (enough loads in flight per wave while keeping VGPR use near 64), one for rows of at
 // most 64 vectors.  Scalar path (hidden not a multiple of the vector width, or misaligned
 // pointers): nv in {4,16}.  Rows narrower than 256 lanes are packed several per workgroup.
@@ -55,7 +55,7 @@ bool choose_geometry(int64_t rows, int64_t hidden, int vec, Geometry* g) {
   int64_t tpr = 0;
   const int onv = g_over_nv.load(std::memory_order_relaxed);
   const int otpr = g_over_tpr.load(std::memory_order_relaxed);
-  const bool nv_allowed = vec > 1 ? (onv == 1 || onv == 2 || onv == 4 || onv == 8)
+  const bool nv_allowed = vec > 1 ? (onv == 1 || onv == 2 || onv == 4 || onv == 8 || onv == 16)
                                   : (onv == 4 || onv == 16);
   if (nv_allowed) {
     const int64_t t = otpr > 0 ? otpr : round64(ceil_div(nvec, onv));
@@ -66,7 +66,7 @@ bool choose_geometry(int64_t rows, int64_t hidden, int vec, Geometry* g) {
   }
   if (nv == 0) {
     if (vec > 1) {
-      for (int cand : {1, 2, 4, 8}) {
+      for (int cand : {1, 2, 4, 8, 16}) {
         if (cand == 1 && nvec > 64) continue;
         const int64_t t = round64(ceil_div(nvec, cand));
         if (t <= max_tpr(vec, cand)) {

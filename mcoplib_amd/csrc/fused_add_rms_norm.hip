@@ -30,8 +30,8 @@ k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
-    xv[v] = ld<S, VEC>(x + xlbase + lj);
-    rv[v] = ld<S, VEC>(res + rlbase + lj);
+    xv[v] = ld_nt<S, VEC>(x + xlbase + lj);
+    rv[v] = ld_nt<S, VEC>(res + rlbase + lj);
     wv[v] = ld<S, VEC>(w + lj);
   }
 
@@ -50,7 +50,7 @@ k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
       const double d = (double)t;
       ss = __builtin_fma(d, d, ss);
     }
-    if (p.live && in) st<S, VEC>(res + rbase + (int64_t)j * VEC, o);
+    if (p.live && in) st_nt<S, VEC>(res + rbase + (int64_t)j * VEC, o);
   }
 
   ss = row_reduce(ss, red_sum, tpr, SumOp());
@@ -65,7 +65,7 @@ k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
       for (int e = 0; e < VEC; ++e) {
         o.v[e] = E::from_f(rnd<E>(z[v][e] * rho) * E::to_f(wv[v].v[e]));
       }
-      st<S, VEC>(x + xbase + (int64_t)j * VEC, o);
+      st_nt<S, VEC>(x + xbase + (int64_t)j * VEC, o);
     }
   }
 }
@@ -88,7 +88,8 @@ static void launch_nv(const Geometry& g, void* x, int64_t xs, void* res, const v
       case 1: MCOP_LAUNCH(1); break;
       case 2: MCOP_LAUNCH(2); break;
       case 4: MCOP_LAUNCH(4); break;
-      default: MCOP_LAUNCH(8); break;
+      case 8: MCOP_LAUNCH(8); break;
+      default: MCOP_LAUNCH(16); break;
     }
   }
 #undef MCOP_LAUNCH

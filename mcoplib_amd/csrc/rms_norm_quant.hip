@@ -44,8 +44,8 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
-    xv[v] = ld<S, VEC>(x + lbase + lj);
-    if constexpr (RES) rv[v] = ld<S, VEC>(res + lbase + lj);
+    xv[v] = ld_nt<S, VEC>(x + lbase + lj);
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(res + lbase + lj);
     wv[v] = ld<S, VEC>(w + lj);
   }
 
@@ -69,7 +69,7 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
         Pack<S, VEC> o;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(a[v][e]);
-        st<S, VEC>(res + base + (int64_t)j * VEC, o);
+        st_nt<S, VEC>(res + base + (int64_t)j * VEC, o);
       }
     }
   }
@@ -105,14 +105,15 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
       Pack<uint8_t, VEC> q;
       if constexpr (FP8) {
         float c[VEC];
+        div_by_const<VEC>(c, a[v], s, inv, s_ok);
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) c[e] = clamp_fp8(mcop_fdiv_const(a[v][e], s, inv, s_ok));
+        for (int e = 0; e < VEC; ++e) c[e] = clamp_fp8(c[e]);
         q = cvt_fp8<VEC>(c);
       } else {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(a[v][e] * inv);
       }
-      st<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
+      st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
     }
   }
 }
@@ -137,7 +138,8 @@ static void launch_nv(const Geometry& g, void* out, float* scales, const void* x
       case 1: MCOP_LAUNCH(1); break;
       case 2: MCOP_LAUNCH(2); break;
       case 4: MCOP_LAUNCH(4); break;
-      default: MCOP_LAUNCH(8); break;
+      case 8: MCOP_LAUNCH(8); break;
+      default: MCOP_LAUNCH(16); break;
     }
   }
 #undef MCOP_LAUNCH

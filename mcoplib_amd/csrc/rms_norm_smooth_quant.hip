@@ -49,8 +49,8 @@ k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
-    xv[v] = ld<S, VEC>(x + lbase + lj);
-    if constexpr (RES) rv[v] = ld<S, VEC>(res + lbase + lj);
+    xv[v] = ld_nt<S, VEC>(x + lbase + lj);
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(res + lbase + lj);
     wv[v].p = ld<typename EW::S, VEC>(w + lj);
     sv[v].p = ld<typename ES::S, VEC>(sm + lj);
   }
@@ -72,7 +72,7 @@ k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
       ss = __builtin_fma(d, d, ss);
       a[v][e] = E::to_f(o.v[e]);  // b(a): what the later passes of the reference re-read
     }
-    if (ares != nullptr && p.live && in) st<S, VEC>(ares + base + (int64_t)j * VEC, o);
+    if (ares != nullptr && p.live && in) st_nt<S, VEC>(ares + base + (int64_t)j * VEC, o);
   }
 
   ss = row_reduce(ss, red_sum, tpr, SumOp());
@@ -86,16 +86,22 @@ k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
     Pack<S, VEC> o;
+    float n[VEC];
+    if (standard) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) n[e] = a[v][e] * rho;
+    } else {
+      div_by_const<VEC>(n, a[v], rho, inv_rho, rho_ok);
+    }
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const float n = standard ? a[v][e] * rho : mcop_fdiv_const(a[v][e], rho, inv_rho, rho_ok);
-      const float u = n * wv[v].at(e);
+      const float u = n[e] * wv[v].at(e);
       o.v[e] = E::from_f(u);
       const float vv = u * sv[v].at(e);
       a[v][e] = vv;
       amax = __builtin_fmaxf(amax, __builtin_fabsf(vv));
     }
-    if (anorm != nullptr && p.live && j < nvec) st<S, VEC>(anorm + base + (int64_t)j * VEC, o);
+    if (anorm != nullptr && p.live && j < nvec) st_nt<S, VEC>(anorm + base + (int64_t)j * VEC, o);
   }
   amax = row_reduce(amax, red_max, tpr, MaxOp());
 
@@ -117,7 +123,7 @@ k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 #pragma unroll
         for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-127>(a[v][e] * inv);
       }
-      st<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
+      st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
     }
   }
 }
@@ -159,7 +165,8 @@ static void launch_nv(const Geometry& g, const Args& a, hipStream_t st) {
       case 1: MCOP_LAUNCH(1); break;
       case 2: MCOP_LAUNCH(2); break;
       case 4: MCOP_LAUNCH(4); break;
-      default: MCOP_LAUNCH(8); break;
+      case 8: MCOP_LAUNCH(8); break;
+      default: MCOP_LAUNCH(16); break;
     }
   }
 #undef MCOP_LAUNCH

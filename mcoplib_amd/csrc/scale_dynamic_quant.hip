@@ -29,7 +29,7 @@ k_scale_dynamic_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
-    xv[v] = ld<uint16_t, VEC>(x + lbase + lj);
+    xv[v] = ld_nt<uint16_t, VEC>(x + lbase + lj);
     sv[v] = ld<float, VEC>(sm + lj);
   }
 
@@ -57,7 +57,7 @@ k_scale_dynamic_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
       Pack<uint8_t, VEC> q;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(a[v][e] * inv);
-      st<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
+      st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
     }
   }
 }
@@ -78,7 +78,8 @@ static void launch_nv(const Geometry& g, int8_t* out, float* scales, const void*
       case 1: MCOP_LAUNCH(1); break;
       case 2: MCOP_LAUNCH(2); break;
       case 4: MCOP_LAUNCH(4); break;
-      default: MCOP_LAUNCH(8); break;
+      case 8: MCOP_LAUNCH(8); break;
+      default: MCOP_LAUNCH(16); break;
     }
   }
 #undef MCOP_LAUNCH

@@ -119,7 +119,9 @@ static inline void acc_add(acc64* A, double x) {
   if (fabs(A->s) >= fabs(x)) A->c += (A->s - t) + x; else A->c += (x - t) + A->s;
   A->s = t;
 }
-static inline double acc_val(const acc64* A) { return A->s + A->c; }
+/* An infinite or NaN term makes the compensation NaN (inf - inf); the plain sum is then the
+   binary64 sum of the terms, as for any other order. */
+static inline double acc_val(const acc64* A) { return isfinite(A->s) ? A->s + A->c : A->s; }
 
 /* rho = 1 / sqrt(ss/H + eps): the reference's `rsqrtf(ss / hidden_size + epsilon)`
    (e.g. op/vllm/quantization/fused_kernels/layernorm_utils.cuh:273-274) with each binary32
