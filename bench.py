@@ -44,6 +44,10 @@ def parse():
                     help="rotated input sets (default: enough for > 1 GiB, at least 3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--warmup-seconds", type=float, default=2.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run three 1 GiB device-to-device copies (a kernel of known "
+                         "traffic, used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     return ap.parse_args()
 
 
@@ -189,13 +193,20 @@ def main() -> int:
     dev = "cuda:0"
     torch.cuda.set_device(0)
     wl = WORKLOADS[args.workload]
+    if args.copy_calibration:
+        src = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     n_sets = args.sets or max(3, -(-(1 << 30) // wl.bytes))
     sets = [wl.make(torch, dev, 100 + i) for i in range(n_sets)]
     launches = [wl.launcher(torch, d) for d in sets]
     # warm-up: the requested steps, continued until the GPU has been busy for ~2 s so that
     # clocks and power state have settled before the timed region
     i, t_w = 0, time.perf_counter()
-    while i < args.warmup or time.perf_counter() - t_w < 2.0:
+    while i < args.warmup or time.perf_counter() - t_w < args.warmup_seconds:
         launches[i % len(launches)]()
         i += 1
         if i % 64 == 0:
@@ -215,8 +226,9 @@ def main() -> int:
     wall = time.perf_counter() - t0
     total_ms = t_start.elapsed_time(t_stop)
     ms_per_step = total_ms / K
-    # (2) the kernel's average launch duration: the same K steps with an event pair around
-    # every launch (on torch's current stream, the stream the kernel is launched on)
+    # (2) a second pass with an event pair around every launch: the spread of single-launch
+    # times (each pair also times the event packets themselves, so its mean sits above the
+    # back-to-back figure, which is what rocprofv3's kernel trace reports)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(K)]
     for i in range(K):
@@ -224,8 +236,10 @@ def main() -> int:
         launches[i % len(launches)]()
         ev[i][1].record()
     torch.cuda.synchronize()
-    per_launch_ms = [a.elapsed_time(b) for a, b in ev]
-    kernel_ms = statistics.mean(per_launch_ms)
+    per_launch_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    # one step is exactly one launch of the kernel and nothing else runs on the stream, so the
+    # kernel's average launch duration over the timed region is total / K
+    kernel_ms = ms_per_step
 
     value = wl.bytes / (ms_per_step * 1e-3) / 1e9
     achieved = wl.bytes / (kernel_ms * 1e-3) / 1e9
@@ -254,6 +268,8 @@ def main() -> int:
                      "traffic": traffic,
                      "kernel": KERNEL_NAME[wl.kind],
                      "kernel_avg_us": round(kernel_ms * 1e3, 3),
+                     "single_launch_us_p10_p50_p90": [
+                         round(per_launch_ms[int(q * (K - 1))] * 1e3, 3) for q in (0.1, 0.5, 0.9)],
                      "algorithmic_bytes_per_launch": wl.bytes},
         "host_wall_s": round(wall, 4),
     }

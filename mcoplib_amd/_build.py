@@ -43,33 +43,36 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *COMPILE_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, build_dir: Path = BUILD, defines: tuple = ()) -> Path:
+    obj = build_dir / (src.stem + ".o")
+    cmd = [HIPCC, *COMPILE_FLAGS, *[f"-D{d}" for d in defines], "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> Path:
-    """Compile every kernel source and link libmcop_norm.so. Always rebuilds."""
+def build(jobs: int | None = None, verbose: bool = True, out: Path = LIB,
+          defines: tuple = ()) -> Path:
+    """Compile every kernel source and link libmcop_norm.so (or `out`, with extra -D
+    `defines`, for tuning builds). Always rebuilds."""
     if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    BUILD.mkdir(exist_ok=True)
+    build_dir = BUILD if out == LIB else BUILD / out.stem
+    build_dir.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda s: _compile(s, build_dir, defines), srcs))
+    tmp = out.with_suffix(".so.tmp")
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources", file=sys.stderr)
-    return LIB
+        print(f"built {out} from {len(srcs)} sources", file=sys.stderr)
+    return out
 
 
 def main() -> None:

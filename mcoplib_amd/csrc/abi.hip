@@ -5,6 +5,10 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
 
 #include "../../include/mcop_norm.h"
 #include "rowkern.h"
@@ -45,11 +49,56 @@ bool aligned(int bytes, const void* p0, const void* p1, const void* p2, const vo
   return true;
 }
 
-// Vector path: vectors per lane nv in {1,2,4,8,16}; the default is two 16-byte vectors per tensor
-// per lane (enough loads in flight per wave while keeping VGPR use near 64), one for rows of at
-// most 64 vectors.  Scalar path (hidden not a multiple of the vector width, or misaligned
-// pointers): nv in {4,16}.  Rows narrower than 256 lanes are packed several per workgroup.
-bool choose_geometry(int64_t rows, int64_t hidden, int vec, Geometry* g) {
+namespace {
+// MCOP_DEBUG_TRACE=1|ON prints every launch decision to stdout (the reference's env switch of
+// the same name prints every operator's arguments).
+bool trace_enabled() {
+  static const bool on = [] {
+    const char* v = getenv("MCOP_DEBUG_TRACE");
+    return v != nullptr && (strcmp(v, "1") == 0 || strcmp(v, "ON") == 0 || strcmp(v, "on") == 0);
+  }();
+  return on;
+}
+
+// Resident workgroups per CU of one kernel at one workgroup size (hipOccupancy..., cached; the
+// answer depends only on the kernel's registers / LDS and the architecture).
+// Kernels that spill registers to scratch (private segment > 0) count as 0: per-lane scratch
+// traffic would compete with the streamed rows.
+int blocks_per_cu(const void* kernel, int block) {
+  static std::mutex mu;
+  static std::unordered_map<uint64_t, int> cache;
+  const uint64_t key = (uint64_t)reinterpret_cast<uintptr_t>(kernel) * 4099u + (uint64_t)block;
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
+  int n = 0;
+  hipFuncAttributes attr;
+  if (hipFuncGetAttributes(&attr, kernel) != hipSuccess || attr.localSizeBytes > 0 ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, block, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    n = 0;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  cache[key] = n;
+  return n;
+}
+}  // namespace
+
+// Launch shape of a row kernel.  A lane holds nv vectors of each streamed tensor, a row spans
+// tpr = nvec / nv lanes rounded up to whole waves, and rows narrower than 256 lanes are packed
+// several per workgroup.  Rules, from measurements on MI355X (bf16 rows of 4096-16384):
+//   - at most 256 rows (decode): row latency matters; the smallest nv >= 2 whose row fits
+//     (1 for rows of at most 64 vectors);
+//   - otherwise nv = 2 when its workgroups have at most 512 lanes and fill the CU (32 resident
+//     waves, from the kernel's occupancy); else nv = 4 (e.g. 7-wave workgroups leave a third of
+//     the wave slots empty, 16-wave ones reduce across too many waves: 4 vectors per lane was
+//     8-15% faster there); 8 or 16 only for rows that do not fit otherwise.  Kernels that spill
+//     registers are skipped while another shape fits.
+// Scalar path (hidden not a multiple of the vector width, or misaligned pointers): nv in {4,16}.
+bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, KernelOfNv kernels,
+                     Geometry* g) {
   const int64_t nvec = hidden / vec;
   int nv = 0;
   int64_t tpr = 0;
@@ -65,25 +114,43 @@ bool choose_geometry(int64_t rows, int64_t hidden, int vec, Geometry* g) {
     }
   }
   if (nv == 0) {
-    if (vec > 1) {
-      for (int cand : {1, 2, 4, 8, 16}) {
-        if (cand == 1 && nvec > 64) continue;
-        const int64_t t = round64(ceil_div(nvec, cand));
-        if (t <= max_tpr(vec, cand)) {
-          nv = cand;
-          tpr = t;
-          break;
-        }
+    static const int kVecNv[] = {1, 2, 4, 8, 16};
+    static const int kScalarNv[] = {4, 16};
+    const int* cands = vec > 1 ? kVecNv : kScalarNv;
+    const int ncand = vec > 1 ? 5 : 2;
+    const bool latency = rows <= 256;
+    int fallback_nv = 0;
+    int64_t fallback_tpr = 0;
+    for (int c = 0; c < ncand && nv == 0; ++c) {
+      const int cand = cands[c];
+      const int64_t t = round64(ceil_div(nvec, cand));
+      if (t > max_tpr(vec, cand)) continue;
+      if (vec > 1 && cand == 1 && nvec > 64) continue;
+      if (fallback_nv == 0) {
+        fallback_nv = cand;
+        fallback_tpr = t;
       }
-    } else {
-      for (int cand : {4, 16}) {
-        const int64_t t = round64(ceil_div(nvec, cand));
-        if (t <= max_tpr(vec, cand)) {
-          nv = cand;
-          tpr = t;
-          break;
-        }
+      if (latency || (vec > 1 && cand == 1)) {
+        nv = cand;
+        tpr = t;
+        break;
       }
+      const int rpb = t < 256 ? (int)(256 / t) : 1;
+      const int block = (int)t * rpb;
+      const int nb = blocks_per_cu(kernels(cand), block);
+      const int waves = nb * block / 64;
+      if (trace_enabled()) {
+        fprintf(stdout, "[mcop]   %s candidate nv=%d tpr=%lld wg=%d resident_wgs/CU=%d\n", op,
+                cand, (long long)t, block, nb);
+      }
+      if (nb == 0) continue;  // spills (or cannot launch at this size)
+      if (vec > 1 && cand == 2 && (t > 512 || waves < 32)) continue;
+      nv = cand;
+      tpr = t;
+    }
+    if (nv == 0) {
+      nv = fallback_nv;
+      tpr = fallback_tpr;
     }
   }
   if (nv == 0) return false;
@@ -92,6 +159,12 @@ bool choose_geometry(int64_t rows, int64_t hidden, int vec, Geometry* g) {
   g->tpr = (int)tpr;
   g->rpb = tpr < 256 ? (int)(256 / tpr) : 1;
   g->blocks = ceil_div(rows, g->rpb);
+  if (trace_enabled()) {
+    fprintf(stdout, "[mcop] %s rows=%lld hidden=%lld vec=%d nv=%d tpr=%d rows/wg=%d wgs=%lld\n",
+            op, (long long)rows, (long long)hidden, g->vec, g->nv, g->tpr, g->rpb,
+            (long long)g->blocks);
+    fflush(stdout);
+  }
   return true;
 }
 

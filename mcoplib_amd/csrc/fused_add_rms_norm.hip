@@ -42,14 +42,16 @@ k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
     const int j = vec_index(v, tpr, p.lt);
     const bool in = j < nvec;
     Pack<S, VEC> o;
+    double vs = 0.0;  // lanes past the row end (a copy of vector 0) do not count
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       o.v[e] = E::from_f(E::to_f(xv[v].v[e]) + E::to_f(rv[v].v[e]));
-      const float t = in ? E::to_f(o.v[e]) : 0.0f;
+      const float t = E::to_f(o.v[e]);
       z[v][e] = t;
       const double d = (double)t;
-      ss = __builtin_fma(d, d, ss);
+      vs = __builtin_fma(d, d, vs);
     }
+    ss += in ? vs : 0.0;
     if (p.live && in) st_nt<S, VEC>(res + rbase + (int64_t)j * VEC, o);
   }
 
@@ -95,13 +97,30 @@ static void launch_nv(const Geometry& g, void* x, int64_t xs, void* res, const v
 #undef MCOP_LAUNCH
 }
 
+template <class E, int VEC>
+static const void* kernel_of(int nv) {
+  if constexpr (VEC == 1) {
+    return nv == 4 ? reinterpret_cast<const void*>(&k_fused_add_rms_norm<E, 1, 4>)
+                   : reinterpret_cast<const void*>(&k_fused_add_rms_norm<E, 1, 16>);
+  } else {
+    switch (nv) {
+      case 1: return reinterpret_cast<const void*>(&k_fused_add_rms_norm<E, VEC, 1>);
+      case 2: return reinterpret_cast<const void*>(&k_fused_add_rms_norm<E, VEC, 2>);
+      case 4: return reinterpret_cast<const void*>(&k_fused_add_rms_norm<E, VEC, 4>);
+      case 8: return reinterpret_cast<const void*>(&k_fused_add_rms_norm<E, VEC, 8>);
+      default: return reinterpret_cast<const void*>(&k_fused_add_rms_norm<E, VEC, 16>);
+    }
+  }
+}
+
 template <class E>
 static int dispatch(void* x, int64_t xs, void* res, const void* w, int64_t rows, int64_t hidden,
                     float eps, hipStream_t st) {
   constexpr int V = E::VEC;
   const bool vec_ok = hidden % V == 0 && xs % V == 0 && aligned(16, x, res, w);
   Geometry g;
-  if (!choose_geometry(rows, hidden, vec_ok ? V : 1, &g)) {
+  if (!choose_geometry("fused_add_rms_norm", rows, hidden, vec_ok ? V : 1, vec_ok ? &kernel_of<E, V> : &kernel_of<E, 1>,
+                       &g)) {
     return set_error(MCOP_E_UNSUPPORTED,
                      "fused_add_rms_norm: hidden_size %lld is larger than the register-resident "
                      "kernels support",

@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
+#include <type_traits>
 
 #include "../../include/mcop_norm.h"
 #include "rowkern.h"
@@ -55,15 +56,17 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
     const bool in = j < nvec;
+    // Lanes past the row end hold a copy of vector 0: it must not count in the sum.
+    double vs = 0.0;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       float t = E::to_f(xv[v].v[e]);
       if constexpr (RES) t += E::to_f(rv[v].v[e]);
-      t = in ? t : 0.0f;
       a[v][e] = t;
       const double d = (double)t;
-      ss = __builtin_fma(d, d, ss);
+      vs = __builtin_fma(d, d, vs);
     }
+    ss += in ? vs : 0.0;
     if constexpr (RES) {
       if (p.live && in) {
         Pack<S, VEC> o;
@@ -77,15 +80,19 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   ss = row_reduce(ss, red_sum, tpr, SumOp());
   const float rho = mcop_inv_rms(ss, hidden, eps);
 
+  // The absmax must skip the copies of vector 0 held past the row end: with an in-place
+  // residual that copy may read vector 0's residual after its owner stored the sum there.
+  // Rows that fill every lane (the common case) skip the test.
+  const bool full = (int64_t)NV * tpr == nvec;
   float amax = 0.0f;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
+    const bool in = full || vec_index(v, tpr, p.lt) < nvec;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      // Lanes past the row end hold a == 0, hence y == +-0: no effect on the max.
       const float y = rnd<E>(rnd<E>(a[v][e] * rho) * E::to_f(wv[v].v[e]));
       a[v][e] = y;
-      amax = __builtin_fmaxf(amax, __builtin_fabsf(y));
+      amax = __builtin_fmaxf(amax, in ? __builtin_fabsf(y) : 0.0f);
     }
   }
   amax = row_reduce(amax, red_max, tpr, MaxOp());
@@ -109,9 +116,14 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 #pragma unroll
         for (int e = 0; e < VEC; ++e) c[e] = clamp_fp8(c[e]);
         q = cvt_fp8<VEC>(c);
-      } else {
+      } else if (std::is_same_v<E, F32> || scale_ub != nullptr) {
+        // fp32 inputs can carry NaN payloads in the low byte, and a scale bound lets |y * inv|
+        // exceed 127: round, convert and saturate
 #pragma unroll
         for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(a[v][e] * inv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) q.v[e] = q_i8_in_range(a[v][e], inv);
       }
       st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
     }
@@ -145,14 +157,32 @@ static void launch_nv(const Geometry& g, void* out, float* scales, const void* x
 #undef MCOP_LAUNCH
 }
 
+template <class E, int VEC, bool FP8, bool RES>
+static const void* kernel_of(int nv) {
+  if constexpr (VEC == 1) {
+    return nv == 4 ? reinterpret_cast<const void*>(&k_rms_norm_quant<E, 1, 4, FP8, RES>)
+                   : reinterpret_cast<const void*>(&k_rms_norm_quant<E, 1, 16, FP8, RES>);
+  } else {
+    switch (nv) {
+      case 1: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 1, FP8, RES>);
+      case 2: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 2, FP8, RES>);
+      case 4: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 4, FP8, RES>);
+      case 8: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 8, FP8, RES>);
+      default: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 16, FP8, RES>);
+    }
+  }
+}
+
 template <class E, bool FP8>
 static int dispatch(void* out, float* scales, const void* x, const void* w,
                     const float* scale_ub, void* res, int64_t rows, int64_t hidden, float eps,
                     hipStream_t st) {
   constexpr int V = E::VEC;
   const bool vec_ok = hidden % V == 0 && aligned(16, x, w, res) && aligned(V, out);
+  const KernelOfNv kernels = vec_ok ? (res ? &kernel_of<E, V, FP8, true> : &kernel_of<E, V, FP8, false>)
+                                    : (res ? &kernel_of<E, 1, FP8, true> : &kernel_of<E, 1, FP8, false>);
   Geometry g;
-  if (!choose_geometry(rows, hidden, vec_ok ? V : 1, &g)) {
+  if (!choose_geometry("rms_norm_dynamic_per_token_quant", rows, hidden, vec_ok ? V : 1, kernels, &g)) {
     return set_error(MCOP_E_UNSUPPORTED,
                      "rms_norm_dynamic_per_token_quant: hidden_size %lld is larger than the "
                      "register-resident kernels support",

@@ -1,224 +1,8 @@
-// rms_norm_smooth_quant.hip -- SmoothQuant (residual add +) RMSNorm + dynamic per-token
-// quantization (mcoplib.op.rms_norm_dynamic_per_token_quant, "fused_rms_norm_dq").
-//
-// Semantics (per row, b() = round to the input dtype), following op/fused_rms_norm_dq.cu of
-// the reference:
-//   a = x (+ r, read only);  after_res <- b(a)                       compute_rms :69-99
-//   rho = 1/sqrt(sum(a^2)/H + eps) on the unrounded a                 :94 (fp64 sum here)
-//   u = (b(a) / rho) * w     [literal form; (b(a) * rho) * w with MCOP_SQ_STANDARD_NORM]
-//   after_norm <- b(u);  v = u * smooth                              norm_and_quant :163-186
-//   A = max|v|;  int8: s = A/127, q = sat[-127,127](rne(v * (1/s)))  :125-161, :296-297
-//   fp8 (no reference; same inverted-scale form): s = A/448, q = e4m3fn(clamp(v * (1/s), +-448))
-//   A == 0: s = 0 and q = 0.
-// One pass: the row stays in VGPRs between the two reductions, so HBM sees x (and residual)
-// read once and after_res, after_norm, the codes and the scale written once.  The division by
-// rho is the correctly rounded quotient, computed with the per-row reciprocal and one
-// Markstein correction (mcop_fdiv_const).
-#include <hip/hip_runtime.h>
-
-#include "../../include/mcop_norm.h"
-#include "rowkern.h"
-
-namespace mcop {
-
-// Weight / smooth-scale vectors may be stored in the input dtype or in fp32.
-template <class EW, int VEC>
-struct WVec {
-  Pack<typename EW::S, VEC> p;
-  __device__ __forceinline__ float at(int e) const { return EW::to_f(p.v[e]); }
-};
-
-template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES>
-__global__ void __launch_bounds__(max_tpr(VEC, NV))
-k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
-                        const typename E::S* __restrict__ x, const typename EW::S* __restrict__ w,
-                        const typename ES::S* __restrict__ sm, typename E::S* __restrict__ ares,
-                        typename E::S* __restrict__ anorm, const typename E::S* __restrict__ res,
-                        int64_t rows, int hidden, int tpr, float eps, uint32_t flags) {
-  using S = typename E::S;
-  __shared__ double red_sum[16];
-  __shared__ float red_max[16];
-  const RowPos p = row_pos(rows, tpr);
-  const int nvec = hidden / VEC;
-  const int64_t base = p.row * (int64_t)hidden;
-  const int64_t lbase = p.lrow * (int64_t)hidden;
-
-  Pack<S, VEC> xv[NV], rv[NV];
-  WVec<EW, VEC> wv[NV];
-  WVec<ES, VEC> sv[NV];
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
-    xv[v] = ld_nt<S, VEC>(x + lbase + lj);
-    if constexpr (RES) rv[v] = ld_nt<S, VEC>(res + lbase + lj);
-    wv[v].p = ld<typename EW::S, VEC>(w + lj);
-    sv[v].p = ld<typename ES::S, VEC>(sm + lj);
-  }
-
-  float a[NV][VEC];
-  double ss = 0.0;
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int j = vec_index(v, tpr, p.lt);
-    const bool in = j < nvec;
-    Pack<S, VEC> o;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      float t = E::to_f(xv[v].v[e]);
-      if constexpr (RES) t += E::to_f(rv[v].v[e]);
-      t = in ? t : 0.0f;
-      o.v[e] = E::from_f(t);
-      const double d = (double)t;
-      ss = __builtin_fma(d, d, ss);
-      a[v][e] = E::to_f(o.v[e]);  // b(a): what the later passes of the reference re-read
-    }
-    if (ares != nullptr && p.live && in) st_nt<S, VEC>(ares + base + (int64_t)j * VEC, o);
-  }
-
-  ss = row_reduce(ss, red_sum, tpr, SumOp());
-  const float rho = mcop_inv_rms(ss, hidden, eps);
-  const float inv_rho = mcop_div_rn(1.0f, rho);
-  const bool rho_ok = mcop_divisor_ok(rho);
-  const bool standard = (flags & MCOP_SQ_STANDARD_NORM) != 0;
-
-  float amax = 0.0f;
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int j = vec_index(v, tpr, p.lt);
-    Pack<S, VEC> o;
-    float n[VEC];
-    if (standard) {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) n[e] = a[v][e] * rho;
-    } else {
-      div_by_const<VEC>(n, a[v], rho, inv_rho, rho_ok);
-    }
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const float u = n[e] * wv[v].at(e);
-      o.v[e] = E::from_f(u);
-      const float vv = u * sv[v].at(e);
-      a[v][e] = vv;
-      amax = __builtin_fmaxf(amax, __builtin_fabsf(vv));
-    }
-    if (anorm != nullptr && p.live && j < nvec) st_nt<S, VEC>(anorm + base + (int64_t)j * VEC, o);
-  }
-  amax = row_reduce(amax, red_max, tpr, MaxOp());
-
-  const float s = mcop_div_rn(amax, FP8 ? 448.0f : 127.0f);
-  if (p.live && p.lt == 0) scales[p.row] = s;
-  const float inv = amax > 0.0f ? mcop_div_rn(1.0f, s) : 0.0f;
-
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int j = vec_index(v, tpr, p.lt);
-    if (p.live && j < nvec) {
-      Pack<uint8_t, VEC> q;
-      if constexpr (FP8) {
-        float c[VEC];
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) c[e] = clamp_fp8(a[v][e] * inv);
-        q = cvt_fp8<VEC>(c);
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-127>(a[v][e] * inv);
-      }
-      st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
-    }
-  }
-}
-
-struct Args {
-  void* out;
-  float* scales;
-  const void* x;
-  const void* w;
-  const void* sm;
-  void* ares;
-  void* anorm;
-  const void* res;
-  int64_t rows;
-  int hidden;
-  float eps;
-  uint32_t flags;
-};
-
-template <class E, class EW, class ES, int VEC, bool FP8, bool RES>
-static void launch_nv(const Geometry& g, const Args& a, hipStream_t st) {
-  using S = typename E::S;
-  const dim3 grid((unsigned)g.blocks), block((unsigned)(g.tpr * g.rpb));
-  auto* o = static_cast<uint8_t*>(a.out);
-  auto* xp = static_cast<const S*>(a.x);
-  auto* wp = static_cast<const typename EW::S*>(a.w);
-  auto* sp = static_cast<const typename ES::S*>(a.sm);
-  auto* arp = static_cast<S*>(a.ares);
-  auto* anp = static_cast<S*>(a.anorm);
-  auto* rp = static_cast<const S*>(a.res);
-#define MCOP_LAUNCH(NVV)                                                                     \
-  hipLaunchKernelGGL((k_rms_norm_smooth_quant<E, EW, ES, VEC, NVV, FP8, RES>), grid, block, 0, \
-                     st, o, a.scales, xp, wp, sp, arp, anp, rp, a.rows, a.hidden, g.tpr,       \
-                     a.eps, a.flags)
-  if constexpr (VEC == 1) {
-    if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
-  } else {
-    switch (g.nv) {
-      case 1: MCOP_LAUNCH(1); break;
-      case 2: MCOP_LAUNCH(2); break;
-      case 4: MCOP_LAUNCH(4); break;
-      case 8: MCOP_LAUNCH(8); break;
-      default: MCOP_LAUNCH(16); break;
-    }
-  }
-#undef MCOP_LAUNCH
-}
-
-template <class E, class EW, class ES, bool FP8>
-static int dispatch(const Args& a, hipStream_t st) {
-  constexpr int V = E::VEC;
-  constexpr int WB = (int)sizeof(typename EW::S) * V, SB = (int)sizeof(typename ES::S) * V;
-  const bool vec_ok = a.hidden % V == 0 && aligned(16, a.x, a.ares, a.anorm, a.res) &&
-                      aligned(WB, a.w) && aligned(SB, a.sm) && aligned(V, a.out);
-  Geometry g;
-  if (!choose_geometry(a.rows, a.hidden, vec_ok ? V : 1, &g)) {
-    return set_error(MCOP_E_UNSUPPORTED,
-                     "rms_norm_dynamic_per_token_quant (smooth): hidden_size %d is larger than "
-                     "the register-resident kernels support",
-                     a.hidden);
-  }
-  const bool has_res = a.res != nullptr;
-  if (g.vec == 1) {
-    if (has_res) launch_nv<E, EW, ES, 1, FP8, true>(g, a, st);
-    else launch_nv<E, EW, ES, 1, FP8, false>(g, a, st);
-  } else {
-    if (has_res) launch_nv<E, EW, ES, V, FP8, true>(g, a, st);
-    else launch_nv<E, EW, ES, V, FP8, false>(g, a, st);
-  }
-  return check_launch("rms_norm_dynamic_per_token_quant (smooth)");
-}
-
-template <class E, class EW, class ES>
-static int dispatch_out(const Args& a, bool fp8, hipStream_t st) {
-  return fp8 ? dispatch<E, EW, ES, true>(a, st) : dispatch<E, EW, ES, false>(a, st);
-}
-
-// Weight and smooth dtypes: each is the input dtype or fp32.
-template <class E>
-static int dispatch_ws(const Args& a, mcop_dtype wdt, mcop_dtype sdt, mcop_dtype in_dt, bool fp8,
-                       hipStream_t st) {
-  const bool w32 = wdt == MCOP_F32, s32 = sdt == MCOP_F32;
-  if ((!w32 && wdt != in_dt) || (!s32 && sdt != in_dt)) {
-    return set_error(MCOP_E_INVALID,
-                     "rms_norm_dynamic_per_token_quant (smooth): weight dtype %d / smooth dtype "
-                     "%d must each be the input dtype %d or fp32",
-                     (int)wdt, (int)sdt, (int)in_dt);
-  }
-  if (w32 && s32) return dispatch_out<E, F32, F32>(a, fp8, st);
-  if (w32) return dispatch_out<E, F32, E>(a, fp8, st);
-  if (s32) return dispatch_out<E, E, F32>(a, fp8, st);
-  return dispatch_out<E, E, E>(a, fp8, st);
-}
-
-}  // namespace mcop
+// rms_norm_smooth_quant.hip -- entry point of the SmoothQuant (residual add +) RMSNorm + dynamic
+// per-token quantization (mcoplib.op.rms_norm_dynamic_per_token_quant, "fused_rms_norm_dq");
+// the kernel and its semantics are in smooth_quant_kernel.h.  This unit instantiates the fp32
+// input kernels; the bf16 and fp16 ones are in rms_norm_smooth_quant_{bf16,f16}.hip.
+#include "smooth_quant_kernel.h"
 
 extern "C" int mcop_rms_norm_smooth_quant(void* out, mcop_dtype out_dtype, float* scales,
                                           const void* input, const void* weight,
@@ -250,8 +34,8 @@ extern "C" int mcop_rms_norm_smooth_quant(void* out, mcop_dtype out_dtype, float
   const bool fp8 = out_dtype == MCOP_FP8_E4M3FN;
   auto st = static_cast<hipStream_t>(stream);
   switch (in_dtype) {
-    case MCOP_BF16: return dispatch_ws<BF16>(a, weight_dtype, smooth_dtype, in_dtype, fp8, st);
-    case MCOP_F16: return dispatch_ws<F16>(a, weight_dtype, smooth_dtype, in_dtype, fp8, st);
+    case MCOP_BF16: return dispatch_smooth_bf16(a, weight_dtype, smooth_dtype, fp8, st);
+    case MCOP_F16: return dispatch_smooth_f16(a, weight_dtype, smooth_dtype, fp8, st);
     case MCOP_F32:
       if (weight_dtype != MCOP_F32 || smooth_dtype != MCOP_F32) {
         return set_error(MCOP_E_INVALID,

@@ -85,10 +85,21 @@ template <> struct RawOf<16> { using T = u32x4; };
 // Streaming (non-temporal) load / store of a Pack: data touched once per call (the rows of x,
 // residual and the outputs) is marked so it does not displace reused data (the weight vector)
 // in the caches.  Measured on MI355X: +10% HBM throughput for the row kernels.
+// Build-time switches of the streaming hints (both on by default; the tuning sweeps build
+// variants with them off).
+#ifndef MCOP_NT_LOADS
+#define MCOP_NT_LOADS 1
+#endif
+#ifndef MCOP_NT_STORES
+#define MCOP_NT_STORES 1
+#endif
+
 template <class T, int N>
 __device__ __forceinline__ Pack<T, N> ld_nt(const T* p) {
   constexpr int B = (int)sizeof(T) * N;
-  if constexpr (B == 32) {
+  if constexpr (!MCOP_NT_LOADS) {
+    return ld<T, N>(p);
+  } else if constexpr (B == 32) {
     const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
     const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p) + 1);
     struct Two { u32x4 a, b; };
@@ -101,8 +112,12 @@ __device__ __forceinline__ Pack<T, N> ld_nt(const T* p) {
 template <class T, int N>
 __device__ __forceinline__ void st_nt(T* p, const Pack<T, N>& v) {
   constexpr int B = (int)sizeof(T) * N;
-  using R = typename RawOf<B>::T;
-  __builtin_nontemporal_store(__builtin_bit_cast(R, v), reinterpret_cast<R*>(p));
+  if constexpr (!MCOP_NT_STORES) {
+    st<T, N>(p, v);
+  } else {
+    using R = typename RawOf<B>::T;
+    __builtin_nontemporal_store(__builtin_bit_cast(R, v), reinterpret_cast<R*>(p));
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -122,6 +137,17 @@ template <int LO>
 __device__ __forceinline__ uint8_t q_i8(float v) {
   const int i = cvt_rne_i32(v);
   return (uint8_t)(i < LO ? LO : (i > 127 ? 127 : i));
+}
+
+// int8 code of t = y * inv when |t| <= 127.5 is guaranteed (absmax scaling, no scale bound):
+// RN(t + 1.5 * 2^23) holds rne(t) in the low mantissa bits (exact for |t| < 2^22), so its low
+// byte is the two's-complement code.  Two operations instead of round / convert / clamp; the
+// empty asm keeps the product rounded on its own (no fused multiply-add).  A NaN t keeps the
+// payload of y, whose low 13 bits are zero for bf16 / fp16 values, so NaN codes 0 as in q_i8.
+__device__ __forceinline__ uint8_t q_i8_in_range(float y, float inv) {
+  float t = y * inv;
+  asm("" : "+v"(t));
+  return (uint8_t)__builtin_bit_cast(uint32_t, t + 12582912.0f);
 }
 
 // OCP fp8 e4m3fn codes of N values already clamped to [-448, 448] (v_cvt_pk_fp8_f32: RNE).
@@ -222,11 +248,18 @@ struct RowPos {
   int lt;
   bool live;
 };
+// Workgroups hold several rows only when tpr is 64 or 128 (a power of two), so the row within
+// the workgroup is a shift (tpr is a kernel argument: the shift amount is scalar work).
 __device__ __forceinline__ RowPos row_pos(int64_t num_rows, int tpr) {
-  const int rpb = blockDim.x / tpr;
   RowPos p;
-  p.row = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
-  p.lt = threadIdx.x % tpr;
+  if ((int)blockDim.x == tpr) {
+    p.row = blockIdx.x;
+    p.lt = threadIdx.x;
+  } else {
+    const int sh = 31 - __builtin_clz((unsigned)tpr);
+    p.row = ((int64_t)blockIdx.x << (31 - __builtin_clz(blockDim.x >> sh))) + (threadIdx.x >> sh);
+    p.lt = threadIdx.x & (tpr - 1);
+  }
   p.live = p.row < num_rows;
   p.lrow = p.live ? p.row : num_rows - 1;
   return p;
@@ -256,9 +289,13 @@ struct Geometry {
   int64_t blocks;
 };
 
+// The kernel instantiation used for a given number of vectors per lane (for occupancy queries).
+using KernelOfNv = const void* (*)(int nv);
+
 // Picks the launch shape of a row kernel. `vec` is 1 or the 16-byte vector width; returns false
 // when the row does not fit (hidden too large for the register-resident kernels).
-bool choose_geometry(int64_t rows, int64_t hidden, int vec, Geometry* g);
+bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, KernelOfNv kernels,
+                     Geometry* g);
 
 // True when every non-null pointer is aligned to `bytes`.
 bool aligned(int bytes, const void* p0, const void* p1 = nullptr, const void* p2 = nullptr,

@@ -35,12 +35,12 @@ k_scale_dynamic_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 
   float a[NV][VEC];
   float amax = 0.0f;
+  // Lanes past the row end hold a copy of vector 0, which does not change the max.
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const bool in = vec_index(v, tpr, p.lt) < nvec;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const float t = in ? BF16::to_f(xv[v].v[e]) * sv[v].v[e] : 0.0f;
+      const float t = BF16::to_f(xv[v].v[e]) * sv[v].v[e];
       a[v][e] = t;
       amax = __builtin_fmaxf(amax, __builtin_fabsf(t));
     }
@@ -85,6 +85,22 @@ static void launch_nv(const Geometry& g, int8_t* out, float* scales, const void*
 #undef MCOP_LAUNCH
 }
 
+template <int VEC>
+static const void* kernel_of(int nv) {
+  if constexpr (VEC == 1) {
+    return nv == 4 ? reinterpret_cast<const void*>(&k_scale_dynamic_quant<1, 4>)
+                   : reinterpret_cast<const void*>(&k_scale_dynamic_quant<1, 16>);
+  } else {
+    switch (nv) {
+      case 1: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 1>);
+      case 2: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 2>);
+      case 4: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 4>);
+      case 8: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 8>);
+      default: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 16>);
+    }
+  }
+}
+
 }  // namespace mcop
 
 extern "C" int mcop_scale_dynamic_quant(int8_t* out, float* scales, const void* input,
@@ -103,7 +119,8 @@ extern "C" int mcop_scale_dynamic_quant(int8_t* out, float* scales, const void* 
   constexpr int V = BF16::VEC;
   const bool vec_ok = hidden_size % V == 0 && aligned(16, input, smooth) && aligned(V, out);
   Geometry g;
-  if (!choose_geometry(num_tokens, hidden_size, vec_ok ? V : 1, &g)) {
+  if (!choose_geometry("scale_dynamic_quant", num_tokens, hidden_size, vec_ok ? V : 1,
+                       vec_ok ? &kernel_of<V> : &kernel_of<1>, &g)) {
     return set_error(MCOP_E_UNSUPPORTED,
                      "scale_dynamic_quant: hidden_size %lld is larger than the register-resident "
                      "kernels support",
