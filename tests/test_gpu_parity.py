@@ -1,5 +1,5 @@
 """GPU parity: the HIP kernels (through the drop-in surfaces and the C ABI) against the CPU oracle
-on the same seeded inputs, at the BASELINE configurations and at the shapes the reference's own
+on the same seeded inputs, at the benchmark configurations (cfg1-cfg5) and at the shapes the reference's own
 test enumerates (unit_test/test_fused_rms_norm_dq.py:13-24)."""
 
 import pytest
@@ -70,7 +70,7 @@ def _outlier_x(T, H, seed):
 
 
 def test_config3_add_norm_int8_outliers():
-    """x, residual [8192, 8192] bf16, 1% outlier channels x20, eps 1e-5."""
+    """Config 3 (the headline workload): x, residual [8192, 8192] bf16, 1% outlier channels x20, eps 1e-5."""
     T = H = 8192
     say("config 3: 8192x8192 add + rmsnorm + int8, outliers")
     x = _outlier_x(T, H, 3)
@@ -88,7 +88,7 @@ def test_config3_add_norm_int8_outliers():
 
 
 def test_config2_fused_add_rms_norm():
-    """in-place fused_add_rms_norm, [4096, 4096] bf16, eps 1e-6."""
+    """Config 2: in-place fused_add_rms_norm, [4096, 4096] bf16, eps 1e-6."""
     T = H = 4096
     say("config 2: fused_add_rms_norm 4096x4096")
     x = randn((T, H), 20, torch.bfloat16)
@@ -180,7 +180,7 @@ def test_h4_shapes(T, H, dtype, wdt, sdt):
 
 
 def test_config4_smooth_quant_fp8():
-    """fused_rms_norm_dq to fp8-e4m3fn with SmoothQuant, [16384, 7168] bf16,
+    """Config 4: fused_rms_norm_dq to fp8-e4m3fn with SmoothQuant, [16384, 7168] bf16,
     bf16 weight, fp32 smooth ~U(0.5, 2)."""
     say("config 4: 16384x7168 smooth quant fp8")
     _h4_case(16384, 7168, torch.bfloat16, torch.bfloat16, torch.float32, torch.float8_e4m3fn,
@@ -194,7 +194,7 @@ def test_config5_decode(T):
 
 
 def test_config5_large_sampled_rows():
-    """BASELINE config 5 (bandwidth leg): [32768, 16384] bf16 add + norm + int8.  Inputs are
+    """Config 5 (bandwidth leg): [32768, 16384] bf16 add + norm + int8.  Inputs are
     generated on the device; the oracle checks a sample of rows (rows are independent)."""
     T, H = 32768, 16384
     say("config 5 large: 32768x16384")
