@@ -1,6 +1,7 @@
 """Build libmcop_norm.so (the gfx950 kernels and their C ABI) in-tree with hipcc.
 
-Usage: python -m mcoplib_amd._build [--jobs N]
+Usage: python mcoplib_amd/_build.py [--jobs N]
+(run as a script: importing the package would load the library this builds)
 
 Each csrc/*.hip translation unit is compiled for gfx950 only, in parallel, then linked into
 mcoplib_amd/libmcop_norm.so next to this file. Objects go to mcoplib_amd/_build/.

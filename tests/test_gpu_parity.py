@@ -230,28 +230,38 @@ def test_h5_parity_shapes():
         assert_codes(q, q_ref, "h5 codes")
 
 
-def test_launch_shape_does_not_change_bits():
+@pytest.mark.parametrize("T", [512, 517])
+def test_launch_shape_does_not_change_bits(T):
     """The row sum is accumulated in fp64 and rounded once: every split of a row over lanes
-    gives the same bits."""
-    T, H = 512, 4096
-    say("launch shape independence")
+    gives the same bits (all four row kernels)."""
+    H = 4096
+    say(f"launch shape independence T={T}")
     x = randn((T, H), 60, torch.bfloat16).to(DEV)
     r0 = randn((T, H), 61, torch.bfloat16).to(DEV)
     w = weight(H, 62, torch.bfloat16).to(DEV)
+    sm = (0.5 + 1.5 * torch.rand(H, generator=gen(63))).to(DEV)
+    shapes = [(0, 0), (1, 512), (2, 256), (4, 128), (8, 64), (2, 1024), (4, 512), (1, 1024)]
     outs = []
     try:
-        for nv, tpr in [(0, 0), (1, 512), (2, 256), (4, 128), (8, 64), (2, 1024), (4, 512),
-                        (1, 1024)]:
+        for nv, tpr in shapes:
             _lib.set_launch_override(nv, tpr)
             r = r0.clone()
             q, s = custom_ops.rms_norm_dynamic_per_token_quant(x, w, 1e-6, torch.int8,
                                                                residual=r)
-            outs.append((q.cpu(), s.cpu(), r.cpu()))
+            x1, r1 = x.clone(), r0.clone()
+            torch.ops._C.fused_add_rms_norm(x1, r1, w, 1e-6)
+            q4 = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=DEV)
+            s4 = torch.empty(T, device=DEV)
+            ar, an = torch.empty_like(x), torch.empty_like(x)
+            op.rms_norm_dynamic_per_token_quant(q4, x, w, sm, s4, 1e-6, ar, an, r0)
+            q5, s5 = op.scale_dynamic_quant(x, sm, torch.int8)
+            outs.append([t.cpu() for t in (q, s, r, x1, r1, q4.view(torch.uint8), s4, ar, an,
+                                           q5, s5)])
     finally:
         _lib.set_launch_override(0, 0)
-    for q, s, r in outs[1:]:
-        assert torch.equal(q, outs[0][0]) and torch.equal(s, outs[0][1])
-        assert torch.equal(r, outs[0][2])
+    for o in outs[1:]:
+        for a, b in zip(o, outs[0]):
+            assert torch.equal(a, b)
 
 
 def test_repeatable():
