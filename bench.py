@@ -39,7 +39,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="cfg3",
                     choices=["cfg2", "cfg3", "cfg4", "cfg5-large", "cfg5-decode1",
-                             "cfg5-decode4", "cfg5-decode16", "cfg5-decode64"])
+                             "cfg5-decode4", "cfg5-decode16", "cfg5-decode64", "ptq-int8",
+                             "ptq-int8-azp", "ptq-fp8"])
     ap.add_argument("--sets", type=int, default=0,
                     help="rotated input sets (default: enough for > 1 GiB, at least 3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -67,6 +68,10 @@ class Workload:
             return 8 * T * H + 2 * H
         if self.kind == "smooth_fp8":      # read x; write q, after_res, after_norm; w, smooth, s
             return 2 * T * H + T * H + 4 * T * H + 2 * H + 4 * H + 4 * T
+        if self.kind in ("ptq_int8", "ptq_fp8"):  # read x; write q, s
+            return 3 * T * H + 4 * T
+        if self.kind == "ptq_int8_azp":    # read x; write q, s, azp
+            return 3 * T * H + 8 * T
         raise ValueError(self.kind)
 
     def make(self, torch, dev, seed):
@@ -84,6 +89,12 @@ class Workload:
         if self.kind == "add_norm_int8":
             d["q"] = torch.empty(T, H, dtype=torch.int8, device=dev)
             d["s"] = torch.empty(T, 1, dtype=torch.float32, device=dev)
+        if self.kind.startswith("ptq_"):
+            qdt = torch.float8_e4m3fn if self.kind == "ptq_fp8" else torch.int8
+            d["q"] = torch.empty(T, H, dtype=qdt, device=dev)
+            d["s"] = torch.empty(T, 1, dtype=torch.float32, device=dev)
+            d["azp"] = (torch.empty(T, 1, dtype=torch.int32, device=dev)
+                        if self.kind == "ptq_int8_azp" else None)
         if self.kind == "smooth_fp8":
             d["sm"] = 0.5 + 1.5 * torch.rand(H, generator=g, device=dev)
             d["q"] = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=dev)
@@ -100,6 +111,11 @@ class Workload:
                 d["q"], d["x"], d["w"], d["s"], self.eps, None, d["r"])
         if self.kind == "fused_add":
             return lambda: torch.ops._C.fused_add_rms_norm(d["x"], d["r"], d["w"], self.eps)
+        if self.kind == "ptq_fp8":
+            return lambda: torch.ops._C.dynamic_per_token_scaled_fp8_quant(d["q"], d["x"], d["s"],
+                                                                         None)
+        if self.kind.startswith("ptq_int8"):
+            return lambda: torch.ops._C.dynamic_scaled_int8_quant(d["q"], d["x"], d["s"], d["azp"])
         return lambda: op.rms_norm_dynamic_per_token_quant(
             d["q"], d["x"], d["w"], d["sm"], d["s"], self.eps, d["ar"], d["an"], None)
 
@@ -111,9 +127,14 @@ WORKLOADS = {
     "cfg5-large": Workload("cfg5-large", 32768, 16384, 1e-6, "add_norm_int8"),
     **{f"cfg5-decode{t}": Workload(f"cfg5-decode{t}", t, 5120, 1e-6, "add_norm_int8")
        for t in (1, 4, 16, 64)},
+    # the standalone quantizers, at the headline shape (the step after an unfused norm)
+    "ptq-int8": Workload("ptq-int8", 8192, 8192, 0.0, "ptq_int8"),
+    "ptq-int8-azp": Workload("ptq-int8-azp", 8192, 8192, 0.0, "ptq_int8_azp"),
+    "ptq-fp8": Workload("ptq-fp8", 8192, 8192, 0.0, "ptq_fp8"),
 }
 KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "fused_add": "k_fused_add_rms_norm",
-               "smooth_fp8": "k_rms_norm_smooth_quant"}
+               "smooth_fp8": "k_rms_norm_smooth_quant", "ptq_int8": "k_per_token_quant",
+               "ptq_int8_azp": "k_per_token_quant", "ptq_fp8": "k_per_token_quant"}
 
 
 # ------------------------------------------------------------------------------ pieces
@@ -147,6 +168,10 @@ def cpu_baseline(wl: Workload, seconds: float) -> dict:
             oracle.rms_norm_dynamic_per_token_quant(x, w, wl.eps, torch.int8, residual=r)
         elif wl.kind == "fused_add":
             oracle.fused_add_rms_norm(x, r, w, wl.eps)
+        elif wl.kind == "ptq_fp8":
+            oracle.dynamic_per_token_scaled_fp8_quant(x)
+        elif wl.kind.startswith("ptq_int8"):
+            oracle.dynamic_scaled_int8_quant(x, use_azp=wl.kind == "ptq_int8_azp")
         else:
             oracle.rms_norm_smooth_quant(x, w, sm, wl.eps, torch.float8_e4m3fn)
 
@@ -280,8 +305,9 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": f"{wl.name}: {wl.kind} T={wl.T} H={wl.H} bf16 in, "
-                               f"eps={wl.eps}" + (", 1% outlier channels x20" if wl.name == "cfg3" else ""),
+        "config": {"workload": f"{wl.name}: {wl.kind} T={wl.T} H={wl.H} bf16 in"
+                               + ("" if wl.kind.startswith("ptq_") else f", eps={wl.eps}")
+                               + (", 1% outlier channels x20" if wl.name == "cfg3" else ""),
                    "tokens": wl.T, "hidden": wl.H, "io": "bf16 -> int8/fp8 + fp32 scales",
                    "rotated_input_sets": len(sets)},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),

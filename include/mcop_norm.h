@@ -109,6 +109,31 @@ int mcop_rms_norm_smooth_quant(void* out, mcop_dtype out_dtype, float* scales,
 int mcop_scale_dynamic_quant(int8_t* out, float* scales, const void* input, const float* smooth,
                              int64_t num_tokens, int64_t hidden_size, void* stream);
 
+/* Dynamic per-token int8 quantization without normalisation (vLLM `_C::dynamic_scaled_int8_quant`).
+ *   azp == NULL (symmetric): A = max|x|; scales[t] = A/127; q = sat[-127,127](rne(x * (127/A)))
+ *     (A == 0 gives q = 0);
+ *   azp != NULL (asymmetric): s = (max x - min x)/255; azp[t] = rne(-128 - min x / s);
+ *     q = sat[-128,127](rne(x * (1/s)) + azp[t]); a constant row (s == 0) gives azp = q = -128.
+ * input bf16/fp16/fp32 [T,H] contiguous; out int8 [T,H]; scales fp32 [T]; azp int32 [T].
+ * Replaces dynamic_scaled_int8_quant(),
+ * op/vllm/quantization/compressed_tensors/int8_quant_kernels.cu:459-527 (kernels :94-132,
+ * :370-422; schema op/vllm/torch_bindings.cpp:374-379). */
+int mcop_dynamic_scaled_int8_quant(int8_t* out, float* scales, int32_t* azp, const void* input,
+                                   int64_t num_tokens, int64_t hidden_size, mcop_dtype in_dtype,
+                                   void* stream);
+
+/* Dynamic per-token fp8-e4m3fn quantization without normalisation
+ * (vLLM `_C::dynamic_per_token_scaled_fp8_quant`):
+ *   A = max|x| (min with *scale_ub); s = max(A/448, 1/(448*512)); q = e4m3fn(clamp(x/s, +-448)).
+ * Rows of input and out may be strided (element strides >= hidden_size).
+ * Replaces dynamic_per_token_scaled_fp8_quant(), op/vllm/quantization/fp8/common.cu:375-411
+ * (kernel :142-180; schema op/vllm/torch_bindings.cpp:359-364). */
+int mcop_dynamic_per_token_scaled_fp8_quant(uint8_t* out, float* scales, const void* input,
+                                            const float* scale_ub, int64_t num_tokens,
+                                            int64_t hidden_size, int64_t input_row_stride,
+                                            int64_t output_row_stride, mcop_dtype in_dtype,
+                                            void* stream);
+
 /* The clamp-and-convert step shared by every fp8 epilogue, elementwise:
  *   out[i] = e4m3fn(clamp(in[i] * mul, -448, 448))   (RNE; clamp with fmin/fmax semantics)
  * No reference counterpart as an entry point (the step is float_to_fp8,

@@ -1,9 +1,10 @@
 """``torch.ops._C`` surface (the vLLM operator library that mcoplib builds as ``mcoplib._C``).
 
 Importing this module registers, in the ``_C`` torch.library namespace, the schemas of
-op/vllm/torch_bindings.cpp:161-164 (``fused_add_rms_norm``) and :216-221
-(``rms_norm_dynamic_per_token_quant``) with implementations for the CUDA (HIP) dispatch key that
-call libmcop_norm.so.  If another library (vLLM's own ``_C``) already defined a schema, only the
+op/vllm/torch_bindings.cpp:161-164 (``fused_add_rms_norm``), :216-221
+(``rms_norm_dynamic_per_token_quant``), :359-364 (``dynamic_per_token_scaled_fp8_quant``) and
+:374-379 (``dynamic_scaled_int8_quant``) with implementations for the CUDA (HIP) dispatch key
+that call libmcop_norm.so.  If another library (vLLM's own ``_C``) already defined a schema, only the
 CUDA implementation is registered over it.  There is no CPU implementation: calling these ops on
 CPU tensors raises, as the reference does.
 """
@@ -15,7 +16,8 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._checks import dispatch_check, numel_check, on_cuda, rows_of, torch_check
+from ._checks import (contiguous_check, dispatch_check, numel_check, on_cuda, rows_of,
+                      torch_check)
 from .op import _norm_quant
 
 SCHEMAS = {
@@ -24,6 +26,12 @@ SCHEMAS = {
     "rms_norm_dynamic_per_token_quant":
         "rms_norm_dynamic_per_token_quant(Tensor! result, Tensor input, Tensor weight, "
         "Tensor! scale, float epsilon, Tensor? scale_ub, Tensor!? residual) -> ()",
+    "dynamic_scaled_int8_quant":
+        "dynamic_scaled_int8_quant(Tensor! result, Tensor input, Tensor! scale, "
+        "Tensor!? azp) -> ()",
+    "dynamic_per_token_scaled_fp8_quant":
+        "dynamic_per_token_scaled_fp8_quant(Tensor! result, Tensor input, Tensor! scale, "
+        "Tensor? scale_ub) -> ()",
 }
 
 
@@ -82,9 +90,76 @@ def rms_norm_dynamic_per_token_quant(result: torch.Tensor, input: torch.Tensor,
                 scale_ub, residual)
 
 
+def dynamic_scaled_int8_quant(result: torch.Tensor, input: torch.Tensor, scale: torch.Tensor,
+                              azp: Optional[torch.Tensor] = None) -> None:
+    """Per-token int8 quantization, symmetric or with a per-token zero point (reference host
+    function op/vllm/quantization/compressed_tensors/int8_quant_kernels.cu:459-527)."""
+    name = "dynamic_scaled_int8_quant"
+    torch_check(input.is_contiguous(), "input.is_contiguous()")
+    torch_check(result.is_contiguous(), "out.is_contiguous()")
+    torch_check(scale.is_contiguous(), "scales.is_contiguous()")
+    torch_check(azp is None or azp.is_contiguous(), "!azp || azp->is_contiguous()")
+    dispatch_check(input.dtype, "dynamic_scaled_int8_quant_kernel")
+    if result.dtype != torch.int8:
+        raise RuntimeError(f"expected scalar type Char but found {result.dtype}")
+    if scale.dtype != torch.float32:
+        raise RuntimeError(f"expected scalar type Float but found {scale.dtype}")
+    if azp is not None and azp.dtype != torch.int32:
+        raise RuntimeError(f"expected scalar type Int but found {azp.dtype}")
+    on_cuda(name, result, input, scale, azp)
+    T, H = rows_of(input)
+    numel_check(name, "result", result, T * H)
+    numel_check(name, "scale", scale, T)
+    if azp is not None:
+        numel_check(name, "azp", azp, T)
+    with _lib.device_of(input):
+        _lib.check(_lib.lib.mcop_dynamic_scaled_int8_quant(
+            result.data_ptr(), scale.data_ptr(), None if azp is None else azp.data_ptr(),
+            input.data_ptr(), T, H, _lib.DTYPE_CODE[input.dtype], _lib.stream_of(input)))
+
+
+def dynamic_per_token_scaled_fp8_quant(result: torch.Tensor, input: torch.Tensor,
+                                       scale: torch.Tensor,
+                                       scale_ub: Optional[torch.Tensor] = None) -> None:
+    """Per-token fp8-e4m3fn quantization (reference host function
+    op/vllm/quantization/fp8/common.cu:375-411); rows of input and result may be strided."""
+    name = "dynamic_per_token_scaled_fp8_quant"
+    torch_check(input.stride(-1) == 1, "last dimension of input must be contiguous")
+    torch_check(result.stride(-1) == 1, "last dimension of output must be contiguous")
+    dispatch_check(input.dtype, "dynamic_per_token_scaled_fp8_quant_kernel_scalar_type")
+    dispatch_check(result.dtype, "dynamic_per_token_scaled_fp8_quant_kernel_fp8_type",
+                   allowed=(torch.float8_e4m3fn,))
+    if scale.dtype != torch.float32:
+        raise RuntimeError(f"expected scalar type Float but found {scale.dtype}")
+    on_cuda(name, result, input, scale, scale_ub)
+    T, H = rows_of(input)
+    if result.shape != input.shape:
+        raise RuntimeError(f"{name}: result shape {tuple(result.shape)} != input shape")
+    numel_check(name, "scale", scale, T)
+    contiguous_check(name, "scale", scale)
+    if scale_ub is not None and (scale_ub.dtype != torch.float32 or scale_ub.numel() < 1):
+        raise RuntimeError(f"{name}: scale_ub must be a float32 tensor with one element")
+
+    def row_stride(t: torch.Tensor) -> int:
+        if t.dim() < 2 or T <= 1:
+            return H
+        for d in range(t.dim() - 2):
+            if t.size(d) > 1 and t.stride(d) != t.stride(d + 1) * t.size(d + 1):
+                raise RuntimeError(f"{name}: rows must be uniformly strided")
+        return t.stride(-2)
+
+    with _lib.device_of(input):
+        _lib.check(_lib.lib.mcop_dynamic_per_token_scaled_fp8_quant(
+            result.data_ptr(), scale.data_ptr(), input.data_ptr(),
+            None if scale_ub is None else scale_ub.data_ptr(), T, H, row_stride(input),
+            row_stride(result), _lib.DTYPE_CODE[input.dtype], _lib.stream_of(input)))
+
+
 _IMPLS = {
     "fused_add_rms_norm": fused_add_rms_norm,
     "rms_norm_dynamic_per_token_quant": rms_norm_dynamic_per_token_quant,
+    "dynamic_scaled_int8_quant": dynamic_scaled_int8_quant,
+    "dynamic_per_token_scaled_fp8_quant": dynamic_per_token_scaled_fp8_quant,
 }
 
 _library = torch.library.Library("_C", "FRAGMENT")

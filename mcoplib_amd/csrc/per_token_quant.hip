@@ -1,0 +1,263 @@
+// per_token_quant.hip -- standalone dynamic per-token quantizers (vLLM `_C` ops): int8
+// symmetric, int8 asymmetric (zero point) and fp8-e4m3fn, one pass over HBM.
+//
+// Semantics (per row, v = f(x) widened exactly):
+//   int8 symmetric   op/vllm/quantization/compressed_tensors/int8_quant_kernels.cu:94-132
+//     A = max|v|; scale = A / 127; q = sat[-127,127](rne(v * (A > 0 ? 127 / A : 0)))
+//   int8 zero point  :370-422
+//     s = (max v - min v) / 255; zp = rne(-128 - min v / s); q = sat[-128,127](rne(v * (1/s)) + zp)
+//     (a constant row, s == 0, has no finite zero point: zp = -128 and q = -128 here)
+//   fp8 e4m3fn       op/vllm/quantization/fp8/common.cu:142-180
+//     A = max|v| (min with *scale_ub); s = max(A / 448, 1/(448*512)); q = e4m3fn(clamp(v / s))
+// The row is loaded once into VGPRs; one max reduction (two for the zero point form).
+#include <hip/hip_runtime.h>
+
+#include "../../include/mcop_norm.h"
+#include "rowkern.h"
+
+namespace mcop {
+
+enum PtqMode { PTQ_INT8 = 0, PTQ_INT8_AZP = 1, PTQ_FP8 = 2 };
+
+template <class E, int VEC, int NV, int MODE>
+__global__ void __launch_bounds__(max_tpr(VEC, NV))
+k_per_token_quant(uint8_t* __restrict__ out, float* __restrict__ scales, int32_t* __restrict__ azp,
+                  const typename E::S* __restrict__ x, const float* __restrict__ scale_ub,
+                  int64_t rows, int hidden, int64_t in_stride, int64_t out_stride, int tpr) {
+  using S = typename E::S;
+  __shared__ float red_a[16];
+  __shared__ float red_b[16];
+  const RowPos p = row_pos(rows, tpr);
+  const int nvec = hidden / VEC;
+  const int64_t lbase = p.lrow * in_stride;
+  const int64_t obase = p.row * out_stride;
+
+  Pack<S, VEC> xv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
+    xv[v] = ld_nt<S, VEC>(x + lbase + lj);
+  }
+  // Lanes past the row end hold a copy of vector 0 (read only: no effect on max or min).
+  float a[NV][VEC];
+  float mx = MODE == PTQ_INT8_AZP ? -__builtin_inff() : 0.0f;
+  float nmn = -__builtin_inff();  // max of -v, i.e. -(min v)
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float t = E::to_f(xv[v].v[e]);
+      a[v][e] = t;
+      if constexpr (MODE == PTQ_INT8_AZP) {
+        mx = __builtin_fmaxf(mx, t);
+        nmn = __builtin_fmaxf(nmn, -t);
+      } else {
+        mx = __builtin_fmaxf(mx, __builtin_fabsf(t));
+      }
+    }
+  }
+  mx = row_reduce(mx, red_a, tpr, MaxOp());
+
+  if constexpr (MODE == PTQ_INT8_AZP) {
+    nmn = row_reduce(nmn, red_b, tpr, MaxOp());
+    const float mn = -nmn;
+    const float s = mcop_div_rn(mx - mn, 255.0f);
+    const bool degenerate = !(s > 0.0f);
+    // zp = rne(-128 - mn / s) converted with saturation (it lies in [-128, 127] for s > 0)
+    const int zp = degenerate ? -128 : cvt_rne_i32(-128.0f - mcop_div_rn(mn, s));
+    const float inv = degenerate ? 0.0f : mcop_div_rn(1.0f, s);
+    if (p.live && p.lt == 0) {
+      scales[p.row] = s;
+      azp[p.row] = zp;
+    }
+    // Every v lies in [mn, mx], so |v * inv| <= |mn / s| + 255 (to a relative 2^-21), and
+    // |zp| >= |mn / s| - 129.  With |zp| <= 2^29 (uniform over the row) rne(v * inv) is below 2^30
+    // in magnitude and the int32 sum with zp cannot overflow; otherwise the sum is formed in 64
+    // bits.  rne(v * inv) saturates to int32 and maps NaN to 0; the sum saturates to int8.
+    const bool narrow = zp >= -(1 << 29) && zp <= (1 << 29);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int j = vec_index(v, tpr, p.lt);
+      if (p.live && j < nvec) {
+        Pack<uint8_t, VEC> q;
+        if (narrow) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const int t = cvt_rne_i32(a[v][e] * inv) + zp;
+            q.v[e] = (uint8_t)(int8_t)(t < -128 ? -128 : (t > 127 ? 127 : t));
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const int64_t t = (int64_t)cvt_rne_i32(a[v][e] * inv) + zp;
+            q.v[e] = (uint8_t)(int8_t)(t < -128 ? -128 : (t > 127 ? 127 : t));
+          }
+        }
+        st_nt<uint8_t, VEC>(out + obase + (int64_t)j * VEC, q);
+      }
+    }
+  } else if constexpr (MODE == PTQ_INT8) {
+    if (p.live && p.lt == 0) scales[p.row] = mcop_div_rn(mx, 127.0f);
+    const float inv = mx > 0.0f ? mcop_div_rn(127.0f, mx) : 0.0f;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int j = vec_index(v, tpr, p.lt);
+      if (p.live && j < nvec) {
+        Pack<uint8_t, VEC> q;
+        if constexpr (std::is_same_v<E, F32>) {
+          // fp32 inputs can carry NaN payloads in the low byte: round, convert and saturate
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-127>(a[v][e] * inv);
+        } else {
+          // |v * inv| <= 127 * (1 + 2^-23) < 127.5, so the code never saturates
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) q.v[e] = q_i8_in_range(a[v][e], inv);
+        }
+        st_nt<uint8_t, VEC>(out + obase + (int64_t)j * VEC, q);
+      }
+    }
+  } else {
+    float A = mx;
+    if (scale_ub != nullptr) A = __builtin_fminf(A, *scale_ub);
+    const float s = __builtin_fmaxf(mcop_div_rn(A, 448.0f), 1.0f / 229376.0f);
+    if (p.live && p.lt == 0) scales[p.row] = s;
+    const float inv = mcop_div_rn(1.0f, s);
+    const bool s_ok = mcop_divisor_ok(s);
+    const bool bounded = A == mx && s <= 0x1p100f;  // no scale bound cut the row's absmax
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int j = vec_index(v, tpr, p.lt);
+      if (p.live && j < nvec) {
+        st_nt<uint8_t, VEC>(out + obase + (int64_t)j * VEC,
+                            fp8_quotient_codes<VEC>(a[v], s, inv, s_ok, bounded));
+      }
+    }
+  }
+}
+
+template <class E, int VEC, int MODE>
+static const void* kernel_of(int nv) {
+  if constexpr (VEC == 1) {
+    return nv == 4 ? reinterpret_cast<const void*>(&k_per_token_quant<E, 1, 4, MODE>)
+                   : reinterpret_cast<const void*>(&k_per_token_quant<E, 1, 16, MODE>);
+  } else {
+    switch (nv) {
+      case 1: return reinterpret_cast<const void*>(&k_per_token_quant<E, VEC, 1, MODE>);
+      case 2: return reinterpret_cast<const void*>(&k_per_token_quant<E, VEC, 2, MODE>);
+      case 4: return reinterpret_cast<const void*>(&k_per_token_quant<E, VEC, 4, MODE>);
+      case 8: return reinterpret_cast<const void*>(&k_per_token_quant<E, VEC, 8, MODE>);
+      default: return reinterpret_cast<const void*>(&k_per_token_quant<E, VEC, 16, MODE>);
+    }
+  }
+}
+
+struct PtqArgs {
+  void* out;
+  float* scales;
+  int32_t* azp;
+  const void* x;
+  const float* scale_ub;
+  int64_t rows;
+  int hidden;
+  int64_t in_stride;
+  int64_t out_stride;
+};
+
+template <class E, int VEC, int MODE>
+static void launch_nv(const Geometry& g, const PtqArgs& a, hipStream_t st) {
+  using S = typename E::S;
+  const dim3 grid((unsigned)g.blocks), block((unsigned)(g.tpr * g.rpb));
+  auto* o = static_cast<uint8_t*>(a.out);
+  auto* xp = static_cast<const S*>(a.x);
+#define MCOP_LAUNCH(NVV)                                                                     \
+  hipLaunchKernelGGL((k_per_token_quant<E, VEC, NVV, MODE>), grid, block, 0, st, o, a.scales, \
+                     a.azp, xp, a.scale_ub, a.rows, a.hidden, a.in_stride, a.out_stride, g.tpr)
+  if constexpr (VEC == 1) {
+    if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
+  } else {
+    switch (g.nv) {
+      case 1: MCOP_LAUNCH(1); break;
+      case 2: MCOP_LAUNCH(2); break;
+      case 4: MCOP_LAUNCH(4); break;
+      case 8: MCOP_LAUNCH(8); break;
+      default: MCOP_LAUNCH(16); break;
+    }
+  }
+#undef MCOP_LAUNCH
+}
+
+template <class E, int MODE>
+static int dispatch(const char* name, const PtqArgs& a, hipStream_t st) {
+  constexpr int V = E::VEC;
+  const bool vec_ok = a.hidden % V == 0 && a.in_stride % V == 0 && a.out_stride % V == 0 &&
+                      aligned(16, a.x) && aligned(V, a.out);
+  Geometry g;
+  if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? V : 1,
+                       vec_ok ? &kernel_of<E, V, MODE> : &kernel_of<E, 1, MODE>, &g)) {
+    return set_error(MCOP_E_UNSUPPORTED,
+                     "%s: hidden_size %d is larger than the register-resident kernels support",
+                     name, a.hidden);
+  }
+  if (g.vec == 1) launch_nv<E, 1, MODE>(g, a, st);
+  else launch_nv<E, V, MODE>(g, a, st);
+  return check_launch(name);
+}
+
+template <int MODE>
+static int dispatch_dtype(const char* name, const PtqArgs& a, mcop_dtype dt, hipStream_t st) {
+  switch (dt) {
+    case MCOP_BF16: return dispatch<BF16, MODE>(name, a, st);
+    case MCOP_F16: return dispatch<F16, MODE>(name, a, st);
+    case MCOP_F32: return dispatch<F32, MODE>(name, a, st);
+    default:
+      return set_error(MCOP_E_INVALID, "%s: input dtype %d is not bf16/fp16/fp32", name, (int)dt);
+  }
+}
+
+static int check_shape(const char* name, int64_t rows, int64_t hidden, int64_t in_stride,
+                       int64_t out_stride) {
+  if (rows < 0 || hidden <= 0 || hidden > INT32_MAX || in_stride < hidden ||
+      out_stride < hidden) {
+    return set_error(MCOP_E_INVALID,
+                     "%s: bad shape num_tokens=%lld hidden_size=%lld strides=%lld/%lld", name,
+                     (long long)rows, (long long)hidden, (long long)in_stride,
+                     (long long)out_stride);
+  }
+  return MCOP_OK;
+}
+
+}  // namespace mcop
+
+extern "C" int mcop_dynamic_scaled_int8_quant(int8_t* out, float* scales, int32_t* azp,
+                                              const void* input, int64_t num_tokens,
+                                              int64_t hidden_size, mcop_dtype in_dtype,
+                                              void* stream) {
+  using namespace mcop;
+  const char* name = "dynamic_scaled_int8_quant";
+  if (int rc = check_shape(name, num_tokens, hidden_size, hidden_size, hidden_size)) return rc;
+  if (num_tokens == 0) return MCOP_OK;
+  if (!out || !scales || !input) return set_error(MCOP_E_INVALID, "%s: null pointer", name);
+  const PtqArgs a{out, scales, azp, input, nullptr, num_tokens, (int)hidden_size, hidden_size,
+                  hidden_size};
+  auto st = static_cast<hipStream_t>(stream);
+  return azp ? dispatch_dtype<PTQ_INT8_AZP>(name, a, in_dtype, st)
+             : dispatch_dtype<PTQ_INT8>(name, a, in_dtype, st);
+}
+
+extern "C" int mcop_dynamic_per_token_scaled_fp8_quant(uint8_t* out, float* scales,
+                                                       const void* input, const float* scale_ub,
+                                                       int64_t num_tokens, int64_t hidden_size,
+                                                       int64_t input_row_stride,
+                                                       int64_t output_row_stride,
+                                                       mcop_dtype in_dtype, void* stream) {
+  using namespace mcop;
+  const char* name = "dynamic_per_token_scaled_fp8_quant";
+  if (int rc = check_shape(name, num_tokens, hidden_size, input_row_stride, output_row_stride)) {
+    return rc;
+  }
+  if (num_tokens == 0) return MCOP_OK;
+  if (!out || !scales || !input) return set_error(MCOP_E_INVALID, "%s: null pointer", name);
+  const PtqArgs a{out, scales, nullptr, input, scale_ub, num_tokens, (int)hidden_size,
+                  input_row_stride, output_row_stride};
+  return dispatch_dtype<PTQ_FP8>(name, a, in_dtype, static_cast<hipStream_t>(stream));
+}

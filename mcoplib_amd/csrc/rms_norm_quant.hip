@@ -104,6 +104,7 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   if (p.live && p.lt == 0) scales[p.row] = s;
   const float inv = mcop_div_rn(1.0f, s);
   const bool s_ok = mcop_divisor_ok(s);
+  const bool bounded = A == amax && s <= 0x1p100f;  // no scale bound cut the row's absmax
 
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
@@ -111,11 +112,7 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
     if (p.live && j < nvec) {
       Pack<uint8_t, VEC> q;
       if constexpr (FP8) {
-        float c[VEC];
-        div_by_const<VEC>(c, a[v], s, inv, s_ok);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) c[e] = clamp_fp8(c[e]);
-        q = cvt_fp8<VEC>(c);
+        q = fp8_quotient_codes<VEC>(a[v], s, inv, s_ok, bounded);
       } else if (std::is_same_v<E, F32> || scale_ub != nullptr) {
         // fp32 inputs can carry NaN payloads in the low byte, and a scale bound lets |y * inv|
         // exceed 127: round, convert and saturate

@@ -202,6 +202,34 @@ __device__ __forceinline__ float clamp_fp8(float v) {
   return __builtin_fmaxf(-448.0f, __builtin_fminf(v, 448.0f));
 }
 
+// fp8-e4m3fn codes of clamp(RN(a[e] / b)) for the N values of one vector.
+// `bounded` (uniform over the row) states that every |a| of the row is at most 448 * b * (1 +
+// 2^-22) (the row's absmax was not cut by a scale bound) and that 2^-18 <= b <= 2^100.  Then the
+// Markstein form q0 = a*inv, r = fma(-q0, b, a), q = fma(r, inv, q0) is exact for every element
+// with |a| >= 2^-100 and |a/b| >= 2^-100 (|q| <= 449: no intermediate overflow or underflow);
+// every other element has |a/b| < 2^-82, the form then yields some |q| < 2^-80, and any such
+// value codes to a zero.  copysign gives that zero a's sign (the correction step turns -0 into
+// +0).  NaN elements stay NaN and clamp to +448 as in the division.  Rows that are not bounded
+// take div_by_const.
+template <int N>
+__device__ __forceinline__ Pack<uint8_t, N> fp8_quotient_codes(const float* a, float b, float inv,
+                                                               bool b_ok, bool bounded) {
+  float c[N];
+  if (bounded) {
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      const float q0 = a[e] * inv;
+      const float r = __builtin_fmaf(-q0, b, a[e]);
+      c[e] = __builtin_copysignf(__builtin_fmaf(r, inv, q0), a[e]);
+    }
+  } else {
+    div_by_const<N>(c, a, b, inv, b_ok);
+  }
+#pragma unroll
+  for (int e = 0; e < N; ++e) c[e] = clamp_fp8(c[e]);
+  return cvt_fp8<N>(c);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Row reductions.  Every thread of the workgroup must call them (they may contain a barrier).
 // `lds` holds one slot per wave of the workgroup (at most 16).  The sum is of fp64 partials;

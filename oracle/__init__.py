@@ -43,13 +43,18 @@ def _load() -> ctypes.CDLL:
     lib.oracle_rms_norm_smooth_quant.argtypes = [P, I, P, P, P, I, P, I, P, P, P, I64, I64, I, F, I]
     lib.oracle_scale_dynamic_quant.argtypes = [P, P, P, P, I64, I64]
     lib.oracle_fp8_e4m3fn_from_f32.argtypes = [P, P, I64, F]
+    lib.oracle_dynamic_scaled_int8_quant.argtypes = [P, P, P, I64, I64, I]
+    lib.oracle_dynamic_scaled_int8_azp_quant.argtypes = [P, P, P, P, I64, I64, I]
+    lib.oracle_dynamic_per_token_fp8_quant.argtypes = [P, P, P, P, I64, I64, I64, I64, I]
     for name in ("oracle_f32_to_bf16_array", "oracle_f32_to_f16_array",
                  "oracle_f32_to_e4m3fn_array"):
         getattr(lib, name).argtypes = [P, P, I64]
     for name in ("oracle_fused_add_rms_norm", "oracle_rms_norm_quant",
                  "oracle_rms_norm_smooth_quant", "oracle_scale_dynamic_quant",
                  "oracle_fp8_e4m3fn_from_f32", "oracle_f32_to_bf16_array",
-                 "oracle_f32_to_f16_array", "oracle_f32_to_e4m3fn_array", "oracle_set_threads"):
+                 "oracle_f32_to_f16_array", "oracle_f32_to_e4m3fn_array", "oracle_set_threads",
+                 "oracle_dynamic_scaled_int8_quant", "oracle_dynamic_scaled_int8_azp_quant",
+                 "oracle_dynamic_per_token_fp8_quant"):
         getattr(lib, name).restype = None
     lib.oracle_set_threads.argtypes = [I]
     lib.oracle_num_threads.restype = I
@@ -165,6 +170,46 @@ def scale_dynamic_quant(h: torch.Tensor, smooth: torch.Tensor
     return out, scales
 
 
+# ------------------------------------------------------------------------------------ quantizers
+def dynamic_scaled_int8_quant(x: torch.Tensor, use_azp: bool = False
+                              ) -> tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """vLLM ``_C::dynamic_scaled_int8_quant``
+    (op/vllm/quantization/compressed_tensors/int8_quant_kernels.cu:94-132, 370-422, 459-527).
+
+    Returns (int8 codes shaped like x, scales [T, 1] fp32, azp [T, 1] int32 or None)."""
+    xc = _cpu(x)
+    T, H = _rows(xc)
+    out = torch.empty(xc.shape, dtype=torch.int8)
+    scales = torch.empty((T, 1), dtype=torch.float32)
+    if use_azp:
+        azp = torch.empty((T, 1), dtype=torch.int32)
+        lib().oracle_dynamic_scaled_int8_azp_quant(out.data_ptr(), scales.data_ptr(),
+                                                   azp.data_ptr(), xc.data_ptr(), T, H,
+                                                   _DT[x.dtype])
+        return out, scales, azp
+    lib().oracle_dynamic_scaled_int8_quant(out.data_ptr(), scales.data_ptr(), xc.data_ptr(), T,
+                                           H, _DT[x.dtype])
+    return out, scales, None
+
+
+def dynamic_per_token_scaled_fp8_quant(x: torch.Tensor, scale_ub: Optional[float] = None
+                                       ) -> tuple[torch.Tensor, torch.Tensor]:
+    """vLLM ``_C::dynamic_per_token_scaled_fp8_quant`` (op/vllm/quantization/fp8/common.cu:142-180,
+    375-411).  x may have strided rows (unit last-dimension stride).
+
+    Returns (fp8-e4m3fn codes shaped like x, contiguous; scales [T, 1] fp32)."""
+    assert x.device.type == "cpu", "the oracle takes CPU tensors"
+    xc = x if (x.dim() == 2 and x.stride(-1) == 1) else x.contiguous()
+    T, H = _rows(xc)
+    in_stride = xc.stride(0) if xc.dim() == 2 and T > 1 else H
+    out = torch.empty(xc.shape, dtype=torch.float8_e4m3fn)
+    scales = torch.empty((T, 1), dtype=torch.float32)
+    ub = None if scale_ub is None else ctypes.byref(ctypes.c_float(float(scale_ub)))
+    lib().oracle_dynamic_per_token_fp8_quant(out.data_ptr(), scales.data_ptr(), xc.data_ptr(),
+                                             ub, T, H, in_stride, H, _DT[x.dtype])
+    return out, scales
+
+
 # ------------------------------------------------------------------------------------ formats
 def fp8_e4m3fn_from_f32(x: torch.Tensor, mul: float = 1.0) -> torch.Tensor:
     """e4m3fn(clamp(x * mul, +-448)) as uint8 codes (quant_conversions.cuh:23-28)."""
@@ -196,7 +241,7 @@ def f32_to_e4m3fn_bits(x: torch.Tensor) -> torch.Tensor:
 __all__ = [
     "build", "set_threads", "num_threads", "fused_add_rms_norm",
     "rms_norm_dynamic_per_token_quant", "rms_norm_smooth_quant", "scale_dynamic_quant",
-    "fp8_e4m3fn_from_f32", "f32_to_bf16_bits", "f32_to_f16_bits", "f32_to_e4m3fn_bits",
+    "dynamic_scaled_int8_quant", "dynamic_per_token_scaled_fp8_quant", "fp8_e4m3fn_from_f32", "f32_to_bf16_bits", "f32_to_f16_bits", "f32_to_e4m3fn_bits",
 ]
 
 if os.environ.get("MCOP_ORACLE_THREADS"):

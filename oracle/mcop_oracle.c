@@ -304,6 +304,88 @@ void oracle_scale_dynamic_quant(int8_t* out, float* scales, const uint16_t* h, c
   }
 }
 
+/* ---------------------------------------------------------------- standalone per-token quant */
+
+/* float -> int32 as the reference's float_to_int32_rn
+   (op/vllm/quantization/compressed_tensors/int8_quant_kernels.cu:27-35): round to nearest even,
+   saturate to the int32 range; NaN -> 0 (the hardware conversion's NaN result). */
+static inline int32_t cvt_sat_i32(float v) {
+  if (isnan(v)) return 0;
+  const float t = rintf(v);
+  if (t >= 2147483648.0f) return INT32_MAX;
+  if (t <= -2147483648.0f) return INT32_MIN;
+  return (int32_t)t;
+}
+
+/* vLLM dynamic_scaled_int8_quant without azp,
+   op/vllm/quantization/compressed_tensors/int8_quant_kernels.cu:94-132 (generic kernel) and the
+   register / LDS variants the host selects for 16-bit inputs (:167-339, chosen at :480-518),
+   which do the same arithmetic:
+     A = max|x|; scales[t] = A / 127; inv = 127 / A (0 when A == 0);
+     q = sat[-127,127](rne(x * inv)) (float_to_int8_rn, :14-24).
+   The variants compute 127 / A without the zero test; for A == 0 that gives 0 * inf = NaN,
+   which the conversion maps to 0 -- the same codes. */
+void oracle_dynamic_scaled_int8_quant(int8_t* out, float* scales, const void* x, int64_t T,
+                                      int64_t H, int dt) {
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < T; ++t) {
+    float amax = 0.0f;
+    for (int64_t i = 0; i < H; ++i) amax = fmaxf(amax, fabsf(load_el(x, dt, t * H + i)));
+    scales[t] = amax / 127.0f;
+    const float inv = amax == 0.0f ? 0.0f : 127.0f / amax;
+    for (int64_t i = 0; i < H; ++i) out[t * H + i] = q_int8(load_el(x, dt, t * H + i) * inv, -127);
+  }
+}
+
+/* vLLM dynamic_scaled_int8_quant with azp (asymmetric), int8_quant_kernels.cu:370-422:
+     s = (max x - min x) / 255; zp = (int32) nearbyint(-128 - min x / s); inv = 1 / s;
+     q = sat[-128,127](float_to_int32_rn(x * inv) + zp)  (int32_to_int8, :37-46).
+   The integer sum is formed in 64 bits (the reference's int32 sum cannot overflow for s > 0).
+   A constant row (s == 0) has no zero point -- the reference converts NaN / inf to int there,
+   which has no defined result; this restatement writes s = 0, zp = -128 and q = -128. */
+void oracle_dynamic_scaled_int8_azp_quant(int8_t* out, float* scales, int32_t* azp,
+                                          const void* x, int64_t T, int64_t H, int dt) {
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < T; ++t) {
+    float mx = -INFINITY, mn = INFINITY;
+    for (int64_t i = 0; i < H; ++i) {
+      const float v = load_el(x, dt, t * H + i);
+      mx = fmaxf(mx, v);
+      mn = fminf(mn, v);
+    }
+    const float s = (mx - mn) / 255.0f;
+    const int degenerate = !(s > 0.0f);
+    const int32_t zp = degenerate ? -128 : cvt_sat_i32(-128.0f - mn / s);
+    const float inv = degenerate ? 0.0f : 1.0f / s;
+    scales[t] = s;
+    azp[t] = zp;
+    for (int64_t i = 0; i < H; ++i) {
+      int64_t q = (int64_t)cvt_sat_i32(load_el(x, dt, t * H + i) * inv) + zp;
+      q = q < -128 ? -128 : (q > 127 ? 127 : q);
+      out[t * H + i] = (int8_t)q;
+    }
+  }
+}
+
+/* vLLM dynamic_per_token_scaled_fp8_quant, op/vllm/quantization/fp8/common.cu:142-180
+   (host :375-411), rows at in_stride / out_stride elements:
+     A = max|x| (min with *scale_ub); s = max(A / 448, 1/(448*512)); q = e4m3fn(clamp(x / s)).
+   `scale_ub` is a host pointer here (NULL = none). */
+void oracle_dynamic_per_token_fp8_quant(uint8_t* out, float* scales, const void* x,
+                                        const float* scale_ub, int64_t T, int64_t H,
+                                        int64_t in_stride, int64_t out_stride, int dt) {
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < T; ++t) {
+    float amax = 0.0f;
+    for (int64_t i = 0; i < H; ++i) amax = fmaxf(amax, fabsf(load_el(x, dt, t * in_stride + i)));
+    if (scale_ub) amax = fminf(amax, *scale_ub);
+    const float s = fmaxf(amax / 448.0f, 1.0f / (448.0f * 512.0f));
+    scales[t] = s;
+    for (int64_t i = 0; i < H; ++i)
+      out[t * out_stride + i] = q_fp8(load_el(x, dt, t * in_stride + i) / s);
+  }
+}
+
 /* ---------------------------------------------------------------- elementwise fp8 */
 
 void oracle_fp8_e4m3fn_from_f32(uint8_t* out, const float* in, int64_t n, float mul) {

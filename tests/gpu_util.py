@@ -59,8 +59,9 @@ def assert_scales(s: torch.Tensor, s_ref: torch.Tensor, what: str) -> None:
     r = s_ref.flatten().double()
     zero = r == 0
     assert torch.all(s[zero] == 0), f"{what}: scale should be 0"
-    rel = ((s - r).abs() / r.abs().clamp_min(1e-300))[~zero]
-    n_diff = int((s != r).sum())
+    same = (s == r) | (torch.isnan(s) & torch.isnan(r))  # equal infinities / NaNs included
+    rel = ((s - r).abs() / r.abs().clamp_min(1e-300))[~zero & ~same]
+    n_diff = int((~same).sum())
     say(f"  {what}: {n_diff} of {s.numel()} scales differ (max rel {float(rel.max()) if rel.numel() else 0:.3e})")
     assert rel.numel() == 0 or float(rel.max()) <= SCALE_RTOL, f"{what}: scale rel err"
 
