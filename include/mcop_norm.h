@@ -113,7 +113,8 @@ int mcop_scale_dynamic_quant(int8_t* out, float* scales, const void* input, cons
  *   azp == NULL (symmetric): A = max|x|; scales[t] = A/127; q = sat[-127,127](rne(x * (127/A)))
  *     (A == 0 gives q = 0);
  *   azp != NULL (asymmetric): s = (max x - min x)/255; azp[t] = rne(-128 - min x / s);
- *     q = sat[-128,127](rne(x * (1/s)) + azp[t]); a constant row (s == 0) gives azp = q = -128.
+ *     q = sat[-128,127](rne(x * (1/s)) + azp[t]) (a NaN element codes 127, as the reference's
+ *     fmin clamp before its conversion gives); a constant row (s == 0) gives azp = q = -128.
  * input bf16/fp16/fp32 [T,H] contiguous; out int8 [T,H]; scales fp32 [T]; azp int32 [T].
  * Replaces dynamic_scaled_int8_quant(),
  * op/vllm/quantization/compressed_tensors/int8_quant_kernels.cu:459-527 (kernels :94-132,

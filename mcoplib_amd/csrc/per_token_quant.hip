@@ -5,7 +5,8 @@
 //   int8 symmetric   op/vllm/quantization/compressed_tensors/int8_quant_kernels.cu:94-132
 //     A = max|v|; scale = A / 127; q = sat[-127,127](rne(v * (A > 0 ? 127 / A : 0)))
 //   int8 zero point  :370-422
-//     s = (max v - min v) / 255; zp = rne(-128 - min v / s); q = sat[-128,127](rne(v * (1/s)) + zp)
+//     s = (max v - min v) / 255; zp = rne(-128 - min v / s);
+//     q = sat[-128,127](float_to_int32_rn(v * (1/s)) + zp), NaN products coding 127
 //     (a constant row, s == 0, has no finite zero point: zp = -128 and q = -128 here)
 //   fp8 e4m3fn       op/vllm/quantization/fp8/common.cu:142-180
 //     A = max|v| (min with *scale_ub); s = max(A / 448, 1/(448*512)); q = e4m3fn(clamp(v / s))
@@ -70,10 +71,12 @@ k_per_token_quant(uint8_t* __restrict__ out, float* __restrict__ scales, int32_t
       scales[p.row] = s;
       azp[p.row] = zp;
     }
-    // Every v lies in [mn, mx], so |v * inv| <= |mn / s| + 255 (to a relative 2^-21), and
-    // |zp| >= |mn / s| - 129.  With |zp| <= 2^29 (uniform over the row) rne(v * inv) is below 2^30
-    // in magnitude and the int32 sum with zp cannot overflow; otherwise the sum is formed in 64
-    // bits.  rne(v * inv) saturates to int32 and maps NaN to 0; the sum saturates to int8.
+    // float_to_int32_rn of the reference clamps with fmin/fmax before the saturating
+    // conversion, so a NaN product becomes 2^31 -> INT32_MAX and codes 127.  Every finite v lies
+    // in [mn, mx], so |v * inv| <= |mn / s| + 255 (to a relative 2^-21), and |zp| >= |mn / s| -
+    // 129.  With |zp| <= 2^29 (uniform over the row) the products stay below 2^30 in magnitude:
+    // clamping NaN to 2^30 instead still codes 127, and the int32 sum with zp cannot overflow.
+    // Otherwise the sum is formed in 64 bits.  The sum saturates to int8.
     const bool narrow = zp >= -(1 << 29) && zp <= (1 << 29);
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
@@ -83,13 +86,14 @@ k_per_token_quant(uint8_t* __restrict__ out, float* __restrict__ scales, int32_t
         if (narrow) {
 #pragma unroll
           for (int e = 0; e < VEC; ++e) {
-            const int t = cvt_rne_i32(a[v][e] * inv) + zp;
+            const int t = cvt_rne_i32(__builtin_fminf(a[v][e] * inv, 0x1p30f)) + zp;
             q.v[e] = (uint8_t)(int8_t)(t < -128 ? -128 : (t > 127 ? 127 : t));
           }
         } else {
 #pragma unroll
           for (int e = 0; e < VEC; ++e) {
-            const int64_t t = (int64_t)cvt_rne_i32(a[v][e] * inv) + zp;
+            const int64_t t =
+                (int64_t)cvt_rne_i32(__builtin_fminf(a[v][e] * inv, 0x1p31f)) + zp;
             q.v[e] = (uint8_t)(int8_t)(t < -128 ? -128 : (t > 127 ? 127 : t));
           }
         }

@@ -306,15 +306,23 @@ void oracle_scale_dynamic_quant(int8_t* out, float* scales, const uint16_t* h, c
 
 /* ---------------------------------------------------------------- standalone per-token quant */
 
-/* float -> int32 as the reference's float_to_int32_rn
-   (op/vllm/quantization/compressed_tensors/int8_quant_kernels.cu:27-35): round to nearest even,
-   saturate to the int32 range; NaN -> 0 (the hardware conversion's NaN result). */
+/* float -> int32, round to nearest even, saturating; NaN -> 0 (the hardware conversion's NaN
+   result, as in the reference's azp_t(zp) at int8_quant_kernels.cu:406). */
 static inline int32_t cvt_sat_i32(float v) {
   if (isnan(v)) return 0;
   const float t = rintf(v);
   if (t >= 2147483648.0f) return INT32_MAX;
   if (t <= -2147483648.0f) return INT32_MIN;
   return (int32_t)t;
+}
+
+/* The reference's float_to_int32_rn (int8_quant_kernels.cu:27-35): x = min(x, 2^31),
+   x = max(x, -2^31) with fmin/fmax semantics, then the saturating conversion -- so NaN becomes
+   2^31 and converts to INT32_MAX. */
+static inline int32_t float_to_int32_rn(float v) {
+  v = fminf(v, 2147483648.0f);
+  v = fmaxf(v, -2147483648.0f);
+  return cvt_sat_i32(v);
 }
 
 /* vLLM dynamic_scaled_int8_quant without azp,
@@ -339,8 +347,9 @@ void oracle_dynamic_scaled_int8_quant(int8_t* out, float* scales, const void* x,
 
 /* vLLM dynamic_scaled_int8_quant with azp (asymmetric), int8_quant_kernels.cu:370-422:
      s = (max x - min x) / 255; zp = (int32) nearbyint(-128 - min x / s); inv = 1 / s;
-     q = sat[-128,127](float_to_int32_rn(x * inv) + zp)  (int32_to_int8, :37-46).
-   The integer sum is formed in 64 bits (the reference's int32 sum cannot overflow for s > 0).
+     q = sat[-128,127](float_to_int32_rn(x * inv) + zp)  (int32_to_int8, :37-46);
+   a NaN element therefore codes 127.  The integer sum is formed in 64 bits (the reference's
+   int32 sum overflows only for a NaN element with zp > 0, where saturation gives 127 too).
    A constant row (s == 0) has no zero point -- the reference converts NaN / inf to int there,
    which has no defined result; this restatement writes s = 0, zp = -128 and q = -128. */
 void oracle_dynamic_scaled_int8_azp_quant(int8_t* out, float* scales, int32_t* azp,
@@ -360,7 +369,7 @@ void oracle_dynamic_scaled_int8_azp_quant(int8_t* out, float* scales, int32_t* a
     scales[t] = s;
     azp[t] = zp;
     for (int64_t i = 0; i < H; ++i) {
-      int64_t q = (int64_t)cvt_sat_i32(load_el(x, dt, t * H + i) * inv) + zp;
+      int64_t q = (int64_t)float_to_int32_rn(load_el(x, dt, t * H + i) * inv) + zp;
       q = q < -128 ? -128 : (q > 127 ? 127 : q);
       out[t * H + i] = (int8_t)q;
     }

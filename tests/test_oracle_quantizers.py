@@ -105,6 +105,16 @@ def test_azp_all_positive_row_has_large_zero_point():
     assert q.tolist() == [[-128, -1, 127]]
 
 
+def test_azp_nan_element_codes_like_the_fmin_clamp():
+    # float_to_int32_rn: min(NaN, 2^31) = 2^31 -> INT32_MAX; + zp saturates to 127
+    x = torch.tensor([[-1.0, 0.0, float("nan"), 2.0]], dtype=torch.float32)
+    q, s, azp = oracle.dynamic_scaled_int8_quant(x, use_azp=True)
+    assert azp.item() == -43 and q.tolist() == [[-128, -43, 127, 127]]
+    # the symmetric form converts directly: NaN -> 0
+    q, _, _ = oracle.dynamic_scaled_int8_quant(x)
+    assert q.tolist() == [[-64, 0, 0, 127]]
+
+
 def test_azp_constant_row_is_defined():
     x = torch.full((3, 40), 2.5, dtype=torch.bfloat16)
     x[2] = 0
