@@ -30,6 +30,7 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 HBM_PEAK_GBS = 8000.0
 METRIC = "HBM GB/s & % of peak: fused add-RMSNorm+per-token int8 quant, 8192x8192"
+PAD_SIZE = 3840  # padded workload: bf16 elements per padded row (2 * 3840 bytes)
 
 
 def parse():
@@ -40,7 +41,7 @@ def parse():
     ap.add_argument("--workload", default="cfg3",
                     choices=["cfg2", "cfg3", "cfg4", "cfg5-large", "cfg5-decode1",
                              "cfg5-decode4", "cfg5-decode16", "cfg5-decode64", "ptq-int8",
-                             "ptq-int8-azp", "ptq-fp8"])
+                             "ptq-int8-azp", "ptq-fp8", "padded"])
     ap.add_argument("--sets", type=int, default=0,
                     help="rotated input sets (default: enough for > 1 GiB, at least 3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -72,6 +73,8 @@ class Workload:
             return 3 * T * H + 4 * T
         if self.kind == "ptq_int8_azp":    # read x; write q, s, azp
             return 3 * T * H + 8 * T
+        if self.kind == "padded":          # read x, r; write r, rms, q, padded q + scale, s; w
+            return 10 * T * H + 8 * T + 2 * H
         raise ValueError(self.kind)
 
     def make(self, torch, dev, seed):
@@ -84,9 +87,14 @@ class Workload:
         x = x.to(torch.bfloat16)
         w = (1 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
         d = {"x": x, "w": w}
-        if self.kind in ("add_norm_int8", "fused_add"):
+        if self.kind in ("add_norm_int8", "fused_add", "padded"):
             d["r"] = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
         if self.kind == "add_norm_int8":
+            d["q"] = torch.empty(T, H, dtype=torch.int8, device=dev)
+            d["s"] = torch.empty(T, 1, dtype=torch.float32, device=dev)
+        if self.kind == "padded":
+            d["p"] = torch.empty(T, 2 * PAD_SIZE, dtype=torch.int8, device=dev)
+            d["rms"] = torch.empty_like(x)
             d["q"] = torch.empty(T, H, dtype=torch.int8, device=dev)
             d["s"] = torch.empty(T, 1, dtype=torch.float32, device=dev)
         if self.kind.startswith("ptq_"):
@@ -111,6 +119,9 @@ class Workload:
                 d["q"], d["x"], d["w"], d["s"], self.eps, None, d["r"])
         if self.kind == "fused_add":
             return lambda: torch.ops._C.fused_add_rms_norm(d["x"], d["r"], d["w"], self.eps)
+        if self.kind == "padded":
+            return lambda: op.fused_add_rms_norm_dynamic_per_token_quant_padding_output(
+                d["p"], d["rms"], d["q"], d["s"], d["x"], d["r"], d["w"], PAD_SIZE, self.eps)
         if self.kind == "ptq_fp8":
             return lambda: torch.ops._C.dynamic_per_token_scaled_fp8_quant(d["q"], d["x"], d["s"],
                                                                          None)
@@ -131,10 +142,13 @@ WORKLOADS = {
     "ptq-int8": Workload("ptq-int8", 8192, 8192, 0.0, "ptq_int8"),
     "ptq-int8-azp": Workload("ptq-int8-azp", 8192, 8192, 0.0, "ptq_int8_azp"),
     "ptq-fp8": Workload("ptq-fp8", 8192, 8192, 0.0, "ptq_fp8"),
+    # the padded wire format at DeepSeek's width (H 7168, rows of 2 * 3840 bytes)
+    "padded": Workload("padded", 8192, 7168, 1e-6, "padded"),
 }
 KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "fused_add": "k_fused_add_rms_norm",
                "smooth_fp8": "k_rms_norm_smooth_quant", "ptq_int8": "k_per_token_quant",
-               "ptq_int8_azp": "k_per_token_quant", "ptq_fp8": "k_per_token_quant"}
+               "ptq_int8_azp": "k_per_token_quant", "ptq_fp8": "k_per_token_quant",
+               "padded": "k_add_rms_norm_quant_padded"}
 
 
 # ------------------------------------------------------------------------------ pieces
@@ -168,6 +182,8 @@ def cpu_baseline(wl: Workload, seconds: float) -> dict:
             oracle.rms_norm_dynamic_per_token_quant(x, w, wl.eps, torch.int8, residual=r)
         elif wl.kind == "fused_add":
             oracle.fused_add_rms_norm(x, r, w, wl.eps)
+        elif wl.kind == "padded":
+            oracle.add_rms_norm_quant_padded(x, r, w, PAD_SIZE, wl.eps)
         elif wl.kind == "ptq_fp8":
             oracle.dynamic_per_token_scaled_fp8_quant(x)
         elif wl.kind.startswith("ptq_int8"):

@@ -135,6 +135,25 @@ int mcop_dynamic_per_token_scaled_fp8_quant(uint8_t* out, float* scales, const v
                                             int64_t output_row_stride, mcop_dtype in_dtype,
                                             void* stream);
 
+/* Residual add + RMSNorm + per-token int8 quantization into a padded per-row wire layout
+ * (mcoplib.op.fused_add_rms_norm_dynamic_per_token_quant_padding_output).
+ *   output: int8 [T, 2*pad_size] bytes; row t holds its H codes at bytes [0, H) and its fp32
+ *     scale at bytes [H, H+4); the rest of the row is not written (2*pad_size >= H + 4);
+ *   output_rms: bf16 [T,H] normalized values; output_quant_int8: int8 [T,H] the same codes;
+ *   out_scales: fp32 [T]; input, residual (updated in place: input + residual), weight: bf16.
+ * Two rounding chains, as the reference dispatches them: H == 7168 keeps a = x + r in fp32
+ * (rms = b((a*w)*rho), q = sat[-127,127](rne((a*w)*rho / s))), other H round bf16 products
+ * (q from y = b(b(b(a)*rho)*w)); s = max(absmax*rho/127, FLT_EPSILON) with absmax taken over
+ * a*w (H == 7168) or b(b(a)*w).
+ * Replaces add_rms_norm_dynamic_per_token_quant_padding_output(),
+ * op/fused_add_layernorm_per_token_quant_padding_output.cu:397-416 (kernels :181-283 and
+ * :287-340, dispatch :344-395; pybind op/pybind.cpp:54; Python wrapper
+ * mcoplib/custom_ops.py:7-27). */
+int mcop_fused_add_rms_norm_dynamic_per_token_quant_padding_output(
+    int8_t* output, void* output_rms, int8_t* output_quant_int8, float* out_scales,
+    const void* input, void* residual, const void* weight, int64_t num_tokens,
+    int64_t hidden_size, int64_t pad_size, float epsilon, void* stream);
+
 /* The clamp-and-convert step shared by every fp8 epilogue, elementwise:
  *   out[i] = e4m3fn(clamp(in[i] * mul, -448, 448))   (RNE; clamp with fmin/fmax semantics)
  * No reference counterpart as an entry point (the step is float_to_fp8,

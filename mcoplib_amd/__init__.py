@@ -3,10 +3,14 @@ per-token quantization path.
 
 Surfaces (same names, argument order and in-place conventions as the reference):
   mcoplib_amd.op          -- mcoplib.op: rms_norm_dynamic_per_token_quant (fused_rms_norm_dq),
-                             rms_norm_dynamic_per_token_quant_custom, scale_dynamic_quant
-  mcoplib_amd.custom_ops  -- mcoplib.custom_ops.rms_norm_dynamic_per_token_quant
-  mcoplib_amd._C          -- registers torch.ops._C.fused_add_rms_norm and
-                             torch.ops._C.rms_norm_dynamic_per_token_quant
+                             rms_norm_dynamic_per_token_quant_custom, scale_dynamic_quant,
+                             fused_add_rms_norm_dynamic_per_token_quant_padding_output
+  mcoplib_amd.custom_ops  -- mcoplib.custom_ops.rms_norm_dynamic_per_token_quant and
+                             fused_add_rms_norm_dynamic_per_token_quant_padding_output
+  mcoplib_amd._C          -- registers torch.ops._C.fused_add_rms_norm,
+                             torch.ops._C.rms_norm_dynamic_per_token_quant,
+                             torch.ops._C.dynamic_scaled_int8_quant and
+                             torch.ops._C.dynamic_per_token_scaled_fp8_quant
 
 All of them call libmcop_norm.so (hand-written HIP kernels, C ABI in include/mcop_norm.h).
 Importing the package fails if that library is not built: there is no other implementation.

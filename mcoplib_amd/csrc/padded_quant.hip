@@ -1,0 +1,231 @@
+// padded_quant.hip -- residual add + RMSNorm + per-token int8 quantization into a padded
+// per-row wire layout (mcoplib.op.fused_add_rms_norm_dynamic_per_token_quant_padding_output),
+// one pass over HBM.
+//
+// Layout of `padded` (row stride pad_bytes = 2 * pad_size bytes): row t holds its H int8 codes
+// at bytes [0, H) and its fp32 scale at bytes [H, H + 4); the remaining bytes are not written
+// (op/fused_add_layernorm_per_token_quant_padding_output.cu:216, 246, 255, 320).
+//
+// The reference dispatches two kernels with different rounding chains (entry :344-395):
+//   H == 7168 ("opt" kernel, :181-283), a = x + r in fp32, never rounded in between:
+//     r <- b(a); p = a * w; A = max|p|; rho = 1/sqrt(sum a^2 / H + eps);
+//     s = max((A * rho) / 127, FLT_EPSILON); u = p * rho;
+//     rms <- b(u); q = sat[-127,127](rne(u * (1/s)))
+//   any other H ("generic" kernel, :287-340), with bf16 products rounded to bf16:
+//     r <- b(a); A = max|b(b(a) * w)|; rho as above; s as above;
+//     y = b(b(b(a) * rho) * w); q = sat[-127,127](rne(y * (1/s)))
+//     The generic kernel writes only `padded` and the residual; here it also writes rms <- y,
+//     the unpacked codes and scales[t], so every output is defined for every H.
+// Both write q to `padded` and to the unpacked int8 output, s to `padded` and (opt) scales[t].
+// b() = round to bf16 (RNE); the row sum is the fp64 sum rounded once (order-independent).
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+
+#include "../../include/mcop_norm.h"
+#include "rowkern.h"
+
+namespace mcop {
+
+template <int VEC, int NV, bool OPT>
+__global__ void __launch_bounds__(max_tpr(VEC, NV))
+k_add_rms_norm_quant_padded(uint8_t* __restrict__ padded, uint16_t* __restrict__ rms,
+                            uint8_t* __restrict__ q_out, float* __restrict__ scales,
+                            const uint16_t* __restrict__ x, uint16_t* __restrict__ res,
+                            const uint16_t* __restrict__ w, int64_t rows, int hidden,
+                            int64_t pad_bytes, int tpr, float eps) {
+  using E = BF16;
+  __shared__ double red_sum[16];
+  __shared__ float red_max[16];
+  const RowPos p = row_pos(rows, tpr);
+  const int nvec = hidden / VEC;
+  const int64_t base = p.row * (int64_t)hidden;
+  const int64_t lbase = p.lrow * (int64_t)hidden;
+  const int64_t pbase = p.row * pad_bytes;
+
+  Pack<uint16_t, VEC> xv[NV], rv[NV], wv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
+    xv[v] = ld_nt<uint16_t, VEC>(x + lbase + lj);
+    rv[v] = ld_nt<uint16_t, VEC>(res + lbase + lj);
+    wv[v] = ld<uint16_t, VEC>(w + lj);
+  }
+
+  // a: opt keeps p = a * w (fp32); generic keeps b(a) (the residual value it re-reads)
+  const bool full = (int64_t)NV * tpr == nvec;
+  float a[NV][VEC];
+  double ss = 0.0;
+  float amax = 0.0f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int j = vec_index(v, tpr, p.lt);
+    const bool in = j < nvec;
+    double vs = 0.0;
+    Pack<uint16_t, VEC> o;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float t = E::to_f(xv[v].v[e]) + E::to_f(rv[v].v[e]);
+      const double d = (double)t;
+      vs = __builtin_fma(d, d, vs);
+      o.v[e] = E::from_f(t);
+      const float wf = E::to_f(wv[v].v[e]);
+      float m;
+      if constexpr (OPT) {
+        a[v][e] = t * wf;
+        m = a[v][e];
+      } else {
+        a[v][e] = E::to_f(o.v[e]);
+        m = rnd<E>(a[v][e] * wf);
+      }
+      // lanes past the row end hold a copy of vector 0, possibly of the updated residual
+      amax = __builtin_fmaxf(amax, (full || in) ? __builtin_fabsf(m) : 0.0f);
+    }
+    ss += in ? vs : 0.0;
+    if (p.live && in) st_nt<uint16_t, VEC>(res + base + (int64_t)j * VEC, o);
+  }
+  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  amax = row_reduce(amax, red_max, tpr, MaxOp());
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+  const float s = __builtin_fmaxf(mcop_div_rn(amax * rho, 127.0f), FLT_EPSILON);
+  const float inv = mcop_div_rn(1.0f, s);
+  if (p.live && p.lt == 0) {
+    scales[p.row] = s;
+    uint8_t* sp = padded + pbase + hidden;
+    if ((reinterpret_cast<uintptr_t>(sp) & 3) == 0) {
+      *reinterpret_cast<float*>(sp) = s;
+    } else {
+      const uint32_t b = __builtin_bit_cast(uint32_t, s);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sp[k] = (uint8_t)(b >> (8 * k));
+    }
+  }
+
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int j = vec_index(v, tpr, p.lt);
+    if (p.live && j < nvec) {
+      Pack<uint16_t, VEC> o;
+      Pack<uint8_t, VEC> q;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        float y;
+        if constexpr (OPT) {
+          y = a[v][e] * rho;
+          o.v[e] = E::from_f(y);
+        } else {
+          o.v[e] = E::from_f(rnd<E>(a[v][e] * rho) * E::to_f(wv[v].v[e]));
+          y = E::to_f(o.v[e]);
+        }
+        q.v[e] = q_i8<-127>(y * inv);
+      }
+      st_nt<uint16_t, VEC>(rms + base + (int64_t)j * VEC, o);
+      st_nt<uint8_t, VEC>(q_out + base + (int64_t)j * VEC, q);
+      st_nt<uint8_t, VEC>(padded + pbase + (int64_t)j * VEC, q);
+    }
+  }
+}
+
+template <int VEC, bool OPT>
+static const void* kernel_of(int nv) {
+  if constexpr (VEC == 1) {
+    return nv == 4 ? reinterpret_cast<const void*>(&k_add_rms_norm_quant_padded<1, 4, OPT>)
+                   : reinterpret_cast<const void*>(&k_add_rms_norm_quant_padded<1, 16, OPT>);
+  } else {
+    switch (nv) {
+      case 1: return reinterpret_cast<const void*>(&k_add_rms_norm_quant_padded<VEC, 1, OPT>);
+      case 2: return reinterpret_cast<const void*>(&k_add_rms_norm_quant_padded<VEC, 2, OPT>);
+      case 4: return reinterpret_cast<const void*>(&k_add_rms_norm_quant_padded<VEC, 4, OPT>);
+      case 8: return reinterpret_cast<const void*>(&k_add_rms_norm_quant_padded<VEC, 8, OPT>);
+      default: return reinterpret_cast<const void*>(&k_add_rms_norm_quant_padded<VEC, 16, OPT>);
+    }
+  }
+}
+
+struct PadArgs {
+  uint8_t* padded;
+  uint16_t* rms;
+  uint8_t* q;
+  float* scales;
+  const uint16_t* x;
+  uint16_t* res;
+  const uint16_t* w;
+  int64_t rows;
+  int hidden;
+  int64_t pad_bytes;
+  float eps;
+};
+
+template <int VEC, bool OPT>
+static void launch_nv(const Geometry& g, const PadArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)g.blocks), block((unsigned)(g.tpr * g.rpb));
+#define MCOP_LAUNCH(NVV)                                                                       \
+  hipLaunchKernelGGL((k_add_rms_norm_quant_padded<VEC, NVV, OPT>), grid, block, 0, st,          \
+                     a.padded, a.rms, a.q, a.scales, a.x, a.res, a.w, a.rows, a.hidden,       \
+                     a.pad_bytes, g.tpr, a.eps)
+  if constexpr (VEC == 1) {
+    if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
+  } else {
+    switch (g.nv) {
+      case 1: MCOP_LAUNCH(1); break;
+      case 2: MCOP_LAUNCH(2); break;
+      case 4: MCOP_LAUNCH(4); break;
+      case 8: MCOP_LAUNCH(8); break;
+      default: MCOP_LAUNCH(16); break;
+    }
+  }
+#undef MCOP_LAUNCH
+}
+
+template <bool OPT>
+static int dispatch(const PadArgs& a, hipStream_t st) {
+  const char* name = "fused_add_rms_norm_dynamic_per_token_quant_padding_output";
+  const bool vec_ok = a.hidden % 8 == 0 && a.pad_bytes % 8 == 0 &&
+                      aligned(16, a.x, a.res, a.w, a.rms) && aligned(8, a.q, a.padded);
+  Geometry g;
+  if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? 8 : 1,
+                       vec_ok ? &kernel_of<8, OPT> : &kernel_of<1, OPT>, &g)) {
+    return set_error(MCOP_E_UNSUPPORTED,
+                     "%s: hidden_size %d is larger than the register-resident kernels support",
+                     name, a.hidden);
+  }
+  if (g.vec == 1) launch_nv<1, OPT>(g, a, st);
+  else launch_nv<8, OPT>(g, a, st);
+  return check_launch(name);
+}
+
+}  // namespace mcop
+
+extern "C" int mcop_fused_add_rms_norm_dynamic_per_token_quant_padding_output(
+    int8_t* output, void* output_rms, int8_t* output_quant_int8, float* out_scales,
+    const void* input, void* residual, const void* weight, int64_t num_tokens,
+    int64_t hidden_size, int64_t pad_size, float epsilon, void* stream) {
+  using namespace mcop;
+  const char* name = "fused_add_rms_norm_dynamic_per_token_quant_padding_output";
+  if (num_tokens < 0 || hidden_size <= 0 || hidden_size > INT32_MAX || pad_size <= 0 ||
+      2 * pad_size < hidden_size + 4) {
+    return set_error(MCOP_E_INVALID,
+                     "%s: bad shape num_tokens=%lld hidden_size=%lld pad_size=%lld (a padded "
+                     "row of 2*pad_size bytes must hold hidden_size codes and a 4-byte scale)",
+                     name, (long long)num_tokens, (long long)hidden_size, (long long)pad_size);
+  }
+  if (num_tokens == 0) return MCOP_OK;
+  if (!output || !output_rms || !output_quant_int8 || !out_scales || !input || !residual ||
+      !weight) {
+    return set_error(MCOP_E_INVALID, "%s: null pointer", name);
+  }
+  const PadArgs a{reinterpret_cast<uint8_t*>(output),
+                  static_cast<uint16_t*>(output_rms),
+                  reinterpret_cast<uint8_t*>(output_quant_int8),
+                  out_scales,
+                  static_cast<const uint16_t*>(input),
+                  static_cast<uint16_t*>(residual),
+                  static_cast<const uint16_t*>(weight),
+                  num_tokens,
+                  (int)hidden_size,
+                  2 * pad_size,
+                  epsilon};
+  auto st = static_cast<hipStream_t>(stream);
+  // the reference's dispatch: the "opt" rounding chain for H == 7168, the generic one otherwise
+  return hidden_size == 7168 ? dispatch<true>(a, st) : dispatch<false>(a, st);
+}

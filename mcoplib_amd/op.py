@@ -1,10 +1,11 @@
 """``mcoplib.op`` surface of the fused norm/quant path, backed by libmcop_norm.so (gfx950).
 
-Functions keep the reference pybind signatures (op/pybind.cpp:42, 51, 55; declarations in
+Functions keep the reference pybind signatures (op/pybind.cpp:42, 51, 54, 55; declarations in
 include/fused_rms_norm_dq.h:3-12, include/rms_norm_dynamic_per_token_quant.h:2-8,
-include/scale_dynamic_quant.h:6-10), their positional argument order, in-place outputs and
-error behaviour.  Every call enqueues one kernel on torch's current stream of the tensors'
-device and returns without synchronizing.
+include/scale_dynamic_quant.h:6-10,
+include/fused_add_layernorm_per_token_quant_padding_output.h:3-11), their positional argument
+order, in-place outputs and error behaviour.  Every call enqueues one kernel on torch's current
+stream of the tensors' device and returns without synchronizing.
 """
 
 from __future__ import annotations
@@ -21,6 +22,7 @@ __all__ = [
     "rms_norm_dynamic_per_token_quant",
     "rms_norm_dynamic_per_token_quant_custom",
     "scale_dynamic_quant",
+    "fused_add_rms_norm_dynamic_per_token_quant_padding_output",
 ]
 
 
@@ -148,3 +150,49 @@ def scale_dynamic_quant(hidden_states: torch.Tensor, smooth_scales: torch.Tensor
             output.data_ptr(), scales.data_ptr(), hidden_states.data_ptr(),
             smooth_scales.data_ptr(), T, H, _lib.stream_of(hidden_states)))
     return output, scales
+
+
+def fused_add_rms_norm_dynamic_per_token_quant_padding_output(
+        output: torch.Tensor, output_rms: torch.Tensor, output_quant_int8: torch.Tensor,
+        out_scales: torch.Tensor, input: torch.Tensor, residual: torch.Tensor,
+        weight: torch.Tensor, pad_size: int, epsilon: float) -> None:
+    """Residual add + RMSNorm + per-token int8 quantization with a padded per-row output
+    (reference entry op/fused_add_layernorm_per_token_quant_padding_output.cu:397-416).
+
+    ``output`` (int8, 2*pad_size bytes per row) receives each row's codes at bytes [0, H) and
+    its fp32 scale at bytes [H, H+4); ``output_rms`` (bf16) the normalized row,
+    ``output_quant_int8`` the codes again, ``out_scales`` the scales; ``residual`` becomes
+    input + residual.  bf16 input, int8 output, as in the reference.  H == 7168 uses the
+    reference's fp32 chain (its "opt" kernel); other H its bf16-rounded chain, and here every
+    output is written for every H (the reference's generic kernel leaves output_rms,
+    output_quant_int8 and out_scales unwritten)."""
+    name = "fused_add_rms_norm_dynamic_per_token_quant_padding_output"
+    torch_check(output.dtype == torch.int8, "output.dtype() == torch::kInt8")
+    torch_check(input.dtype == torch.bfloat16, "input.dtype() == at::ScalarType::BFloat16")
+    torch_check(output.is_contiguous() and input.is_contiguous(),
+                "output.is_contiguous() && input.is_contiguous()")
+    on_cuda(name, output, output_rms, output_quant_int8, out_scales, input, residual, weight)
+    T, H = rows_of(input)
+    pad = int(pad_size)
+    if 2 * pad < H + 4:
+        raise RuntimeError(f"{name}: a padded row of 2*pad_size = {2 * pad} bytes cannot hold "
+                           f"{H} codes and a 4-byte scale")
+    numel_check(name, "output", output, T * 2 * pad)
+    for what, t, dt in (("output_rms", output_rms, torch.bfloat16),
+                        ("output_quant_int8", output_quant_int8, torch.int8),
+                        ("residual", residual, torch.bfloat16),
+                        ("weight", weight, torch.bfloat16),
+                        ("out_scales", out_scales, torch.float32)):
+        if t.dtype != dt:
+            raise RuntimeError(f"{name}: {what} must be {dt}, got {t.dtype}")
+        contiguous_check(name, what, t)
+    numel_check(name, "output_rms", output_rms, T * H)
+    numel_check(name, "output_quant_int8", output_quant_int8, T * H)
+    numel_check(name, "residual", residual, T * H)
+    numel_check(name, "weight", weight, H)
+    numel_check(name, "out_scales", out_scales, T)
+    with _lib.device_of(input):
+        _lib.check(_lib.lib.mcop_fused_add_rms_norm_dynamic_per_token_quant_padding_output(
+            output.data_ptr(), output_rms.data_ptr(), output_quant_int8.data_ptr(),
+            out_scales.data_ptr(), input.data_ptr(), residual.data_ptr(), weight.data_ptr(),
+            T, H, pad, float(epsilon), _lib.stream_of(input)))

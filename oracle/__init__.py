@@ -46,6 +46,7 @@ def _load() -> ctypes.CDLL:
     lib.oracle_dynamic_scaled_int8_quant.argtypes = [P, P, P, I64, I64, I]
     lib.oracle_dynamic_scaled_int8_azp_quant.argtypes = [P, P, P, P, I64, I64, I]
     lib.oracle_dynamic_per_token_fp8_quant.argtypes = [P, P, P, P, I64, I64, I64, I64, I]
+    lib.oracle_add_rms_norm_quant_padded.argtypes = [P, I64, P, P, P, P, P, P, I64, I64, F]
     for name in ("oracle_f32_to_bf16_array", "oracle_f32_to_f16_array",
                  "oracle_f32_to_e4m3fn_array"):
         getattr(lib, name).argtypes = [P, P, I64]
@@ -54,7 +55,7 @@ def _load() -> ctypes.CDLL:
                  "oracle_fp8_e4m3fn_from_f32", "oracle_f32_to_bf16_array",
                  "oracle_f32_to_f16_array", "oracle_f32_to_e4m3fn_array", "oracle_set_threads",
                  "oracle_dynamic_scaled_int8_quant", "oracle_dynamic_scaled_int8_azp_quant",
-                 "oracle_dynamic_per_token_fp8_quant"):
+                 "oracle_dynamic_per_token_fp8_quant", "oracle_add_rms_norm_quant_padded"):
         getattr(lib, name).restype = None
     lib.oracle_set_threads.argtypes = [I]
     lib.oracle_num_threads.restype = I
@@ -210,6 +211,28 @@ def dynamic_per_token_scaled_fp8_quant(x: torch.Tensor, scale_ub: Optional[float
     return out, scales
 
 
+# ------------------------------------------------------------------------------------ padded
+def add_rms_norm_quant_padded(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                              pad_size: int, eps: float, fill: int = 0):
+    """mcoplib ``fused_add_rms_norm_dynamic_per_token_quant_padding_output``
+    (op/fused_add_layernorm_per_token_quant_padding_output.cu:181-416).  bf16 only.
+
+    Returns (padded uint8 [T, 2*pad_size] -- bytes the op does not write hold ``fill`` --,
+    new residual, output_rms bf16, codes int8, scales [T, 1] fp32)."""
+    xc, w = _cpu(x), _cpu(weight)
+    assert xc.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+    T, H = _rows(xc)
+    ro = _cpu(residual).clone()
+    padded = torch.full((T, 2 * pad_size), fill, dtype=torch.uint8)
+    rms = torch.empty_like(xc)
+    q = torch.empty(xc.shape, dtype=torch.int8)
+    scales = torch.empty((T, 1), dtype=torch.float32)
+    lib().oracle_add_rms_norm_quant_padded(padded.data_ptr(), 2 * pad_size, rms.data_ptr(),
+                                           q.data_ptr(), scales.data_ptr(), xc.data_ptr(),
+                                           ro.data_ptr(), w.data_ptr(), T, H, float(eps))
+    return padded, ro, rms, q, scales
+
+
 # ------------------------------------------------------------------------------------ formats
 def fp8_e4m3fn_from_f32(x: torch.Tensor, mul: float = 1.0) -> torch.Tensor:
     """e4m3fn(clamp(x * mul, +-448)) as uint8 codes (quant_conversions.cuh:23-28)."""
@@ -241,7 +264,8 @@ def f32_to_e4m3fn_bits(x: torch.Tensor) -> torch.Tensor:
 __all__ = [
     "build", "set_threads", "num_threads", "fused_add_rms_norm",
     "rms_norm_dynamic_per_token_quant", "rms_norm_smooth_quant", "scale_dynamic_quant",
-    "dynamic_scaled_int8_quant", "dynamic_per_token_scaled_fp8_quant", "fp8_e4m3fn_from_f32", "f32_to_bf16_bits", "f32_to_f16_bits", "f32_to_e4m3fn_bits",
+    "dynamic_scaled_int8_quant", "dynamic_per_token_scaled_fp8_quant",
+    "add_rms_norm_quant_padded", "fp8_e4m3fn_from_f32", "f32_to_bf16_bits", "f32_to_f16_bits", "f32_to_e4m3fn_bits",
 ]
 
 if os.environ.get("MCOP_ORACLE_THREADS"):

@@ -395,6 +395,66 @@ void oracle_dynamic_per_token_fp8_quant(uint8_t* out, float* scales, const void*
   }
 }
 
+/* ---------------------------------------------------------------- padded wire format */
+
+/* mcoplib fused_add_rms_norm_dynamic_per_token_quant_padding_output,
+   op/fused_add_layernorm_per_token_quant_padding_output.cu (entry :397-416, dispatch :344-395).
+   Row t of `padded` (pad_bytes per row) receives the H codes at bytes [0, H) and the fp32 scale
+   at bytes [H, H+4) (:216, :246, :255, :320); nothing else of the row is written.
+   H == 7168, the "opt" kernel (:181-283), a = x + r in fp32:
+     r <- b(a); p = a * w; A = max|p|; rho = 1/sqrt(S/H + eps);
+     s = max((A * rho) / 127, FLT_EPSILON); u = p * rho; rms <- b(u);
+     q = sat[-127,127](rne(u * (1/s)))  (float_to_int8_rn of kernel/utils.h:219-226).
+   Other H, the generic kernel (:287-340): A = max|b(b(a) * w)| (bf16 product, :308);
+     y = b(b(b(a) * rho) * w) (:334); q = sat[-127,127](rne(y * (1/s))); the reference writes
+     only `padded` and r -- here rms <- y, q and scales[t] are written too. */
+void oracle_add_rms_norm_quant_padded(uint8_t* padded, int64_t pad_bytes, uint16_t* rms,
+                                      int8_t* q, float* scales, const uint16_t* x, uint16_t* r,
+                                      const uint16_t* w, int64_t T, int64_t H, float eps) {
+  const int opt = H == 7168;
+#pragma omp parallel
+  {
+    float* a = (float*)malloc((size_t)H * sizeof(float));
+#pragma omp for schedule(static)
+    for (int64_t t = 0; t < T; ++t) {
+      acc64 S = {0.0, 0.0};
+      float amax = 0.0f;
+      for (int64_t i = 0; i < H; ++i) {
+        const float v = bf16_to_f32(x[t * H + i]) + bf16_to_f32(r[t * H + i]);
+        acc_add(&S, (double)v * (double)v);
+        r[t * H + i] = oracle_f32_to_bf16(v);
+        const float wf = bf16_to_f32(w[i]);
+        if (opt) {
+          a[i] = v * wf;
+          amax = fmaxf(amax, fabsf(a[i]));
+        } else {
+          a[i] = bf16_to_f32(r[t * H + i]);
+          amax = fmaxf(amax, fabsf(rnd_el(a[i] * wf, DT_BF16)));
+        }
+      }
+      const float rho = inv_rms(acc_val(&S), H, eps);
+      const float s = fmaxf((amax * rho) / 127.0f, FLT_EPSILON);
+      const float inv = 1.0f / s;
+      scales[t] = s;
+      memcpy(padded + t * pad_bytes + H, &s, 4);
+      for (int64_t i = 0; i < H; ++i) {
+        float y;
+        if (opt) {
+          y = a[i] * rho;
+          rms[t * H + i] = oracle_f32_to_bf16(y);
+        } else {
+          y = rnd_el(rnd_el(a[i] * rho, DT_BF16) * bf16_to_f32(w[i]), DT_BF16);
+          rms[t * H + i] = oracle_f32_to_bf16(y);
+        }
+        const int8_t c = q_int8(y * inv, -127);
+        q[t * H + i] = c;
+        padded[t * pad_bytes + i] = (uint8_t)c;
+      }
+    }
+    free(a);
+  }
+}
+
 /* ---------------------------------------------------------------- elementwise fp8 */
 
 void oracle_fp8_e4m3fn_from_f32(uint8_t* out, const float* in, int64_t n, float mul) {

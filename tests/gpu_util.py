@@ -9,6 +9,7 @@ be bit-exact everywhere; the tests report how many elements differ at all.
 
 from __future__ import annotations
 
+import os
 import sys
 
 import torch
@@ -16,6 +17,8 @@ import torch
 DEV = "cuda:0"
 SCALE_RTOL = 1e-6
 CODE_FRAC = 1e-4
+# MCOP_TEST_EXACT=1 tightens the bar to bit equality for codes and scales as well
+EXACT = os.environ.get("MCOP_TEST_EXACT", "") == "1"
 
 
 def gen(seed: int) -> torch.Generator:
@@ -52,6 +55,7 @@ def assert_codes(q: torch.Tensor, q_ref: torch.Tensor, what: str) -> None:
     say(f"  {what}: {n_diff} of {d.numel()} codes differ (max step {int(d.max()) if d.numel() else 0})")
     assert int(d.max() if d.numel() else 0) <= 1, f"{what}: code differs by more than one step"
     assert frac <= CODE_FRAC, f"{what}: {n_diff} codes differ ({frac:.2e} > {CODE_FRAC})"
+    assert not EXACT or n_diff == 0, f"{what}: {n_diff} codes differ (exact mode)"
 
 
 def assert_scales(s: torch.Tensor, s_ref: torch.Tensor, what: str) -> None:
@@ -64,6 +68,7 @@ def assert_scales(s: torch.Tensor, s_ref: torch.Tensor, what: str) -> None:
     n_diff = int((~same).sum())
     say(f"  {what}: {n_diff} of {s.numel()} scales differ (max rel {float(rel.max()) if rel.numel() else 0:.3e})")
     assert rel.numel() == 0 or float(rel.max()) <= SCALE_RTOL, f"{what}: scale rel err"
+    assert not EXACT or n_diff == 0, f"{what}: {n_diff} scales differ (exact mode)"
 
 
 def assert_exact(t: torch.Tensor, ref: torch.Tensor, what: str) -> None:
