@@ -31,6 +31,7 @@ ROOT = Path(__file__).resolve().parent
 HBM_PEAK_GBS = 8000.0
 METRIC = "HBM GB/s & % of peak: fused add-RMSNorm+per-token int8 quant, 8192x8192"
 PAD_SIZE = 3840  # padded workload: bf16 elements per padded row (2 * 3840 bytes)
+BLOCK_GROUP = 128  # block-fp8 workload: elements per scale group
 
 
 def parse():
@@ -41,7 +42,7 @@ def parse():
     ap.add_argument("--workload", default="cfg3",
                     choices=["cfg2", "cfg3", "cfg4", "cfg5-large", "cfg5-decode1",
                              "cfg5-decode4", "cfg5-decode16", "cfg5-decode64", "ptq-int8",
-                             "ptq-int8-azp", "ptq-fp8", "padded"])
+                             "ptq-int8-azp", "ptq-fp8", "padded", "block-fp8"])
     ap.add_argument("--sets", type=int, default=0,
                     help="rotated input sets (default: enough for > 1 GiB, at least 3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -75,6 +76,8 @@ class Workload:
             return 3 * T * H + 8 * T
         if self.kind == "padded":          # read x, r; write r, rms, q, padded q + scale, s; w
             return 10 * T * H + 8 * T + 2 * H
+        if self.kind == "block_fp8":       # read x, r, w; write r, q, one scale per group
+            return 7 * T * H + 2 * H + 4 * T * (H // BLOCK_GROUP)
         raise ValueError(self.kind)
 
     def make(self, torch, dev, seed):
@@ -87,11 +90,14 @@ class Workload:
         x = x.to(torch.bfloat16)
         w = (1 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
         d = {"x": x, "w": w}
-        if self.kind in ("add_norm_int8", "fused_add", "padded"):
+        if self.kind in ("add_norm_int8", "fused_add", "padded", "block_fp8"):
             d["r"] = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
         if self.kind == "add_norm_int8":
             d["q"] = torch.empty(T, H, dtype=torch.int8, device=dev)
             d["s"] = torch.empty(T, 1, dtype=torch.float32, device=dev)
+        if self.kind == "block_fp8":
+            d["q"] = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=dev)
+            d["s"] = torch.empty(T, H // BLOCK_GROUP, dtype=torch.float32, device=dev)
         if self.kind == "padded":
             d["p"] = torch.empty(T, 2 * PAD_SIZE, dtype=torch.int8, device=dev)
             d["rms"] = torch.empty_like(x)
@@ -119,6 +125,9 @@ class Workload:
                 d["q"], d["x"], d["w"], d["s"], self.eps, None, d["r"])
         if self.kind == "fused_add":
             return lambda: torch.ops._C.fused_add_rms_norm(d["x"], d["r"], d["w"], self.eps)
+        if self.kind == "block_fp8":
+            return lambda: torch.ops._C.rms_norm_per_block_quant(
+                d["q"], d["x"], d["w"], d["s"], self.eps, None, d["r"], BLOCK_GROUP, False)
         if self.kind == "padded":
             return lambda: op.fused_add_rms_norm_dynamic_per_token_quant_padding_output(
                 d["p"], d["rms"], d["q"], d["s"], d["x"], d["r"], d["w"], PAD_SIZE, self.eps)
@@ -144,11 +153,13 @@ WORKLOADS = {
     "ptq-fp8": Workload("ptq-fp8", 8192, 8192, 0.0, "ptq_fp8"),
     # the padded wire format at DeepSeek's width (H 7168, rows of 2 * 3840 bytes)
     "padded": Workload("padded", 8192, 7168, 1e-6, "padded"),
+    # per-group (128) fp8 scales for block-scaled GEMMs, at the headline shape with residual
+    "block-fp8": Workload("block-fp8", 8192, 8192, 1e-6, "block_fp8"),
 }
 KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "fused_add": "k_fused_add_rms_norm",
                "smooth_fp8": "k_rms_norm_smooth_quant", "ptq_int8": "k_per_token_quant",
                "ptq_int8_azp": "k_per_token_quant", "ptq_fp8": "k_per_token_quant",
-               "padded": "k_add_rms_norm_quant_padded"}
+               "padded": "k_add_rms_norm_quant_padded", "block_fp8": "k_rms_norm_group_quant"}
 
 
 # ------------------------------------------------------------------------------ pieces
@@ -182,6 +193,9 @@ def cpu_baseline(wl: Workload, seconds: float) -> dict:
             oracle.rms_norm_dynamic_per_token_quant(x, w, wl.eps, torch.int8, residual=r)
         elif wl.kind == "fused_add":
             oracle.fused_add_rms_norm(x, r, w, wl.eps)
+        elif wl.kind == "block_fp8":
+            oracle.rms_norm_per_block_quant(x, w, wl.eps, torch.float8_e4m3fn, BLOCK_GROUP,
+                                            residual=r)
         elif wl.kind == "padded":
             oracle.add_rms_norm_quant_padded(x, r, w, PAD_SIZE, wl.eps)
         elif wl.kind == "ptq_fp8":

@@ -135,6 +135,22 @@ int mcop_dynamic_per_token_scaled_fp8_quant(uint8_t* out, float* scales, const v
                                             int64_t output_row_stride, mcop_dtype in_dtype,
                                             void* stream);
 
+/* (Residual add +) RMSNorm + dynamic per-group quantization (vLLM `_C::rms_norm_per_block_quant`):
+ * as mcop_rms_norm_dynamic_per_token_quant, but with one scale per group of group_size (64 or
+ * 128) consecutive elements of a row: A_g = max|y| over the group (min with *scale_ub, fp8
+ * only), s_g = max(A_g/127, FLT_EPSILON) (int8) or max(A_g/448, 1/(448*512)) (fp8).
+ * scales: fp32 [T, H/group_size], or [H/group_size, T] when is_scale_transposed != 0.
+ * hidden_size must be a multiple of group_size.
+ * Replaces rms_norm_per_block_quant(),
+ * op/vllm/quantization/fused_kernels/fused_layernorm_dynamic_per_token_quant.cu:238-270
+ * (dispatch :194-236, kernel :92-126, layernorm_utils.cuh:283-393, 455-535; schema
+ * op/vllm/torch_bindings.cpp:224-229). */
+int mcop_rms_norm_per_block_quant(void* out, mcop_dtype out_dtype, float* scales,
+                                  const void* input, const void* weight, const float* scale_ub,
+                                  void* residual, int64_t num_tokens, int64_t hidden_size,
+                                  mcop_dtype in_dtype, float epsilon, int64_t group_size,
+                                  int is_scale_transposed, void* stream);
+
 /* Residual add + RMSNorm + per-token int8 quantization into a padded per-row wire layout
  * (mcoplib.op.fused_add_rms_norm_dynamic_per_token_quant_padding_output).
  *   output: int8 [T, 2*pad_size] bytes; row t holds its H codes at bytes [0, H) and its fp32

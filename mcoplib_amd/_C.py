@@ -2,9 +2,9 @@
 
 Importing this module registers, in the ``_C`` torch.library namespace, the schemas of
 op/vllm/torch_bindings.cpp:161-164 (``fused_add_rms_norm``), :216-221
-(``rms_norm_dynamic_per_token_quant``), :359-364 (``dynamic_per_token_scaled_fp8_quant``) and
-:374-379 (``dynamic_scaled_int8_quant``) with implementations for the CUDA (HIP) dispatch key
-that call libmcop_norm.so.  If another library (vLLM's own ``_C``) already defined a schema, only the
+(``rms_norm_dynamic_per_token_quant``), :224-229 (``rms_norm_per_block_quant``), :359-364
+(``dynamic_per_token_scaled_fp8_quant``) and :374-379 (``dynamic_scaled_int8_quant``) with
+implementations for the CUDA (HIP) dispatch key that call libmcop_norm.so.  If another library (vLLM's own ``_C``) already defined a schema, only the
 CUDA implementation is registered over it.  There is no CPU implementation: calling these ops on
 CPU tensors raises, as the reference does.
 """
@@ -26,6 +26,10 @@ SCHEMAS = {
     "rms_norm_dynamic_per_token_quant":
         "rms_norm_dynamic_per_token_quant(Tensor! result, Tensor input, Tensor weight, "
         "Tensor! scale, float epsilon, Tensor? scale_ub, Tensor!? residual) -> ()",
+    "rms_norm_per_block_quant":
+        "rms_norm_per_block_quant(Tensor! result, Tensor input, Tensor weight, Tensor! scale, "
+        "float epsilon, Tensor? scale_ub, Tensor!? residual, int group_size, "
+        "bool is_scale_transposed) -> ()",
     "dynamic_scaled_int8_quant":
         "dynamic_scaled_int8_quant(Tensor! result, Tensor input, Tensor! scale, "
         "Tensor!? azp) -> ()",
@@ -88,6 +92,54 @@ def rms_norm_dynamic_per_token_quant(result: torch.Tensor, input: torch.Tensor,
     dispatch_check(input.dtype, "rms_norm_dynamic_per_token_quant_dispatch")
     _norm_quant("rms_norm_dynamic_per_token_quant", result, input, weight, scale, epsilon,
                 scale_ub, residual)
+
+
+def rms_norm_per_block_quant(result: torch.Tensor, input: torch.Tensor, weight: torch.Tensor,
+                             scale: torch.Tensor, epsilon: float,
+                             scale_ub: Optional[torch.Tensor], residual: Optional[torch.Tensor],
+                             group_size: int, is_scale_transposed: bool) -> None:
+    """(Residual add +) RMSNorm + dynamic per-group int8 / fp8-e4m3fn quantization, one scale
+    per group of 64 or 128 elements (reference host function
+    op/vllm/quantization/fused_kernels/fused_layernorm_dynamic_per_token_quant.cu:238-270)."""
+    name = "rms_norm_per_block_quant"
+    fp8 = torch.float8_e4m3fn
+    torch_check(result.dtype in (fp8, torch.int8),
+                "out.dtype() == kFp8Type || out.dtype() == torch::kInt8")
+    torch_check(result.is_contiguous() and input.is_contiguous(),
+                "out.is_contiguous() && input.is_contiguous()")
+    if scale_ub is not None:
+        torch_check(result.dtype == fp8, "out.dtype() == kFp8Type")
+    torch_check(weight.dtype == input.dtype, "weight.dtype() == input.dtype()")
+    torch_check(scale.dtype == torch.float32, "scales.dtype() == torch::kFloat32")
+    if residual is not None:
+        torch_check(residual.dtype == input.dtype,
+                    "residual->scalar_type() == input.scalar_type()")
+    if group_size not in (64, 128):
+        raise RuntimeError(f"Unsupported group size: {group_size}")
+    dispatch_check(input.dtype, "rms_norm_per_block_quant_fp_dispatch")
+    on_cuda(name, result, input, weight, scale, scale_ub, residual)
+    T, H = rows_of(input)
+    if H % group_size != 0:
+        raise RuntimeError(f"{name}: hidden_size {H} is not a multiple of group_size "
+                           f"{group_size}")
+    numel_check(name, "result", result, T * H)
+    numel_check(name, "weight", weight, H)
+    numel_check(name, "scale", scale, T * (H // group_size))
+    contiguous_check(name, "weight", weight)
+    contiguous_check(name, "scale", scale)
+    if residual is not None:
+        contiguous_check(name, "residual", residual)
+        numel_check(name, "residual", residual, T * H)
+    if scale_ub is not None and (scale_ub.dtype != torch.float32 or scale_ub.numel() < 1):
+        raise RuntimeError(f"{name}: scale_ub must be a float32 tensor with one element")
+    with _lib.device_of(input):
+        _lib.check(_lib.lib.mcop_rms_norm_per_block_quant(
+            result.data_ptr(), _lib.DTYPE_CODE[result.dtype], scale.data_ptr(),
+            input.data_ptr(), weight.data_ptr(),
+            None if scale_ub is None else scale_ub.data_ptr(),
+            None if residual is None else residual.data_ptr(), T, H,
+            _lib.DTYPE_CODE[input.dtype], float(epsilon), int(group_size),
+            1 if is_scale_transposed else 0, _lib.stream_of(input)))
 
 
 def dynamic_scaled_int8_quant(result: torch.Tensor, input: torch.Tensor, scale: torch.Tensor,
@@ -160,6 +212,7 @@ _IMPLS = {
     "rms_norm_dynamic_per_token_quant": rms_norm_dynamic_per_token_quant,
     "dynamic_scaled_int8_quant": dynamic_scaled_int8_quant,
     "dynamic_per_token_scaled_fp8_quant": dynamic_per_token_scaled_fp8_quant,
+    "rms_norm_per_block_quant": rms_norm_per_block_quant,
 }
 
 _library = torch.library.Library("_C", "FRAGMENT")

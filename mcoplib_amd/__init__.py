@@ -9,6 +9,7 @@ Surfaces (same names, argument order and in-place conventions as the reference):
                              fused_add_rms_norm_dynamic_per_token_quant_padding_output
   mcoplib_amd._C          -- registers torch.ops._C.fused_add_rms_norm,
                              torch.ops._C.rms_norm_dynamic_per_token_quant,
+                             torch.ops._C.rms_norm_per_block_quant,
                              torch.ops._C.dynamic_scaled_int8_quant and
                              torch.ops._C.dynamic_per_token_scaled_fp8_quant
 

@@ -1,0 +1,270 @@
+// group_quant.hip -- (residual add +) RMSNorm + dynamic per-group int8 / fp8-e4m3fn
+// quantization (vLLM `_C::rms_norm_per_block_quant`), one pass over HBM.
+//
+// Semantics (per row, a = x [+ r] in fp32, b() = round to the input dtype; paths relative to
+// op/vllm/quantization/fused_kernels/ of the reference):
+//   residual <- b(a)                           layernorm_utils.cuh:500-508
+//   rho = 1/sqrt(sum(a^2)/H + eps)             layernorm_utils.cuh:223-279 (order: fp64 sum)
+//   y = b(b(a*rho) * w)                        layernorm_utils.cuh:325-329, 530-531
+//   per group g of G = 64 or 128 consecutive elements:
+//     A_g = max|y| over the group, min(A_g, *scale_ub)          :303-352
+//     int8: s_g = max(A_g/127, FLT_EPSILON); q = sat[-128,127](rne(y * (1/s_g)))
+//     fp8 : s_g = max(A_g/448, 1/(448*512)); q = e4m3fn(clamp(y / s_g, +-448))
+//   scales[t * (H/G) + g], or scales[g * T + t] when transposed   :352-357, 517-521
+// (the int8 code is the intended round-to-nearest-even with saturation, as for the per-token
+// kernel of the same file).
+//
+// Lane mapping: the vector paths keep the row kernels' strided mapping (vector j = v*tpr + lane),
+// so the G/VEC vectors of one group sit in G/VEC consecutive lanes and the group maximum is a
+// butterfly over those lanes of one wave; the element-wise path (misaligned tensors) gives each
+// lane NV consecutive elements instead, so a group spans G/NV lanes.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <type_traits>
+
+#include "../../include/mcop_norm.h"
+#include "rowkern.h"
+
+namespace mcop {
+
+// max over aligned runs of `lanes` consecutive lanes (a power of two <= 64) of one wave
+__device__ __forceinline__ float group_max(float v, int lanes) {
+  for (int m = 1; m < lanes; m <<= 1) v = __builtin_fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+template <class E, int VEC, int NV, bool FP8, bool RES>
+__global__ void __launch_bounds__(max_tpr(VEC, NV))
+k_rms_norm_group_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
+                       const typename E::S* __restrict__ x, const typename E::S* __restrict__ w,
+                       const float* __restrict__ scale_ub, typename E::S* __restrict__ res,
+                       int64_t rows, int hidden, int tpr, float eps, int group,
+                       int64_t scale_row_stride, int64_t scale_group_stride) {
+  using S = typename E::S;
+  constexpr bool BLOCKED = VEC == 1;
+  __shared__ double red_sum[16];
+  const RowPos p = row_pos(rows, tpr);
+  const int nvec = hidden / VEC;
+  const int64_t base = p.row * (int64_t)hidden;
+  const int64_t lbase = p.lrow * (int64_t)hidden;
+  auto index = [&](int v) { return BLOCKED ? p.lt * NV + v : vec_index(v, tpr, p.lt); };
+
+  Pack<S, VEC> xv[NV], rv[NV], wv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int64_t lj = (int64_t)load_index(index(v), nvec) * VEC;
+    xv[v] = ld_nt<S, VEC>(x + lbase + lj);
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(res + lbase + lj);
+    wv[v] = ld<S, VEC>(w + lj);
+  }
+
+  float a[NV][VEC];
+  double ss = 0.0;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int j = index(v);
+    const bool in = j < nvec;
+    double vs = 0.0;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float t = E::to_f(xv[v].v[e]);
+      if constexpr (RES) t += E::to_f(rv[v].v[e]);
+      a[v][e] = t;
+      const double d = (double)t;
+      vs = __builtin_fma(d, d, vs);
+    }
+    ss += in ? vs : 0.0;
+    if constexpr (RES) {
+      if (p.live && in) {
+        Pack<S, VEC> o;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(a[v][e]);
+        st_nt<S, VEC>(res + base + (int64_t)j * VEC, o);
+      }
+    }
+  }
+  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+
+  // Groups are whole (hidden % group == 0), so a group's lanes are all inside the row or all
+  // past its end; the latter compute on copies and store nothing.
+  float m[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    m[v] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float y = rnd<E>(rnd<E>(a[v][e] * rho) * E::to_f(wv[v].v[e]));
+      a[v][e] = y;
+      m[v] = __builtin_fmaxf(m[v], __builtin_fabsf(y));
+    }
+  }
+  if constexpr (BLOCKED) {
+    float mm = m[0];
+#pragma unroll
+    for (int v = 1; v < NV; ++v) mm = __builtin_fmaxf(mm, m[v]);
+    mm = group_max(mm, group / NV);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) m[v] = mm;
+  } else {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) m[v] = group_max(m[v], group / VEC);
+  }
+
+  const float ub = scale_ub != nullptr ? *scale_ub : 0.0f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int j = index(v);
+    if (!(p.live && j < nvec)) continue;
+    const float A = scale_ub != nullptr ? __builtin_fminf(m[v], ub) : m[v];
+    const float s = FP8 ? __builtin_fmaxf(mcop_div_rn(A, 448.0f), 1.0f / 229376.0f)
+                        : __builtin_fmaxf(mcop_div_rn(A, 127.0f), FLT_EPSILON);
+    const int g = (int)(((int64_t)j * VEC) / group);
+    if ((((int64_t)j * VEC) % group) == 0) {
+      scales[p.row * scale_row_stride + (int64_t)g * scale_group_stride] = s;
+    }
+    const float inv = mcop_div_rn(1.0f, s);
+    Pack<uint8_t, VEC> q;
+    if constexpr (FP8) {
+      const bool bounded = A == m[v] && s <= 0x1p100f;
+      q = fp8_quotient_codes<VEC>(a[v], s, inv, mcop_divisor_ok(s), bounded);
+    } else if constexpr (std::is_same_v<E, F32>) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(a[v][e] * inv);
+    } else {
+      // |y * inv| <= 127 * (1 + 2^-22) < 127.5 (int8 takes no scale bound)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) q.v[e] = q_i8_in_range(a[v][e], inv);
+    }
+    st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
+  }
+}
+
+template <class E, int VEC, bool FP8, bool RES>
+static const void* kernel_of(int nv) {
+  if constexpr (VEC == 1) {
+    return nv == 4 ? reinterpret_cast<const void*>(&k_rms_norm_group_quant<E, 1, 4, FP8, RES>)
+                   : reinterpret_cast<const void*>(&k_rms_norm_group_quant<E, 1, 16, FP8, RES>);
+  } else {
+    switch (nv) {
+      case 1: return reinterpret_cast<const void*>(&k_rms_norm_group_quant<E, VEC, 1, FP8, RES>);
+      case 2: return reinterpret_cast<const void*>(&k_rms_norm_group_quant<E, VEC, 2, FP8, RES>);
+      case 4: return reinterpret_cast<const void*>(&k_rms_norm_group_quant<E, VEC, 4, FP8, RES>);
+      case 8: return reinterpret_cast<const void*>(&k_rms_norm_group_quant<E, VEC, 8, FP8, RES>);
+      default: return reinterpret_cast<const void*>(&k_rms_norm_group_quant<E, VEC, 16, FP8, RES>);
+    }
+  }
+}
+
+struct GqArgs {
+  void* out;
+  float* scales;
+  const void* x;
+  const void* w;
+  const float* scale_ub;
+  void* res;
+  int64_t rows;
+  int hidden;
+  float eps;
+  int group;
+  int64_t srow;
+  int64_t sgrp;
+};
+
+template <class E, int VEC, bool FP8, bool RES>
+static void launch_nv(const Geometry& g, const GqArgs& a, hipStream_t st) {
+  using S = typename E::S;
+  const dim3 grid((unsigned)g.blocks), block((unsigned)(g.tpr * g.rpb));
+  auto* o = static_cast<uint8_t*>(a.out);
+  auto* xp = static_cast<const S*>(a.x);
+  auto* wp = static_cast<const S*>(a.w);
+  auto* rp = static_cast<S*>(a.res);
+#define MCOP_LAUNCH(NVV)                                                                        \
+  hipLaunchKernelGGL((k_rms_norm_group_quant<E, VEC, NVV, FP8, RES>), grid, block, 0, st, o,    \
+                     a.scales, xp, wp, a.scale_ub, rp, a.rows, a.hidden, g.tpr, a.eps, a.group, \
+                     a.srow, a.sgrp)
+  if constexpr (VEC == 1) {
+    if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
+  } else {
+    switch (g.nv) {
+      case 1: MCOP_LAUNCH(1); break;
+      case 2: MCOP_LAUNCH(2); break;
+      case 4: MCOP_LAUNCH(4); break;
+      case 8: MCOP_LAUNCH(8); break;
+      default: MCOP_LAUNCH(16); break;
+    }
+  }
+#undef MCOP_LAUNCH
+}
+
+template <class E, bool FP8>
+static int dispatch(const GqArgs& a, hipStream_t st) {
+  const char* name = "rms_norm_per_block_quant";
+  constexpr int V = E::VEC;
+  const bool vec_ok = a.hidden % V == 0 && aligned(16, a.x, a.w, a.res) && aligned(V, a.out);
+  const KernelOfNv kernels =
+      vec_ok ? (a.res ? &kernel_of<E, V, FP8, true> : &kernel_of<E, V, FP8, false>)
+             : (a.res ? &kernel_of<E, 1, FP8, true> : &kernel_of<E, 1, FP8, false>);
+  Geometry g;
+  if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? V : 1, kernels, &g)) {
+    return set_error(MCOP_E_UNSUPPORTED,
+                     "%s: hidden_size %d is larger than the register-resident kernels support",
+                     name, a.hidden);
+  }
+  if (g.vec == 1) {
+    if (a.res) launch_nv<E, 1, FP8, true>(g, a, st);
+    else launch_nv<E, 1, FP8, false>(g, a, st);
+  } else {
+    if (a.res) launch_nv<E, V, FP8, true>(g, a, st);
+    else launch_nv<E, V, FP8, false>(g, a, st);
+  }
+  return check_launch(name);
+}
+
+}  // namespace mcop
+
+extern "C" int mcop_rms_norm_per_block_quant(void* out, mcop_dtype out_dtype, float* scales,
+                                             const void* input, const void* weight,
+                                             const float* scale_ub, void* residual,
+                                             int64_t num_tokens, int64_t hidden_size,
+                                             mcop_dtype in_dtype, float epsilon,
+                                             int64_t group_size, int is_scale_transposed,
+                                             void* stream) {
+  using namespace mcop;
+  const char* name = "rms_norm_per_block_quant";
+  if (num_tokens < 0 || hidden_size <= 0 || hidden_size > INT32_MAX) {
+    return set_error(MCOP_E_INVALID, "%s: bad shape num_tokens=%lld hidden_size=%lld", name,
+                     (long long)num_tokens, (long long)hidden_size);
+  }
+  if (group_size != 64 && group_size != 128) {
+    return set_error(MCOP_E_INVALID, "%s: unsupported group size %lld (64 or 128)", name,
+                     (long long)group_size);
+  }
+  if (hidden_size % group_size != 0) {
+    return set_error(MCOP_E_INVALID, "%s: hidden_size %lld is not a multiple of group_size %lld",
+                     name, (long long)hidden_size, (long long)group_size);
+  }
+  if (num_tokens == 0) return MCOP_OK;
+  if (!out || !scales || !input || !weight) {
+    return set_error(MCOP_E_INVALID, "%s: null pointer", name);
+  }
+  if (out_dtype != MCOP_I8 && out_dtype != MCOP_FP8_E4M3FN) {
+    return set_error(MCOP_E_INVALID, "%s: out dtype %d is not int8 or fp8_e4m3fn", name,
+                     (int)out_dtype);
+  }
+  const int64_t groups = hidden_size / group_size;
+  const GqArgs a{out, scales, input, weight, scale_ub, residual, num_tokens, (int)hidden_size,
+                 epsilon, (int)group_size, is_scale_transposed ? 1 : groups,
+                 is_scale_transposed ? num_tokens : 1};
+  const bool fp8 = out_dtype == MCOP_FP8_E4M3FN;
+  auto st = static_cast<hipStream_t>(stream);
+  switch (in_dtype) {
+    case MCOP_BF16: return fp8 ? dispatch<BF16, true>(a, st) : dispatch<BF16, false>(a, st);
+    case MCOP_F16: return fp8 ? dispatch<F16, true>(a, st) : dispatch<F16, false>(a, st);
+    case MCOP_F32: return fp8 ? dispatch<F32, true>(a, st) : dispatch<F32, false>(a, st);
+    default:
+      return set_error(MCOP_E_INVALID, "%s: input dtype %d is not bf16/fp16/fp32", name,
+                       (int)in_dtype);
+  }
+}

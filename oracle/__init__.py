@@ -47,6 +47,7 @@ def _load() -> ctypes.CDLL:
     lib.oracle_dynamic_scaled_int8_azp_quant.argtypes = [P, P, P, P, I64, I64, I]
     lib.oracle_dynamic_per_token_fp8_quant.argtypes = [P, P, P, P, I64, I64, I64, I64, I]
     lib.oracle_add_rms_norm_quant_padded.argtypes = [P, I64, P, P, P, P, P, P, I64, I64, F]
+    lib.oracle_rms_norm_per_block_quant.argtypes = [P, I, P, P, P, P, P, I64, I64, I, F, I64, I]
     for name in ("oracle_f32_to_bf16_array", "oracle_f32_to_f16_array",
                  "oracle_f32_to_e4m3fn_array"):
         getattr(lib, name).argtypes = [P, P, I64]
@@ -55,7 +56,8 @@ def _load() -> ctypes.CDLL:
                  "oracle_fp8_e4m3fn_from_f32", "oracle_f32_to_bf16_array",
                  "oracle_f32_to_f16_array", "oracle_f32_to_e4m3fn_array", "oracle_set_threads",
                  "oracle_dynamic_scaled_int8_quant", "oracle_dynamic_scaled_int8_azp_quant",
-                 "oracle_dynamic_per_token_fp8_quant", "oracle_add_rms_norm_quant_padded"):
+                 "oracle_dynamic_per_token_fp8_quant", "oracle_add_rms_norm_quant_padded",
+                 "oracle_rms_norm_per_block_quant"):
         getattr(lib, name).restype = None
     lib.oracle_set_threads.argtypes = [I]
     lib.oracle_num_threads.restype = I
@@ -127,6 +129,31 @@ def rms_norm_dynamic_per_token_quant(
     lib().oracle_rms_norm_quant(out.data_ptr(), _DT[quant_dtype], scales.data_ptr(),
                                 xc.data_ptr(), w.data_ptr(), ub, _ptr(ro), T, H, _DT[x.dtype],
                                 float(eps))
+    return out, scales, ro
+
+
+def rms_norm_per_block_quant(
+        x: torch.Tensor, weight: torch.Tensor, eps: float, quant_dtype: torch.dtype,
+        group_size: int, scale_ub: Optional[float] = None,
+        residual: Optional[torch.Tensor] = None, is_scale_transposed: bool = False
+) -> tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """vLLM ``_C::rms_norm_per_block_quant``
+    (op/vllm/quantization/fused_kernels/fused_layernorm_dynamic_per_token_quant.cu:92-126,
+    194-270; layernorm_utils.cuh:223-393, 455-535).
+
+    Returns (codes, scales [T, H/G] or [H/G, T] fp32, new residual or None)."""
+    xc, w = _cpu(x), _cpu(weight)
+    T, H = _rows(xc)
+    assert H % group_size == 0
+    NG = H // group_size
+    out = torch.empty(xc.shape, dtype=quant_dtype)
+    scales = torch.empty((NG, T) if is_scale_transposed else (T, NG), dtype=torch.float32)
+    ro = None if residual is None else _cpu(residual).clone()
+    ub = None if scale_ub is None else ctypes.byref(ctypes.c_float(float(scale_ub)))
+    lib().oracle_rms_norm_per_block_quant(out.data_ptr(), _DT[quant_dtype], scales.data_ptr(),
+                                          xc.data_ptr(), w.data_ptr(), ub, _ptr(ro), T, H,
+                                          _DT[x.dtype], float(eps), int(group_size),
+                                          1 if is_scale_transposed else 0)
     return out, scales, ro
 
 
@@ -265,7 +292,7 @@ __all__ = [
     "build", "set_threads", "num_threads", "fused_add_rms_norm",
     "rms_norm_dynamic_per_token_quant", "rms_norm_smooth_quant", "scale_dynamic_quant",
     "dynamic_scaled_int8_quant", "dynamic_per_token_scaled_fp8_quant",
-    "add_rms_norm_quant_padded", "fp8_e4m3fn_from_f32", "f32_to_bf16_bits", "f32_to_f16_bits", "f32_to_e4m3fn_bits",
+    "add_rms_norm_quant_padded", "rms_norm_per_block_quant", "fp8_e4m3fn_from_f32", "f32_to_bf16_bits", "f32_to_f16_bits", "f32_to_e4m3fn_bits",
 ]
 
 if os.environ.get("MCOP_ORACLE_THREADS"):

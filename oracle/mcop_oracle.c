@@ -226,6 +226,55 @@ void oracle_rms_norm_quant(void* out, int out_dt, float* scales, const void* x, 
   }
 }
 
+/* vLLM rms_norm_per_block_quant,
+   op/vllm/quantization/fused_kernels/fused_layernorm_dynamic_per_token_quant.cu:92-126,194-270
+   with vectorized::compute_rms (layernorm_utils.cuh:223-279), the group branch of
+   compute_dynamic_per_token_scales (:283-360) and norm_and_quant (:455-535):
+     a, r <- b(a), rho and y = b(b(a*rho) * w) as in oracle_rms_norm_quant;
+     per group g of G elements: A_g = max|y| (min with ub);
+     int8: s_g = max(A_g/127, FLT_EPSILON), q = sat[-128,127](rne(y * (1/s_g)));
+     fp8:  s_g = max(A_g/448, 1/(448*512)), q = e4m3fn(clamp(y/s_g, +-448));
+     scales[t*(H/G) + g], or scales[g*T + t] when `transposed`. */
+void oracle_rms_norm_per_block_quant(void* out, int out_dt, float* scales, const void* x,
+                                     const void* w, const float* scale_ub, void* r, int64_t T,
+                                     int64_t H, int dt, float eps, int64_t G, int transposed) {
+  const int64_t NG = H / G;
+#pragma omp parallel
+  {
+    float* a = (float*)malloc((size_t)H * sizeof(float));
+#pragma omp for schedule(static)
+    for (int64_t t = 0; t < T; ++t) {
+      acc64 A = {0.0, 0.0};
+      for (int64_t i = 0; i < H; ++i) {
+        float v = load_el(x, dt, t * H + i);
+        if (r) v += load_el(r, dt, t * H + i);
+        a[i] = v;
+        acc_add(&A, (double)v * (double)v);
+      }
+      if (r) for (int64_t i = 0; i < H; ++i) store_el(r, dt, t * H + i, a[i]);
+      const float rho = inv_rms(acc_val(&A), H, eps);
+      for (int64_t i = 0; i < H; ++i) a[i] = rnd_el(rnd_el(a[i] * rho, dt) * load_el(w, dt, i), dt);
+      for (int64_t g = 0; g < NG; ++g) {
+        float amax = 0.0f;
+        for (int64_t i = g * G; i < (g + 1) * G; ++i) amax = fmaxf(amax, fabsf(a[i]));
+        if (scale_ub) amax = fminf(amax, *scale_ub);
+        const float s = out_dt == DT_I8 ? fmaxf(amax / 127.0f, FLT_EPSILON)
+                                        : fmaxf(amax / 448.0f, 1.0f / (448.0f * 512.0f));
+        scales[transposed ? g * T + t : t * NG + g] = s;
+        if (out_dt == DT_I8) {
+          const float inv = 1.0f / s;
+          for (int64_t i = g * G; i < (g + 1) * G; ++i)
+            ((int8_t*)out)[t * H + i] = q_int8(a[i] * inv, -128);
+        } else {
+          for (int64_t i = g * G; i < (g + 1) * G; ++i)
+            ((uint8_t*)out)[t * H + i] = q_fp8(a[i] / s);
+        }
+      }
+    }
+    free(a);
+  }
+}
+
 /* ---------------------------------------------------------------- H4 */
 
 /* mcoplib rms_norm_dynamic_per_token_quant (fused_rms_norm_dq), op/fused_rms_norm_dq.cu:260-303
