@@ -135,6 +135,42 @@ int mcop_dynamic_per_token_scaled_fp8_quant(uint8_t* out, float* scales, const v
                                             int64_t output_row_stride, mcop_dtype in_dtype,
                                             void* stream);
 
+/* (Residual add +) RMSNorm without quantization (mcoplib.op.rms_norm):
+ *   a = x (+ residual, read only); after_res <- b(a) when a residual is given;
+ *   out <- b((a * d) * w), d = rms_div ? RN(1/rho) : rho   (the reference's vectorized kernel,
+ *   taken when H is a multiple of n and H <= 3072*n, n = 4 if the input or the weight is fp32,
+ *   else 8); otherwise its element-wise chain: out <- b((a~ / rho) * w) (rms_div) or
+ *   b((a~ * rho) * w), a~ = b(a) with a residual, x without.  rho = 1/sqrt(sum(a^2)/H + eps).
+ * input, out, residual, after_res: [T,H] contiguous in_dtype; weight [H] in_dtype or fp32.
+ * Replaces rms_norm(), op/fused_rms_norm_dq.cu:980-998 (dispatch :814-978, kernels :305-420;
+ * pybind op/pybind.cpp:44). */
+int mcop_rms_norm(void* out, const void* input, const void* weight, mcop_dtype weight_dtype,
+                  void* after_res, const void* residual, int64_t num_tokens, int64_t hidden_size,
+                  mcop_dtype in_dtype, float epsilon, int rms_div, void* stream);
+
+/* Per-head RMSNorm of heads [head_offset, head_offset + head_norm) of every token
+ * (mcoplib.op.head_rms_norm): input / out [T, num_heads, head_size] contiguous, weight
+ * [num_heads, head_size] (bf16 or fp32; row h normalizes head h); other heads of out are not
+ * written.  out <- b((x * RN(1/rho)) * w) for the reference's vectorized sizes (as for
+ * mcop_rms_norm), else b((x / rho) * w).
+ * Replaces head_rms_norm(), op/fused_rms_norm_dq.cu:804-812 (dispatch :669-802, kernels
+ * :493-578; pybind op/pybind.cpp:43). */
+int mcop_head_rms_norm(void* out, const void* input, const void* weight, mcop_dtype weight_dtype,
+                       int64_t num_tokens, int64_t num_heads, int64_t head_size,
+                       int64_t head_offset, int64_t head_norm, mcop_dtype in_dtype,
+                       float epsilon, void* stream);
+
+/* vLLM `_C::rms_norm`: out[r] <- b(b(x_r * rho) * w) for the num_tokens rows of a 2-D, 3-D or
+ * 4-D input addressed with the given strides (as the reference kernel's arguments:
+ * input.stride(-2), -3, -4 and input.size(-2), -3); out [num_tokens, H] contiguous; weight
+ * [H] in the input dtype.
+ * Replaces rms_norm(), op/vllm/layernorm_kernels.cu:186-231 (kernel :15-86; schema
+ * op/vllm/torch_bindings.cpp:155-158). */
+int mcop_vllm_rms_norm(void* out, const void* input, const void* weight, int64_t num_tokens,
+                       int64_t hidden_size, int num_dims, int64_t input_stride_d2,
+                       int64_t input_stride_d3, int64_t input_stride_d4, int64_t input_shape_d2,
+                       int64_t input_shape_d3, mcop_dtype dtype, float epsilon, void* stream);
+
 /* (Residual add +) RMSNorm + dynamic per-group quantization (vLLM `_C::rms_norm_per_block_quant`):
  * as mcop_rms_norm_dynamic_per_token_quant, but with one scale per group of group_size (64 or
  * 128) consecutive elements of a row: A_g = max|y| over the group (min with *scale_ub, fp8

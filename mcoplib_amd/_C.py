@@ -1,7 +1,7 @@
 """``torch.ops._C`` surface (the vLLM operator library that mcoplib builds as ``mcoplib._C``).
 
 Importing this module registers, in the ``_C`` torch.library namespace, the schemas of
-op/vllm/torch_bindings.cpp:161-164 (``fused_add_rms_norm``), :216-221
+op/vllm/torch_bindings.cpp:155-158 (``rms_norm``), :161-164 (``fused_add_rms_norm``), :216-221
 (``rms_norm_dynamic_per_token_quant``), :224-229 (``rms_norm_per_block_quant``), :359-364
 (``dynamic_per_token_scaled_fp8_quant``) and :374-379 (``dynamic_scaled_int8_quant``) with
 implementations for the CUDA (HIP) dispatch key that call libmcop_norm.so.  If another library (vLLM's own ``_C``) already defined a schema, only the
@@ -21,6 +21,7 @@ from ._checks import (contiguous_check, dispatch_check, numel_check, on_cuda, ro
 from .op import _norm_quant
 
 SCHEMAS = {
+    "rms_norm": "rms_norm(Tensor! result, Tensor input, Tensor weight, float epsilon) -> ()",
     "fused_add_rms_norm":
         "fused_add_rms_norm(Tensor! input, Tensor! residual, Tensor weight, float epsilon) -> ()",
     "rms_norm_dynamic_per_token_quant":
@@ -37,6 +38,33 @@ SCHEMAS = {
         "dynamic_per_token_scaled_fp8_quant(Tensor! result, Tensor input, Tensor! scale, "
         "Tensor? scale_ub) -> ()",
 }
+
+
+def rms_norm(result: torch.Tensor, input: torch.Tensor, weight: torch.Tensor,
+             epsilon: float) -> None:
+    """result <- RMSNorm(input) * weight for every row of a 2-D, 3-D or 4-D input whose rows may
+    be strided (reference host function op/vllm/layernorm_kernels.cu:186-231)."""
+    name = "rms_norm"
+    torch_check(result.is_contiguous(), "out.is_contiguous()")
+    if input.stride(-1) != 1:
+        input = input.contiguous()
+    torch_check(weight.is_contiguous(), "weight.is_contiguous()")
+    dispatch_check(input.dtype, "rms_norm_kernel")
+    if input.dim() not in (2, 3, 4):
+        raise RuntimeError(f"Expects rank 2, 3 or 4 tensors but got {input.dim()}")
+    if weight.dtype != input.dtype or result.dtype != input.dtype:
+        raise RuntimeError(f"{name}: result, input and weight must share one dtype")
+    on_cuda(name, result, input, weight)
+    T, H = rows_of(input)
+    numel_check(name, "result", result, T * H)
+    numel_check(name, "weight", weight, H)
+    nd = input.dim()
+    with _lib.device_of(input):
+        _lib.check(_lib.lib.mcop_vllm_rms_norm(
+            result.data_ptr(), input.data_ptr(), weight.data_ptr(), T, H, nd, input.stride(-2),
+            input.stride(-3) if nd >= 3 else 0, input.stride(-4) if nd >= 4 else 0,
+            input.size(-2) if nd >= 3 else 0, input.size(-3) if nd >= 4 else 0,
+            _lib.DTYPE_CODE[input.dtype], float(epsilon), _lib.stream_of(input)))
 
 
 def fused_add_rms_norm(input: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
@@ -208,6 +236,7 @@ def dynamic_per_token_scaled_fp8_quant(result: torch.Tensor, input: torch.Tensor
 
 
 _IMPLS = {
+    "rms_norm": rms_norm,
     "fused_add_rms_norm": fused_add_rms_norm,
     "rms_norm_dynamic_per_token_quant": rms_norm_dynamic_per_token_quant,
     "dynamic_scaled_int8_quant": dynamic_scaled_int8_quant,

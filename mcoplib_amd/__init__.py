@@ -4,10 +4,11 @@ per-token quantization path.
 Surfaces (same names, argument order and in-place conventions as the reference):
   mcoplib_amd.op          -- mcoplib.op: rms_norm_dynamic_per_token_quant (fused_rms_norm_dq),
                              rms_norm_dynamic_per_token_quant_custom, scale_dynamic_quant,
-                             fused_add_rms_norm_dynamic_per_token_quant_padding_output
+                             fused_add_rms_norm_dynamic_per_token_quant_padding_output,
+                             rms_norm, head_rms_norm
   mcoplib_amd.custom_ops  -- mcoplib.custom_ops.rms_norm_dynamic_per_token_quant and
                              fused_add_rms_norm_dynamic_per_token_quant_padding_output
-  mcoplib_amd._C          -- registers torch.ops._C.fused_add_rms_norm,
+  mcoplib_amd._C          -- registers torch.ops._C.rms_norm, torch.ops._C.fused_add_rms_norm,
                              torch.ops._C.rms_norm_dynamic_per_token_quant,
                              torch.ops._C.rms_norm_per_block_quant,
                              torch.ops._C.dynamic_scaled_int8_quant and

@@ -1,0 +1,253 @@
+// norm_kernel.h -- the RMSNorm row kernel without quantization and its dispatch, shared by the
+// translation units that instantiate it per input dtype (rms_norm*.hip).
+//
+// One kernel serves three reference operators whose rounding chains differ (b() = round to the
+// input dtype, a = x [+ r] in fp32, rho = 1/sqrt(sum(a^2)/H + eps), fp64 row sum here):
+//   NORM_VLLM  vLLM _C::rms_norm (op/vllm/layernorm_kernels.cu:15-86):
+//              y = b(b(x * rho) * w)
+//   NORM_MC    mcoplib.op.rms_norm / head_rms_norm, their vectorized kernels
+//              (op/fused_rms_norm_dq.cu:305-382, 493-557):
+//              y = b((a * d) * w), d = rms_div ? RN(1/rho) : rho, a unrounded
+//   NORM_MC_GENERIC  the same operators' element-wise kernels (:389-420, 559-578 with
+//              compute_rms :69-99, norm_without_smooth :189-209, do_head_norm :212-224), which
+//              the reference runs when the row is not a whole number of its vectors or longer
+//              than three vectors per thread of a 1024-thread block:
+//              y = b((a~ / rho) * w) if rms_div else b((a~ * rho) * w), a~ = b(a) with a
+//              residual (it re-reads after_res), the input otherwise
+// With a residual (mcoplib.op.rms_norm only) after_res <- b(a); the residual is not updated.
+//
+// Rows are addressed through a three-level index so that one kernel covers contiguous rows,
+// vLLM's 3-D / 4-D strided inputs and head_rms_norm's selected heads with per-head weights:
+//   row r = (i0 * n1 + i1) * n2 + i2;  input row at i0*s0 + i1*s1 + i2*s2, output row at
+//   i0*o0 + i1*o1 + i2*o2, weight at i2*w2; residual and after_res rows at r * H.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "../../include/mcop_norm.h"
+#include "rowkern.h"
+
+namespace mcop {
+
+enum NormMode { NORM_VLLM = 0, NORM_MC = 1, NORM_MC_GENERIC = 2 };
+
+struct RowMap {
+  int64_t n1, n2;      // extents of the two inner indices (1 when unused)
+  int64_t s0, s1, s2;  // input element strides
+  int64_t o0, o1, o2;  // output element strides
+  int64_t w2;          // weight element stride per inner index (0: one weight row)
+};
+
+struct RowOffsets {
+  int64_t in, out, w;
+};
+
+__device__ __forceinline__ RowOffsets row_offsets(const RowMap& m, int64_t r) {
+  int64_t i0 = r, i1 = 0, i2 = 0;
+  if (m.n2 != 1) {
+    i2 = r % m.n2;
+    i0 = r / m.n2;
+  }
+  if (m.n1 != 1) {
+    i1 = i0 % m.n1;
+    i0 = i0 / m.n1;
+  }
+  return {i0 * m.s0 + i1 * m.s1 + i2 * m.s2, i0 * m.o0 + i1 * m.o1 + i2 * m.o2, i2 * m.w2};
+}
+
+template <class EW, int VEC>
+struct NormW {
+  Pack<typename EW::S, VEC> p;
+  __device__ __forceinline__ float at(int e) const { return EW::to_f(p.v[e]); }
+};
+
+template <class E, class EW, int VEC, int NV, bool RES>
+__global__ void __launch_bounds__(max_tpr(VEC, NV))
+k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
+           const typename E::S* __restrict__ x, const typename EW::S* __restrict__ w,
+           const typename E::S* __restrict__ res, RowMap map, int64_t rows, int hidden, int tpr,
+           float eps, int mode, int rms_div) {
+  using S = typename E::S;
+  __shared__ double red_sum[16];
+  const RowPos p = row_pos(rows, tpr);
+  const int nvec = hidden / VEC;
+  const RowOffsets lo = row_offsets(map, p.lrow);
+  const int64_t out_base = p.row == p.lrow ? lo.out : 0;
+  const int64_t rbase = p.row * (int64_t)hidden;
+  const int64_t lrbase = p.lrow * (int64_t)hidden;
+
+  Pack<S, VEC> xv[NV], rv[NV];
+  NormW<EW, VEC> wv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
+    xv[v] = ld_nt<S, VEC>(x + lo.in + lj);
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(res + lrbase + lj);
+    wv[v].p = ld<typename EW::S, VEC>(w + lo.w + lj);
+  }
+
+  float a[NV][VEC];
+  double ss = 0.0;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int j = vec_index(v, tpr, p.lt);
+    const bool in = j < nvec;
+    double vs = 0.0;  // lanes past the row end (a copy of vector 0) do not count
+    Pack<S, VEC> o;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float t = E::to_f(xv[v].v[e]);
+      if constexpr (RES) t += E::to_f(rv[v].v[e]);
+      const double d = (double)t;
+      vs = __builtin_fma(d, d, vs);
+      if constexpr (RES) {
+        o.v[e] = E::from_f(t);
+        // the element-wise kernels re-read the rounded after_res
+        if (mode == NORM_MC_GENERIC) t = E::to_f(o.v[e]);
+      }
+      a[v][e] = t;
+    }
+    ss += in ? vs : 0.0;
+    if constexpr (RES) {
+      if (p.live && in) st_nt<S, VEC>(ares + rbase + (int64_t)j * VEC, o);
+    }
+  }
+  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+  const float inv_rho = mcop_div_rn(1.0f, rho);
+
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int j = vec_index(v, tpr, p.lt);
+    if (!(p.live && j < nvec)) continue;
+    Pack<S, VEC> o;
+    if (mode == NORM_VLLM) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(rnd<E>(a[v][e] * rho) * wv[v].at(e));
+    } else if (mode == NORM_MC || !rms_div) {
+      const float d = (mode == NORM_MC && rms_div) ? inv_rho : rho;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f((a[v][e] * d) * wv[v].at(e));
+    } else {
+      float n[VEC];
+      div_by_const<VEC>(n, a[v], rho, inv_rho, mcop_divisor_ok(rho));
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(n[e] * wv[v].at(e));
+    }
+    st_nt<S, VEC>(out + out_base + (int64_t)j * VEC, o);
+  }
+}
+
+struct NormArgs {
+  void* out;
+  void* ares;
+  const void* x;
+  const void* w;
+  const void* res;
+  RowMap map;
+  int64_t rows;
+  int hidden;
+  float eps;
+  int mode;
+  int rms_div;
+};
+
+template <class E, class EW, int VEC, bool RES>
+static void norm_launch_nv(const Geometry& g, const NormArgs& a, hipStream_t st) {
+  using S = typename E::S;
+  const dim3 grid((unsigned)g.blocks), block((unsigned)(g.tpr * g.rpb));
+  auto* o = static_cast<S*>(a.out);
+  auto* arp = static_cast<S*>(a.ares);
+  auto* xp = static_cast<const S*>(a.x);
+  auto* wp = static_cast<const typename EW::S*>(a.w);
+  auto* rp = static_cast<const S*>(a.res);
+#define MCOP_LAUNCH(NVV)                                                                       \
+  hipLaunchKernelGGL((k_rms_norm<E, EW, VEC, NVV, RES>), grid, block, 0, st, o, arp, xp, wp, rp, \
+                     a.map, a.rows, a.hidden, g.tpr, a.eps, a.mode, a.rms_div)
+  if constexpr (VEC == 1) {
+    if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
+  } else {
+    switch (g.nv) {
+      case 1: MCOP_LAUNCH(1); break;
+      case 2: MCOP_LAUNCH(2); break;
+      case 4: MCOP_LAUNCH(4); break;
+      case 8: MCOP_LAUNCH(8); break;
+      default: MCOP_LAUNCH(16); break;
+    }
+  }
+#undef MCOP_LAUNCH
+}
+
+template <class E, class EW, int VEC, bool RES>
+static const void* norm_kernel_of(int nv) {
+  if constexpr (VEC == 1) {
+    return nv == 4 ? reinterpret_cast<const void*>(&k_rms_norm<E, EW, 1, 4, RES>)
+                   : reinterpret_cast<const void*>(&k_rms_norm<E, EW, 1, 16, RES>);
+  } else {
+    switch (nv) {
+      case 1: return reinterpret_cast<const void*>(&k_rms_norm<E, EW, VEC, 1, RES>);
+      case 2: return reinterpret_cast<const void*>(&k_rms_norm<E, EW, VEC, 2, RES>);
+      case 4: return reinterpret_cast<const void*>(&k_rms_norm<E, EW, VEC, 4, RES>);
+      case 8: return reinterpret_cast<const void*>(&k_rms_norm<E, EW, VEC, 8, RES>);
+      default: return reinterpret_cast<const void*>(&k_rms_norm<E, EW, VEC, 16, RES>);
+    }
+  }
+}
+
+// Vectors are usable when every row start and the weight rows stay 16-byte aligned.
+template <class E, class EW>
+static bool norm_vec_ok(const NormArgs& a) {
+  constexpr int V = E::VEC;
+  constexpr int WB = (int)sizeof(typename EW::S) * V;
+  const RowMap& m = a.map;
+  const bool strides = m.s0 % V == 0 && m.s1 % V == 0 && m.s2 % V == 0 && m.o0 % V == 0 &&
+                       m.o1 % V == 0 && m.o2 % V == 0 && m.w2 % V == 0;
+  return a.hidden % V == 0 && strides && aligned(16, a.x, a.out, a.res, a.ares) &&
+         aligned(WB, a.w);
+}
+
+template <class E, class EW>
+static int norm_dispatch(const char* name, const NormArgs& a, hipStream_t st) {
+  constexpr int V = E::VEC;
+  const bool vec_ok = norm_vec_ok<E, EW>(a);
+  const bool r = a.res != nullptr;
+  const KernelOfNv kernels =
+      vec_ok ? (r ? &norm_kernel_of<E, EW, V, true> : &norm_kernel_of<E, EW, V, false>)
+             : (r ? &norm_kernel_of<E, EW, 1, true> : &norm_kernel_of<E, EW, 1, false>);
+  Geometry g;
+  if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? V : 1, kernels, &g)) {
+    return set_error(MCOP_E_UNSUPPORTED,
+                     "%s: hidden_size %d is larger than the register-resident kernels support",
+                     name, a.hidden);
+  }
+  if (g.vec == 1) {
+    if (r) norm_launch_nv<E, EW, 1, true>(g, a, st);
+    else norm_launch_nv<E, EW, 1, false>(g, a, st);
+  } else {
+    if (r) norm_launch_nv<E, EW, V, true>(g, a, st);
+    else norm_launch_nv<E, EW, V, false>(g, a, st);
+  }
+  return check_launch(name);
+}
+
+// Weight dtype: the input dtype, fp32 or (head_rms_norm) bf16.
+template <class E>
+int norm_dispatch_w(const char* name, const NormArgs& a, mcop_dtype wdt, hipStream_t st) {
+  switch (wdt) {
+    case MCOP_F32: return norm_dispatch<E, F32>(name, a, st);
+    case MCOP_BF16: return norm_dispatch<E, BF16>(name, a, st);
+    case MCOP_F16:
+      if constexpr (std::is_same_v<E, F16>) return norm_dispatch<E, F16>(name, a, st);
+      [[fallthrough]];
+    default:
+      return set_error(MCOP_E_INVALID, "%s: weight dtype %d is not supported for this input",
+                       name, (int)wdt);
+  }
+}
+
+int norm_dispatch_bf16(const char* name, const NormArgs& a, mcop_dtype wdt, hipStream_t st);
+int norm_dispatch_f16(const char* name, const NormArgs& a, mcop_dtype wdt, hipStream_t st);
+
+}  // namespace mcop

@@ -1,7 +1,7 @@
 """``mcoplib.op`` surface of the fused norm/quant path, backed by libmcop_norm.so (gfx950).
 
-Functions keep the reference pybind signatures (op/pybind.cpp:42, 51, 54, 55; declarations in
-include/fused_rms_norm_dq.h:3-12, include/rms_norm_dynamic_per_token_quant.h:2-8,
+Functions keep the reference pybind signatures (op/pybind.cpp:42-44, 51, 54, 55; declarations
+in include/fused_rms_norm_dq.h:3-24, include/rms_norm_dynamic_per_token_quant.h:2-8,
 include/scale_dynamic_quant.h:6-10,
 include/fused_add_layernorm_per_token_quant_padding_output.h:3-11), their positional argument
 order, in-place outputs and error behaviour.  Every call enqueues one kernel on torch's current
@@ -23,6 +23,8 @@ __all__ = [
     "rms_norm_dynamic_per_token_quant_custom",
     "scale_dynamic_quant",
     "fused_add_rms_norm_dynamic_per_token_quant_padding_output",
+    "rms_norm",
+    "head_rms_norm",
 ]
 
 
@@ -196,3 +198,76 @@ def fused_add_rms_norm_dynamic_per_token_quant_padding_output(
             output.data_ptr(), output_rms.data_ptr(), output_quant_int8.data_ptr(),
             out_scales.data_ptr(), input.data_ptr(), residual.data_ptr(), weight.data_ptr(),
             T, H, pad, float(epsilon), _lib.stream_of(input)))
+
+
+def rms_norm(out: torch.Tensor, input: torch.Tensor, weight: torch.Tensor, var_epsilon: float,
+             after_res: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None,
+             rms_div: bool = True) -> None:
+    """(Residual add +) RMSNorm (reference entry op/fused_rms_norm_dq.cu:980-998).
+
+    out <- (input [+ residual]) / rsqrt(mean(.^2) + eps) * weight when ``rms_div`` (the
+    reference's convention, which its own test asserts), or * rsqrt(...) * weight otherwise;
+    with a residual, after_res <- input + residual (the residual itself is not updated).
+    weight is the input dtype or fp32."""
+    name = "rms_norm"
+    torch_check(out.is_contiguous() and input.is_contiguous(),
+                "out.is_contiguous() && input.is_contiguous()")
+    torch_check(weight.is_contiguous(), "weight.is_contiguous()")
+    dispatch_check(input.dtype, "rms_norm_per_token_dispatch")
+    on_cuda(name, out, input, weight, after_res, residual)
+    T, H = rows_of(input)
+    if out.dtype != input.dtype:
+        raise RuntimeError(f"{name}: out must have the input dtype {input.dtype}")
+    if weight.dtype not in (input.dtype, torch.float32):
+        raise RuntimeError(f"{name}: weight must be {input.dtype} or float32, got {weight.dtype}")
+    numel_check(name, "out", out, T * H)
+    numel_check(name, "weight", weight, H)
+    if residual is not None:
+        if after_res is None:
+            raise RuntimeError(f"{name}: a residual needs an after_res output")
+        for what, t in (("residual", residual), ("after_res", after_res)):
+            if t.dtype != input.dtype:
+                raise RuntimeError(f"{name}: {what} must have the input dtype {input.dtype}")
+            contiguous_check(name, what, t)
+            numel_check(name, what, t, T * H)
+    with _lib.device_of(input):
+        _lib.check(_lib.lib.mcop_rms_norm(
+            out.data_ptr(), input.data_ptr(), weight.data_ptr(), _lib.DTYPE_CODE[weight.dtype],
+            None if residual is None else after_res.data_ptr(),
+            None if residual is None else residual.data_ptr(), T, H,
+            _lib.DTYPE_CODE[input.dtype], float(var_epsilon), 1 if rms_div else 0,
+            _lib.stream_of(input)))
+
+
+def head_rms_norm(out: torch.Tensor, hidden_states: torch.Tensor, weight: torch.Tensor,
+                  var_epsilon: float, head_offset: int, head_norm: int) -> None:
+    """Per-head RMSNorm of heads [head_offset, head_offset + head_norm) of
+    hidden_states [num_tokens, num_heads, head_size] with per-head weights
+    [num_heads, head_size] (bf16 or fp32); out (same shape) is written for those heads only
+    (reference entry op/fused_rms_norm_dq.cu:804-812).  The reference's convention:
+    x / rsqrt(mean(x^2) + eps) * weight."""
+    name = "head_rms_norm"
+    torch_check(out.is_contiguous() and weight.is_contiguous() and hidden_states.is_contiguous(),
+                "out.is_contiguous() && weight.is_contiguous() && hidden_states.is_contiguous()")
+    dispatch_check(hidden_states.dtype, "head_rms_norm_dispatch")
+    on_cuda(name, out, hidden_states, weight)
+    if hidden_states.dim() != 3:
+        raise RuntimeError(f"{name}: hidden_states must be [num_tokens, num_heads, head_size]")
+    T, NH, D = hidden_states.shape
+    if out.shape != hidden_states.shape or out.dtype != hidden_states.dtype:
+        raise RuntimeError(f"{name}: out must match hidden_states in shape and dtype")
+    if weight.dtype not in (torch.bfloat16, torch.float32):
+        raise RuntimeError(f"{name}: weight must be bfloat16 or float32, got {weight.dtype}")
+    head_offset, head_norm = int(head_offset), int(head_norm)
+    if head_offset < 0 or head_norm < 0 or head_offset + head_norm > NH:
+        raise RuntimeError(f"{name}: heads [{head_offset}, {head_offset + head_norm}) are not "
+                           f"inside the {NH} heads")
+    if weight.numel() < (head_offset + head_norm) * D:
+        raise RuntimeError(f"{name}: weight holds {weight.numel()} elements, needs "
+                           f"{(head_offset + head_norm) * D}")
+    with _lib.device_of(hidden_states):
+        _lib.check(_lib.lib.mcop_head_rms_norm(
+            out.data_ptr(), hidden_states.data_ptr(), weight.data_ptr(),
+            _lib.DTYPE_CODE[weight.dtype], T, NH, D, head_offset, head_norm,
+            _lib.DTYPE_CODE[hidden_states.dtype], float(var_epsilon),
+            _lib.stream_of(hidden_states)))

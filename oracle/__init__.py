@@ -48,6 +48,9 @@ def _load() -> ctypes.CDLL:
     lib.oracle_dynamic_per_token_fp8_quant.argtypes = [P, P, P, P, I64, I64, I64, I64, I]
     lib.oracle_add_rms_norm_quant_padded.argtypes = [P, I64, P, P, P, P, P, P, I64, I64, F]
     lib.oracle_rms_norm_per_block_quant.argtypes = [P, I, P, P, P, P, P, I64, I64, I, F, I64, I]
+    lib.oracle_rms_norm.argtypes = [P, P, P, I, P, P, I64, I64, I, F, I]
+    lib.oracle_head_rms_norm.argtypes = [P, P, P, I, I64, I64, I64, I64, I64, I, F]
+    lib.oracle_vllm_rms_norm.argtypes = [P, P, P, I64, I64, I, F]
     for name in ("oracle_f32_to_bf16_array", "oracle_f32_to_f16_array",
                  "oracle_f32_to_e4m3fn_array"):
         getattr(lib, name).argtypes = [P, P, I64]
@@ -57,7 +60,8 @@ def _load() -> ctypes.CDLL:
                  "oracle_f32_to_f16_array", "oracle_f32_to_e4m3fn_array", "oracle_set_threads",
                  "oracle_dynamic_scaled_int8_quant", "oracle_dynamic_scaled_int8_azp_quant",
                  "oracle_dynamic_per_token_fp8_quant", "oracle_add_rms_norm_quant_padded",
-                 "oracle_rms_norm_per_block_quant"):
+                 "oracle_rms_norm_per_block_quant", "oracle_rms_norm", "oracle_head_rms_norm",
+                 "oracle_vllm_rms_norm"):
         getattr(lib, name).restype = None
     lib.oracle_set_threads.argtypes = [I]
     lib.oracle_num_threads.restype = I
@@ -238,6 +242,45 @@ def dynamic_per_token_scaled_fp8_quant(x: torch.Tensor, scale_ub: Optional[float
     return out, scales
 
 
+# ------------------------------------------------------------------------------------ norms
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+             residual: Optional[torch.Tensor] = None, rms_div: bool = True
+             ) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """mcoplib ``op.rms_norm`` (op/fused_rms_norm_dq.cu:305-420, 814-998).
+
+    Returns (out, after_res or None)."""
+    xc, w = _cpu(x), _cpu(weight)
+    T, H = _rows(xc)
+    out = torch.empty_like(xc)
+    r = None if residual is None else _cpu(residual)
+    ares = None if residual is None else torch.empty_like(xc)
+    lib().oracle_rms_norm(out.data_ptr(), xc.data_ptr(), w.data_ptr(), _DT[w.dtype], _ptr(ares),
+                          _ptr(r), T, H, _DT[x.dtype], float(eps), 1 if rms_div else 0)
+    return out, ares
+
+
+def head_rms_norm(out: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, eps: float,
+                  head_offset: int, head_norm: int) -> torch.Tensor:
+    """mcoplib ``op.head_rms_norm`` (op/fused_rms_norm_dq.cu:493-578, 669-812): returns a copy
+    of ``out`` with heads [head_offset, head_offset + head_norm) of x [T, NH, D] normalized."""
+    o, xc, w = _cpu(out).clone(), _cpu(x), _cpu(weight)
+    T, NH, D = xc.shape
+    lib().oracle_head_rms_norm(o.data_ptr(), xc.data_ptr(), w.data_ptr(), _DT[w.dtype], T, NH, D,
+                               int(head_offset), int(head_norm), _DT[x.dtype], float(eps))
+    return o
+
+
+def vllm_rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """vLLM ``_C::rms_norm`` (op/vllm/layernorm_kernels.cu:15-86, 186-231); x of any rank, its
+    rows are normalized in order.  Returns out [T, H] (contiguous, shaped like x)."""
+    xc, w = _cpu(x), _cpu(weight)
+    T, H = _rows(xc)
+    out = torch.empty_like(xc)
+    lib().oracle_vllm_rms_norm(out.data_ptr(), xc.data_ptr(), w.data_ptr(), T, H, _DT[x.dtype],
+                               float(eps))
+    return out
+
+
 # ------------------------------------------------------------------------------------ padded
 def add_rms_norm_quant_padded(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
                               pad_size: int, eps: float, fill: int = 0):
@@ -292,7 +335,8 @@ __all__ = [
     "build", "set_threads", "num_threads", "fused_add_rms_norm",
     "rms_norm_dynamic_per_token_quant", "rms_norm_smooth_quant", "scale_dynamic_quant",
     "dynamic_scaled_int8_quant", "dynamic_per_token_scaled_fp8_quant",
-    "add_rms_norm_quant_padded", "rms_norm_per_block_quant", "fp8_e4m3fn_from_f32", "f32_to_bf16_bits", "f32_to_f16_bits", "f32_to_e4m3fn_bits",
+    "add_rms_norm_quant_padded", "rms_norm_per_block_quant", "rms_norm", "head_rms_norm",
+    "vllm_rms_norm", "fp8_e4m3fn_from_f32", "f32_to_bf16_bits", "f32_to_f16_bits", "f32_to_e4m3fn_bits",
 ]
 
 if os.environ.get("MCOP_ORACLE_THREADS"):

@@ -444,6 +444,103 @@ void oracle_dynamic_per_token_fp8_quant(uint8_t* out, float* scales, const void*
   }
 }
 
+/* ---------------------------------------------------------------- RMSNorm without quant */
+
+/* The reference's choice between its vectorized and element-wise mcoplib norm kernels
+   (op/fused_rms_norm_dq.cu:669-802, 814-978): vectors of n elements, n = 4 when the input or
+   the weight is fp32 (float4 of fp32, or float2 of 16-bit values against fp32 weights), else 8;
+   vectorized when H is a multiple of n and at most three vectors per thread of 1024 threads. */
+static int mc_vectorized(int64_t H, int dt, int wdt) {
+  const int64_t n = (dt == DT_F32 || wdt == DT_F32) ? 4 : 8;
+  return H % n == 0 && H <= 3 * 1024 * n;
+}
+
+/* One mcoplib norm row: vectorized kernel (rms_norm_kernel_align :305-382,
+   head_rms_norm_kernel_align :493-557): y = b((a * d) * w), d = rms_div ? (float)(1.0 / rho)
+   : rho, a unrounded; element-wise kernels (norm_without_smooth :189-209, do_head_norm
+   :212-224): y = b((a~ / rho) * w) or b((a~ * rho) * w), a~ the after_res value re-read. */
+static void mc_norm_row(void* out, int64_t oo, const float* a, const void* w, int wdt,
+                        int64_t wo, int64_t H, int dt, float rho, int rms_div, int vec) {
+  if (vec) {
+    const float d = rms_div ? (float)(1.0 / (double)rho) : rho;
+    for (int64_t i = 0; i < H; ++i) store_el(out, dt, oo + i, (a[i] * d) * load_el(w, wdt, wo + i));
+  } else {
+    for (int64_t i = 0; i < H; ++i) {
+      const float n = rms_div ? a[i] / rho : a[i] * rho;
+      store_el(out, dt, oo + i, n * load_el(w, wdt, wo + i));
+    }
+  }
+}
+
+/* mcoplib.op.rms_norm, op/fused_rms_norm_dq.cu:980-998 (dispatch :814-978, kernels :305-420,
+   compute_rms :69-99): a = x (+ r); after_res <- b(a) with a residual (r is not updated);
+   rho = 1/sqrt(S/H + eps); out row as mc_norm_row. */
+void oracle_rms_norm(void* out, const void* x, const void* w, int wdt, void* after_res,
+                     const void* r, int64_t T, int64_t H, int dt, float eps, int rms_div) {
+  const int vec = mc_vectorized(H, dt, wdt);
+#pragma omp parallel
+  {
+    float* a = (float*)malloc((size_t)H * sizeof(float));
+#pragma omp for schedule(static)
+    for (int64_t t = 0; t < T; ++t) {
+      acc64 S = {0.0, 0.0};
+      for (int64_t i = 0; i < H; ++i) {
+        float v = load_el(x, dt, t * H + i);
+        if (r) v += load_el(r, dt, t * H + i);
+        acc_add(&S, (double)v * (double)v);
+        if (r) {
+          store_el(after_res, dt, t * H + i, v);
+          if (!vec) v = rnd_el(v, dt);
+        }
+        a[i] = v;
+      }
+      mc_norm_row(out, t * H, a, w, wdt, 0, H, dt, inv_rms(acc_val(&S), H, eps), rms_div, vec);
+    }
+    free(a);
+  }
+}
+
+/* mcoplib.op.head_rms_norm, op/fused_rms_norm_dq.cu:804-812 (dispatch :669-802, kernels
+   :493-578): for every token t and head h in [off, off + hn) of x [T, NH, D], the row
+   x[t, h, :] is normalized with weight row w[h, :] (rms_div always set); other heads of out
+   are not written. */
+void oracle_head_rms_norm(void* out, const void* x, const void* w, int wdt, int64_t T,
+                          int64_t NH, int64_t D, int64_t off, int64_t hn, int dt, float eps) {
+  const int vec = mc_vectorized(D, dt, wdt);
+#pragma omp parallel
+  {
+    float* a = (float*)malloc((size_t)D * sizeof(float));
+#pragma omp for schedule(static)
+    for (int64_t k = 0; k < T * hn; ++k) {
+      const int64_t t = k / hn, h = off + k % hn, ro = (t * NH + h) * D;
+      acc64 S = {0.0, 0.0};
+      for (int64_t i = 0; i < D; ++i) {
+        a[i] = load_el(x, dt, ro + i);
+        acc_add(&S, (double)a[i] * (double)a[i]);
+      }
+      mc_norm_row(out, ro, a, w, wdt, h * D, D, dt, inv_rms(acc_val(&S), D, eps), 1, vec);
+    }
+    free(a);
+  }
+}
+
+/* vLLM _C::rms_norm, op/vllm/layernorm_kernels.cu:15-86 (host :186-231), on contiguous rows:
+   rho from S = sum x^2; y = b(b(x * rho) * w) (the 16-bit product rounds to 16 bits, :82). */
+void oracle_vllm_rms_norm(void* out, const void* x, const void* w, int64_t T, int64_t H, int dt,
+                          float eps) {
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < T; ++t) {
+    acc64 S = {0.0, 0.0};
+    for (int64_t i = 0; i < H; ++i) {
+      const double v = load_el(x, dt, t * H + i);
+      acc_add(&S, v * v);
+    }
+    const float rho = inv_rms(acc_val(&S), H, eps);
+    for (int64_t i = 0; i < H; ++i)
+      store_el(out, dt, t * H + i, rnd_el(load_el(x, dt, t * H + i) * rho, dt) * load_el(w, dt, i));
+  }
+}
+
 /* ---------------------------------------------------------------- padded wire format */
 
 /* mcoplib fused_add_rms_norm_dynamic_per_token_quant_padding_output,
