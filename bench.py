@@ -32,6 +32,7 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "HBM GB/s & % of peak: fused add-RMSNorm+per-token int8 quant, 8192x8192"
 PAD_SIZE = 3840  # padded workload: bf16 elements per padded row (2 * 3840 bytes)
 BLOCK_GROUP = 128  # block-fp8 workload: elements per scale group
+HEADS = 8  # head-norm workload: heads per token (all normalized, per-head weights)
 
 
 def parse():
@@ -42,7 +43,8 @@ def parse():
     ap.add_argument("--workload", default="cfg3",
                     choices=["cfg2", "cfg3", "cfg4", "cfg5-large", "cfg5-decode1",
                              "cfg5-decode4", "cfg5-decode16", "cfg5-decode64", "ptq-int8",
-                             "ptq-int8-azp", "ptq-fp8", "padded", "block-fp8"])
+                             "ptq-int8-azp", "ptq-fp8", "padded", "block-fp8", "norm-res",
+                             "vllm-norm", "head-norm"])
     ap.add_argument("--sets", type=int, default=0,
                     help="rotated input sets (default: enough for > 1 GiB, at least 3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -78,6 +80,12 @@ class Workload:
             return 10 * T * H + 8 * T + 2 * H
         if self.kind == "block_fp8":       # read x, r, w; write r, q, one scale per group
             return 7 * T * H + 2 * H + 4 * T * (H // BLOCK_GROUP)
+        if self.kind == "norm_res":        # read x, r, w; write out, after_res
+            return 8 * T * H + 2 * H
+        if self.kind == "vllm_norm":       # read x, w; write out
+            return 4 * T * H + 2 * H
+        if self.kind == "head_norm":       # T rows of HEADS heads: read x, per-head w; write out
+            return 4 * T * H + 2 * HEADS * H
         raise ValueError(self.kind)
 
     def make(self, torch, dev, seed):
@@ -90,7 +98,12 @@ class Workload:
         x = x.to(torch.bfloat16)
         w = (1 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
         d = {"x": x, "w": w}
-        if self.kind in ("add_norm_int8", "fused_add", "padded", "block_fp8"):
+        if self.kind == "head_norm":       # x [T/HEADS tokens, HEADS, H], per-head weights
+            d["x"] = x.view(T // HEADS, HEADS, H)
+            d["w"] = (1 + 0.1 * torch.randn(HEADS, H, generator=g, device=dev)).to(torch.bfloat16)
+        if self.kind in ("norm_res", "vllm_norm", "head_norm"):
+            d["out"] = torch.empty_like(d["x"])
+        if self.kind in ("add_norm_int8", "fused_add", "padded", "block_fp8", "norm_res"):
             d["r"] = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
         if self.kind == "add_norm_int8":
             d["q"] = torch.empty(T, H, dtype=torch.int8, device=dev)
@@ -125,6 +138,13 @@ class Workload:
                 d["q"], d["x"], d["w"], d["s"], self.eps, None, d["r"])
         if self.kind == "fused_add":
             return lambda: torch.ops._C.fused_add_rms_norm(d["x"], d["r"], d["w"], self.eps)
+        if self.kind == "norm_res":
+            d["ares"] = torch.empty_like(d["x"])
+            return lambda: op.rms_norm(d["out"], d["x"], d["w"], self.eps, d["ares"], d["r"], True)
+        if self.kind == "vllm_norm":
+            return lambda: torch.ops._C.rms_norm(d["out"], d["x"], d["w"], self.eps)
+        if self.kind == "head_norm":
+            return lambda: op.head_rms_norm(d["out"], d["x"], d["w"], self.eps, 0, HEADS)
         if self.kind == "block_fp8":
             return lambda: torch.ops._C.rms_norm_per_block_quant(
                 d["q"], d["x"], d["w"], d["s"], self.eps, None, d["r"], BLOCK_GROUP, False)
@@ -155,11 +175,17 @@ WORKLOADS = {
     "padded": Workload("padded", 8192, 7168, 1e-6, "padded"),
     # per-group (128) fp8 scales for block-scaled GEMMs, at the headline shape with residual
     "block-fp8": Workload("block-fp8", 8192, 8192, 1e-6, "block_fp8"),
+    # RMSNorms without quantization: mcoplib rms_norm with residual (after_res), vLLM rms_norm,
+    # and q/k head norm (T rows = tokens x heads of 128)
+    "norm-res": Workload("norm-res", 8192, 8192, 1e-6, "norm_res"),
+    "vllm-norm": Workload("vllm-norm", 8192, 8192, 1e-6, "vllm_norm"),
+    "head-norm": Workload("head-norm", 65536 * 8, 128, 1e-6, "head_norm"),
 }
 KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "fused_add": "k_fused_add_rms_norm",
                "smooth_fp8": "k_rms_norm_smooth_quant", "ptq_int8": "k_per_token_quant",
                "ptq_int8_azp": "k_per_token_quant", "ptq_fp8": "k_per_token_quant",
-               "padded": "k_add_rms_norm_quant_padded", "block_fp8": "k_rms_norm_group_quant"}
+               "padded": "k_add_rms_norm_quant_padded", "block_fp8": "k_rms_norm_group_quant",
+               "norm_res": "k_rms_norm", "vllm_norm": "k_rms_norm", "head_norm": "k_rms_norm"}
 
 
 # ------------------------------------------------------------------------------ pieces
@@ -193,6 +219,13 @@ def cpu_baseline(wl: Workload, seconds: float) -> dict:
             oracle.rms_norm_dynamic_per_token_quant(x, w, wl.eps, torch.int8, residual=r)
         elif wl.kind == "fused_add":
             oracle.fused_add_rms_norm(x, r, w, wl.eps)
+        elif wl.kind == "norm_res":
+            oracle.rms_norm(x, w, wl.eps, residual=r)
+        elif wl.kind == "vllm_norm":
+            oracle.vllm_rms_norm(x, w, wl.eps)
+        elif wl.kind == "head_norm":
+            xs = x.reshape(-1, HEADS, wl.H)
+            oracle.head_rms_norm(xs, xs, w.repeat(HEADS).view(HEADS, wl.H), wl.eps, 0, HEADS)
         elif wl.kind == "block_fp8":
             oracle.rms_norm_per_block_quant(x, w, wl.eps, torch.float8_e4m3fn, BLOCK_GROUP,
                                             residual=r)

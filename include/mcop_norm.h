@@ -222,7 +222,8 @@ int mcop_abi_version(void);
 
 /* Launch-shape override for the row kernels (no reference counterpart; used by the tuning sweep
  * and by the tests that check results do not depend on the launch shape).
- * vectors_per_lane in {0,1,2,4,8,16}, lanes_per_row in {0} or a multiple of 64 up to 1024;
+ * vectors_per_lane in {0,1,2,4,8,16}, lanes_per_row in {0, 16, 32} or a multiple of 64 up to
+ * 1024;
  * 0 restores the automatic choice. A request the row does not fit falls back to automatic.
  * Process-wide; not meant to be changed while other threads launch. */
 int mcop_set_launch_override(int vectors_per_lane, int lanes_per_row);

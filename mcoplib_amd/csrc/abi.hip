@@ -87,8 +87,9 @@ int blocks_per_cu(const void* kernel, int block) {
 }  // namespace
 
 // Launch shape of a row kernel.  A lane holds nv vectors of each streamed tensor, a row spans
-// tpr = nvec / nv lanes rounded up to whole waves, and rows narrower than 256 lanes are packed
-// several per workgroup.  Rules, from measurements on MI355X (bf16 rows of 4096-16384):
+// tpr = nvec / nv lanes rounded up to whole waves (or, for rows of at most 32 lanes, to 16 or
+// 32 lanes: several rows per wave), and rows narrower than 256 lanes are packed several per
+// workgroup.  Rules, from measurements on MI355X (bf16 rows of 4096-16384):
 //   - at most 256 rows (decode): row latency matters; the smallest nv >= 2 whose row fits
 //     (1 for rows of at most 64 vectors);
 //   - otherwise nv = 2 when its workgroups have at most 512 lanes and fill the CU (32 resident
@@ -97,8 +98,18 @@ int blocks_per_cu(const void* kernel, int block) {
 //     8-15% faster there); 8 or 16 only for rows that do not fit otherwise.  Kernels that spill
 //     registers are skipped while another shape fits.
 // Scalar path (hidden not a multiple of the vector width, or misaligned pointers): nv in {4,16}.
+// Lanes per row for n lanes of work: whole waves, or 16 / 32 lanes when the row is that short.
+static int64_t row_lanes(int64_t n, int min_tpr) {
+  if (n <= 32 && min_tpr <= 32) return n <= 16 && min_tpr <= 16 ? 16 : 32;
+  return round64(n);
+}
+
+static bool valid_tpr(int64_t t, int min_tpr) {
+  return (t >= min_tpr && (t == 16 || t == 32)) || (t > 0 && t % 64 == 0);
+}
+
 bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, KernelOfNv kernels,
-                     Geometry* g) {
+                     Geometry* g, int min_tpr) {
   const int64_t nvec = hidden / vec;
   int nv = 0;
   int64_t tpr = 0;
@@ -107,8 +118,8 @@ bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, Kern
   const bool nv_allowed = vec > 1 ? (onv == 1 || onv == 2 || onv == 4 || onv == 8 || onv == 16)
                                   : (onv == 4 || onv == 16);
   if (nv_allowed) {
-    const int64_t t = otpr > 0 ? otpr : round64(ceil_div(nvec, onv));
-    if (t % 64 == 0 && t <= max_tpr(vec, onv) && (int64_t)onv * t >= nvec) {
+    const int64_t t = otpr > 0 ? otpr : row_lanes(ceil_div(nvec, onv), min_tpr);
+    if (valid_tpr(t, min_tpr) && t <= max_tpr(vec, onv) && (int64_t)onv * t >= nvec) {
       nv = onv;
       tpr = t;
     }
@@ -123,7 +134,7 @@ bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, Kern
     int64_t fallback_tpr = 0;
     for (int c = 0; c < ncand && nv == 0; ++c) {
       const int cand = cands[c];
-      const int64_t t = round64(ceil_div(nvec, cand));
+      const int64_t t = row_lanes(ceil_div(nvec, cand), min_tpr);
       if (t > max_tpr(vec, cand)) continue;
       if (vec > 1 && cand == 1 && nvec > 64) continue;
       if (fallback_nv == 0) {
@@ -178,7 +189,7 @@ int mcop_abi_version(void) { return MCOP_ABI_VERSION; }
 
 int mcop_set_launch_override(int vectors_per_lane, int lanes_per_row) {
   if (vectors_per_lane < 0 || lanes_per_row < 0 || lanes_per_row > 1024 ||
-      lanes_per_row % 64 != 0) {
+      (lanes_per_row % 64 != 0 && lanes_per_row != 16 && lanes_per_row != 32)) {
     return mcop::set_error(MCOP_E_INVALID, "mcop_set_launch_override: bad shape (%d, %d)",
                            vectors_per_lane, lanes_per_row);
   }

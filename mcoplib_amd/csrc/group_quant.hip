@@ -207,7 +207,8 @@ static int dispatch(const GqArgs& a, hipStream_t st) {
       vec_ok ? (a.res ? &kernel_of<E, V, FP8, true> : &kernel_of<E, V, FP8, false>)
              : (a.res ? &kernel_of<E, 1, FP8, true> : &kernel_of<E, 1, FP8, false>);
   Geometry g;
-  if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? V : 1, kernels, &g)) {
+  // whole waves per row: a group's lanes must lie inside one row slice of the lane mapping
+  if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? V : 1, kernels, &g, 64)) {
     return set_error(MCOP_E_UNSUPPORTED,
                      "%s: hidden_size %d is larger than the register-resident kernels support",
                      name, a.hidden);

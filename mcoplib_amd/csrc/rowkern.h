@@ -254,6 +254,10 @@ __device__ __forceinline__ T wave_reduce(T v, Op op) {
 
 template <class T, class Op>
 __device__ __forceinline__ T row_reduce(T v, T* lds, int tpr, Op op) {
+  if (tpr < 64) {  // several rows per wave: butterfly within each row's aligned lane segment
+    for (int m = tpr >> 1; m >= 1; m >>= 1) v = op(v, __shfl_xor(v, m, 64));
+    return v;
+  }
   v = wave_reduce(v, op);
   if (tpr == 64) return v;  // the row is one wave
   const int wave = threadIdx.x >> 6;
@@ -276,8 +280,8 @@ struct RowPos {
   int lt;
   bool live;
 };
-// Workgroups hold several rows only when tpr is 64 or 128 (a power of two), so the row within
-// the workgroup is a shift (tpr is a kernel argument: the shift amount is scalar work).
+// Workgroups hold several rows only when tpr is 16, 32, 64 or 128 (a power of two), so the row
+// within the workgroup is a shift (tpr is a kernel argument: the shift amount is scalar work).
 __device__ __forceinline__ RowPos row_pos(int64_t num_rows, int tpr) {
   RowPos p;
   if ((int)blockDim.x == tpr) {
@@ -312,7 +316,7 @@ namespace mcop {
 struct Geometry {
   int vec;     // elements per vector (1 = scalar path)
   int nv;      // vectors per lane
-  int tpr;     // lanes per row (multiple of 64, <= 1024)
+  int tpr;     // lanes per row (16, 32 or a multiple of 64, <= 1024)
   int rpb;     // rows per workgroup
   int64_t blocks;
 };
@@ -321,9 +325,10 @@ struct Geometry {
 using KernelOfNv = const void* (*)(int nv);
 
 // Picks the launch shape of a row kernel. `vec` is 1 or the 16-byte vector width; returns false
-// when the row does not fit (hidden too large for the register-resident kernels).
+// when the row does not fit (hidden too large for the register-resident kernels).  Rows of at
+// most 32 lanes may take 16 or 32 lanes (several rows per wave) unless `min_tpr` is 64.
 bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, KernelOfNv kernels,
-                     Geometry* g);
+                     Geometry* g, int min_tpr = 16);
 
 // True when every non-null pointer is aligned to `bytes`.
 bool aligned(int bytes, const void* p0, const void* p1 = nullptr, const void* p2 = nullptr,
