@@ -29,10 +29,14 @@ k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
   Pack<S, VEC> xv[NV], rv[NV], wv[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
+    wv[v] = ld<S, VEC>(w + (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC);
+  }
+  shared_loads_first();
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
     const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
     xv[v] = ld_nt<S, VEC>(x + xlbase + lj);
     rv[v] = ld_nt<S, VEC>(res + rlbase + lj);
-    wv[v] = ld<S, VEC>(w + lj);
   }
 
   float z[NV][VEC];

@@ -82,10 +82,15 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
   NormW<EW, VEC> wv[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
+    wv[v].p = ld<typename EW::S, VEC>(
+        w + lo.w + (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC);
+  }
+  shared_loads_first();
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
     const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
     xv[v] = ld_nt<S, VEC>(x + lo.in + lj);
     if constexpr (RES) rv[v] = ld_nt<S, VEC>(res + lrbase + lj);
-    wv[v].p = ld<typename EW::S, VEC>(w + lo.w + lj);
   }
 
   float a[NV][VEC];

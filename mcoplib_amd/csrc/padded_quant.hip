@@ -46,10 +46,14 @@ k_add_rms_norm_quant_padded(uint8_t* __restrict__ padded, uint16_t* __restrict__
   Pack<uint16_t, VEC> xv[NV], rv[NV], wv[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
+    wv[v] = ld<uint16_t, VEC>(w + (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC);
+  }
+  shared_loads_first();
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
     const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
     xv[v] = ld_nt<uint16_t, VEC>(x + lbase + lj);
     rv[v] = ld_nt<uint16_t, VEC>(res + lbase + lj);
-    wv[v] = ld<uint16_t, VEC>(w + lj);
   }
 
   // a: opt keeps p = a * w (fp32); generic keeps b(a) (the residual value it re-reads)

@@ -44,10 +44,14 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   Pack<S, VEC> xv[NV], rv[NV], wv[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
+    wv[v] = ld<S, VEC>(w + (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC);
+  }
+  shared_loads_first();
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
     const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
     xv[v] = ld_nt<S, VEC>(x + lbase + lj);
     if constexpr (RES) rv[v] = ld_nt<S, VEC>(res + lbase + lj);
-    wv[v] = ld<S, VEC>(w + lj);
   }
 
   float a[NV][VEC];

@@ -28,9 +28,13 @@ k_scale_dynamic_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   Pack<float, VEC> sv[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
-    xv[v] = ld_nt<uint16_t, VEC>(x + lbase + lj);
-    sv[v] = ld<float, VEC>(sm + lj);
+    sv[v] = ld<float, VEC>(sm + (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC);
+  }
+  shared_loads_first();
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    xv[v] = ld_nt<uint16_t, VEC>(x + lbase +
+                                 (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC);
   }
 
   float a[NV][VEC];

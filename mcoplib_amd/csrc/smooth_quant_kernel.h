@@ -33,31 +33,29 @@ struct WVec {
   __device__ __forceinline__ float at(int e) const { return EW::to_f(p.v[e]); }
 };
 
+// One row (or, for tpr < blockDim, one of the workgroup's rows) given the lane's weight and
+// smooth vectors.
 template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES>
-__global__ void __launch_bounds__(max_tpr(VEC, NV))
-k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
-                        const typename E::S* __restrict__ x, const typename EW::S* __restrict__ w,
-                        const typename ES::S* __restrict__ sm, typename E::S* __restrict__ ares,
-                        typename E::S* __restrict__ anorm, const typename E::S* __restrict__ res,
-                        int64_t rows, int hidden, int tpr, float eps, uint32_t flags) {
+__device__ __forceinline__ void sq_row(const RowPos& p, const WVec<EW, VEC>* wv,
+                                       const WVec<ES, VEC>* sv, uint8_t* __restrict__ out,
+                                       float* __restrict__ scales,
+                                       const typename E::S* __restrict__ x,
+                                       typename E::S* __restrict__ ares,
+                                       typename E::S* __restrict__ anorm,
+                                       const typename E::S* __restrict__ res, int hidden, int tpr,
+                                       float eps, uint32_t flags, double* red_sum,
+                                       float* red_max) {
   using S = typename E::S;
-  __shared__ double red_sum[16];
-  __shared__ float red_max[16];
-  const RowPos p = row_pos(rows, tpr);
   const int nvec = hidden / VEC;
   const int64_t base = p.row * (int64_t)hidden;
   const int64_t lbase = p.lrow * (int64_t)hidden;
 
   Pack<S, VEC> xv[NV], rv[NV];
-  WVec<EW, VEC> wv[NV];
-  WVec<ES, VEC> sv[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
     xv[v] = ld_nt<S, VEC>(x + lbase + lj);
     if constexpr (RES) rv[v] = ld_nt<S, VEC>(res + lbase + lj);
-    wv[v].p = ld<typename EW::S, VEC>(w + lj);
-    sv[v].p = ld<typename ES::S, VEC>(sm + lj);
   }
 
   float a[NV][VEC];
@@ -134,6 +132,32 @@ k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   }
 }
 
+// The weight and smooth vectors (L2-resident, shared by every row) are requested before the
+// row's own streamed loads.
+template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES>
+__global__ void __launch_bounds__(max_tpr(VEC, NV))
+k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
+                        const typename E::S* __restrict__ x, const typename EW::S* __restrict__ w,
+                        const typename ES::S* __restrict__ sm, typename E::S* __restrict__ ares,
+                        typename E::S* __restrict__ anorm, const typename E::S* __restrict__ res,
+                        int64_t rows, int hidden, int tpr, float eps, uint32_t flags) {
+  __shared__ double red_sum[16];
+  __shared__ float red_max[16];
+  const int nvec = hidden / VEC;
+  WVec<EW, VEC> wv[NV];
+  WVec<ES, VEC> sv[NV];
+  const RowPos p = row_pos(rows, tpr);
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
+    wv[v].p = ld<typename EW::S, VEC>(w + lj);
+    sv[v].p = ld<typename ES::S, VEC>(sm + lj);
+  }
+  shared_loads_first();
+  sq_row<E, EW, ES, VEC, NV, FP8, RES>(p, wv, sv, out, scales, x, ares, anorm, res, hidden, tpr,
+                                        eps, flags, red_sum, red_max);
+}
+
 struct Args {
   void* out;
   float* scales;
@@ -160,10 +184,10 @@ static void launch_nv(const Geometry& g, const Args& a, hipStream_t st) {
   auto* arp = static_cast<S*>(a.ares);
   auto* anp = static_cast<S*>(a.anorm);
   auto* rp = static_cast<const S*>(a.res);
-#define MCOP_LAUNCH(NVV)                                                                     \
-  hipLaunchKernelGGL((k_rms_norm_smooth_quant<E, EW, ES, VEC, NVV, FP8, RES>), grid, block, 0, \
-                     st, o, a.scales, xp, wp, sp, arp, anp, rp, a.rows, a.hidden, g.tpr,       \
-                     a.eps, a.flags)
+#define MCOP_LAUNCH(NVV)                                                                        \
+  hipLaunchKernelGGL((k_rms_norm_smooth_quant<E, EW, ES, VEC, NVV, FP8, RES>), grid,      \
+                     block, 0, st, o, a.scales, xp, wp, sp, arp, anp, rp, a.rows, a.hidden,      \
+                     g.tpr, a.eps, a.flags)
   if constexpr (VEC == 1) {
     if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
   } else {

@@ -187,6 +187,18 @@ def test_config4_smooth_quant_fp8():
              False, False, 4)
 
 
+@pytest.mark.parametrize("dtype,wdt,sdt,qdt,with_res,standard", [
+    (torch.bfloat16, torch.bfloat16, torch.bfloat16, torch.int8, True, False),
+    (torch.float16, torch.float32, torch.float32, torch.float8_e4m3fn, False, True),
+    (torch.float32, torch.float32, torch.float32, torch.int8, True, True),
+])
+def test_h4_many_rows_row_loop(dtype, wdt, sdt, qdt, with_res, standard):
+    """Enough rows (> 4 per resident workgroup) for the row-walking launch of the smooth-quant
+    kernel, which keeps weight and smooth vectors in registers across rows."""
+    say(f"h4 row loop 8192x4096 {dtype} {qdt} res={with_res} std={standard}")
+    _h4_case(8192, 4096, dtype, wdt, sdt, qdt, with_res, standard, 21, x_scale=2.0)
+
+
 @pytest.mark.parametrize("T", [1, 4, 16, 64])
 def test_config5_decode(T):
     say(f"config 5 decode T={T}")
