@@ -92,10 +92,12 @@ int blocks_per_cu(const void* kernel, int block) {
 // workgroup.  Rules, from measurements on MI355X (bf16 rows of 4096-16384):
 //   - at most 256 rows (decode): row latency matters; the smallest nv >= 2 whose row fits
 //     (1 for rows of at most 64 vectors);
-//   - otherwise nv = 2 when its workgroups have at most 512 lanes and fill the CU (32 resident
-//     waves, from the kernel's occupancy); else nv = 4 (e.g. 7-wave workgroups leave a third of
-//     the wave slots empty, 16-wave ones reduce across too many waves: 4 vectors per lane was
-//     8-15% faster there); 8 or 16 only for rows that do not fit otherwise.  Kernels that spill
+//   - otherwise nv = 4 when the row fills a 4-wave workgroup with it (bf16 rows of >= 8192:
+//     fewer waves per row share the per-row work of the reductions and scale computations;
+//     2-35% faster than nv = 2, most for the kernels with the heaviest per-row work); else
+//     nv = 2 when its workgroups have at most 512 lanes and fill the CU (32 resident waves,
+//     from the kernel's occupancy); else nv = 4 (e.g. 7-wave workgroups leave a third of the
+//     wave slots empty); 8 or 16 only for rows that do not fit otherwise.  Kernels that spill
 //     registers are skipped while another shape fits.
 // Scalar path (hidden not a multiple of the vector width, or misaligned pointers): nv in {4,16}.
 // Lanes per row for n lanes of work: whole waves, or 16 / 32 lanes when the row is that short.
@@ -155,7 +157,11 @@ bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, Kern
                 cand, (long long)t, block, nb);
       }
       if (nb == 0) continue;  // spills (or cannot launch at this size)
-      if (vec > 1 && cand == 2 && (t > 512 || waves < 32)) continue;
+      // two vectors per lane only for rows that would not fill a 4-wave workgroup at four
+      if (vec > 1 && cand == 2 &&
+          (t > 512 || waves < 32 || row_lanes(ceil_div(nvec, 4), min_tpr) >= 256)) {
+        continue;
+      }
       nv = cand;
       tpr = t;
     }
