@@ -111,7 +111,7 @@ static bool valid_tpr(int64_t t, int min_tpr) {
 }
 
 bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, KernelOfNv kernels,
-                     Geometry* g, int min_tpr) {
+                     Geometry* g, int min_tpr, bool wide_nv4) {
   const int64_t nvec = hidden / vec;
   int nv = 0;
   int64_t tpr = 0;
@@ -159,7 +159,8 @@ bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, Kern
       if (nb == 0) continue;  // spills (or cannot launch at this size)
       // two vectors per lane only for rows that would not fill a 4-wave workgroup at four
       if (vec > 1 && cand == 2 &&
-          (t > 512 || waves < 32 || row_lanes(ceil_div(nvec, 4), min_tpr) >= 256)) {
+          (t > 512 || waves < 32 ||
+           (wide_nv4 && row_lanes(ceil_div(nvec, 4), min_tpr) >= 256))) {
         continue;
       }
       nv = cand;

@@ -340,8 +340,10 @@ using KernelOfNv = const void* (*)(int nv);
 // Picks the launch shape of a row kernel. `vec` is 1 or the 16-byte vector width; returns false
 // when the row does not fit (hidden too large for the register-resident kernels).  Rows of at
 // most 32 lanes may take 16 or 32 lanes (several rows per wave) unless `min_tpr` is 64.
+// `wide_nv4`: take four vectors per lane as soon as the row fills a 4-wave workgroup with them
+// (the default; the per-token norm-quant kernel measured faster at two for 8192-wide rows).
 bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, KernelOfNv kernels,
-                     Geometry* g, int min_tpr = 16);
+                     Geometry* g, int min_tpr = 16, bool wide_nv4 = true);
 
 // True when every non-null pointer is aligned to `bytes`.
 bool aligned(int bytes, const void* p0, const void* p1 = nullptr, const void* p2 = nullptr,
