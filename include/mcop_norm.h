@@ -135,6 +135,24 @@ int mcop_dynamic_per_token_scaled_fp8_quant(uint8_t* out, float* scales, const v
                                             int64_t output_row_stride, mcop_dtype in_dtype,
                                             void* stream);
 
+/* mcoplib's own (residual add +) RMSNorm + per-token int8 quantization
+ * (mcoplib.op.rms_norm_dynamic_per_token_quant_custom), int8 only, with the reference's two
+ * kernels' arithmetic:
+ *   H != 7168: as mcop_rms_norm_dynamic_per_token_quant with int8 out, except
+ *     s = max(A/127, 1.5e-6) and q = sat[-127,127](rne(y * (1/s)));
+ *   H == 7168: p = a * w in fp32 (no bf16 rounding), A = max|p|,
+ *     s = max((A * rho)/127, FLT_EPSILON), q = sat[-127,127](rne((p * rho) * (1/s)));
+ *     scale_ub is not used.
+ * residual (if given) <- b(input + residual).
+ * Replaces rms_norm_dynamic_per_token_quant_custom(), op/rms_norm_dynamic_per_token_quant.cu:
+ * 266-285 (kernels :52-92 with kernel/rms_norm_vllm.cuh:330-454, and :94-186; pybind
+ * op/pybind.cpp:55; Python wrapper mcoplib/custom_ops.py:29-45). */
+int mcop_rms_norm_dynamic_per_token_quant_custom(int8_t* out, float* scales, const void* input,
+                                                 const void* weight, const float* scale_ub,
+                                                 void* residual, int64_t num_tokens,
+                                                 int64_t hidden_size, mcop_dtype in_dtype,
+                                                 float epsilon, void* stream);
+
 /* (Residual add +) RMSNorm without quantization (mcoplib.op.rms_norm):
  *   a = x (+ residual, read only); after_res <- b(a) when a residual is given;
  *   out <- b((a * d) * w), d = rms_div ? RN(1/rho) : rho   (the reference's vectorized kernel,

@@ -48,6 +48,8 @@ def _load() -> ctypes.CDLL:
     lib.mcop_rms_norm.argtypes = [P, P, P, I, P, P, I64, I64, I, F, I, P]
     lib.mcop_head_rms_norm.argtypes = [P, P, P, I, I64, I64, I64, I64, I64, I, F, P]
     lib.mcop_vllm_rms_norm.argtypes = [P, P, P, I64, I64, I, I64, I64, I64, I64, I64, I, F, P]
+    lib.mcop_rms_norm_dynamic_per_token_quant_custom.argtypes = [P, P, P, P, P, P, I64, I64, I,
+                                                                  F, P]
     lib.mcop_set_launch_override.argtypes = [I, I]
     for fn in ("mcop_fused_add_rms_norm", "mcop_rms_norm_dynamic_per_token_quant",
                "mcop_rms_norm_smooth_quant", "mcop_scale_dynamic_quant",
@@ -55,7 +57,7 @@ def _load() -> ctypes.CDLL:
                "mcop_dynamic_scaled_int8_quant", "mcop_dynamic_per_token_scaled_fp8_quant",
                "mcop_fused_add_rms_norm_dynamic_per_token_quant_padding_output",
                "mcop_rms_norm_per_block_quant", "mcop_rms_norm", "mcop_head_rms_norm",
-               "mcop_vllm_rms_norm"):
+               "mcop_vllm_rms_norm", "mcop_rms_norm_dynamic_per_token_quant_custom"):
         getattr(lib, fn).restype = I
     lib.mcop_last_error.restype = ctypes.c_char_p
     lib.mcop_last_error.argtypes = []

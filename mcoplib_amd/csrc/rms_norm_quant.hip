@@ -12,6 +12,14 @@
 // (paths relative to op/vllm/quantization/fused_kernels/ and op/vllm/quantization/ of the
 // reference).
 //
+// mcoplib's own operator of the same name (rms_norm_dynamic_per_token_quant_custom,
+// op/rms_norm_dynamic_per_token_quant.cu:266-285) is int8 only and differs in two ways (MODE):
+//   QM_MC (any H but 7168; kernel/rms_norm_vllm.cuh:330-454): s = max(A/127, 1.5e-6) and
+//     q = sat[-127,127](rne(y * (1/s))) (float_to_int8_rn of kernel/utils.h:219-226);
+//   QM_MC_7168 (H == 7168; op/rms_norm_dynamic_per_token_quant.cu:94-186): no bf16 rounding
+//     between a and the code: p = a * w, A = max|p|, s = max((A * rho)/127, FLT_EPSILON),
+//     q = sat[-127,127](rne((p * rho) * (1/s))); scale_ub is not used.
+//
 // One pass: every lane loads all of its vectors of x, residual and weight before the first
 // reduction and keeps the row in VGPRs; the residual is written back from registers, the codes
 // are produced from registers, so HBM sees x and residual read once, residual and the codes
@@ -26,7 +34,9 @@
 
 namespace mcop {
 
-template <class E, int VEC, int NV, bool FP8, bool RES>
+enum QuantMode { QM_VLLM = 0, QM_MC = 1, QM_MC_7168 = 2 };
+
+template <class E, int VEC, int NV, bool FP8, bool RES, int MODE>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
 k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
                  const typename E::S* __restrict__ x, const typename E::S* __restrict__ w,
@@ -99,7 +109,10 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
     const bool in = full || vec_index(v, tpr, p.lt) < nvec;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const float y = rnd<E>(rnd<E>(a[v][e] * rho) * E::to_f(wv[v].v[e]));
+      // QM_MC_7168 keeps p = a * w unrounded (its code is rne((p * rho) * inv))
+      const float y = MODE == QM_MC_7168
+                          ? a[v][e] * E::to_f(wv[v].v[e])
+                          : rnd<E>(rnd<E>(a[v][e] * rho) * E::to_f(wv[v].v[e]));
       a[v][e] = y;
       amax = __builtin_fmaxf(amax, in ? __builtin_fabsf(y) : 0.0f);
     }
@@ -107,9 +120,15 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   amax = row_reduce(amax, red_max, tpr, MaxOp());
 
   float A = amax;
-  if (scale_ub != nullptr) A = __builtin_fminf(A, *scale_ub);
-  const float s = FP8 ? __builtin_fmaxf(mcop_div_rn(A, 448.0f), 1.0f / 229376.0f)
-                      : __builtin_fmaxf(mcop_div_rn(A, 127.0f), FLT_EPSILON);
+  if (MODE != QM_MC_7168 && scale_ub != nullptr) A = __builtin_fminf(A, *scale_ub);
+  float s;
+  if constexpr (FP8) {
+    s = __builtin_fmaxf(mcop_div_rn(A, 448.0f), 1.0f / 229376.0f);
+  } else if constexpr (MODE == QM_MC_7168) {
+    s = __builtin_fmaxf(mcop_div_rn(A * rho, 127.0f), FLT_EPSILON);
+  } else {
+    s = __builtin_fmaxf(mcop_div_rn(A, 127.0f), MODE == QM_MC ? 1.5e-6f : FLT_EPSILON);
+  }
   if (p.live && p.lt == 0) scales[p.row] = s;
   const float inv = mcop_div_rn(1.0f, s);
   const bool s_ok = mcop_divisor_ok(s);
@@ -120,23 +139,31 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
     const int j = vec_index(v, tpr, p.lt);
     if (p.live && j < nvec) {
       Pack<uint8_t, VEC> q;
+      constexpr int LO = MODE == QM_VLLM ? -128 : -127;
       if constexpr (FP8) {
         q = fp8_quotient_codes<VEC>(a[v], s, inv, s_ok, bounded);
-      } else if (std::is_same_v<E, F32> || scale_ub != nullptr) {
+      } else if (std::is_same_v<E, F32> || (MODE != QM_MC_7168 && scale_ub != nullptr)) {
         // fp32 inputs can carry NaN payloads in the low byte, and a scale bound lets |y * inv|
         // exceed 127: round, convert and saturate
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(a[v][e] * inv);
+        for (int e = 0; e < VEC; ++e) {
+          const float t = MODE == QM_MC_7168 ? a[v][e] * rho : a[v][e];
+          q.v[e] = q_i8<LO>(t * inv);
+        }
       } else {
+        // |t * inv| < 127.5: the code cannot saturate (nor reach -128)
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) q.v[e] = q_i8_in_range(a[v][e], inv);
+        for (int e = 0; e < VEC; ++e) {
+          const float t = MODE == QM_MC_7168 ? a[v][e] * rho : a[v][e];
+          q.v[e] = q_i8_in_range(t, inv);
+        }
       }
       st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
     }
   }
 }
 
-template <class E, int VEC, bool FP8, bool RES>
+template <class E, int VEC, bool FP8, bool RES, int MODE>
 static void launch_nv(const Geometry& g, void* out, float* scales, const void* x, const void* w,
                       const float* scale_ub, void* res, int64_t rows, int hidden, float eps,
                       hipStream_t st) {
@@ -147,7 +174,7 @@ static void launch_nv(const Geometry& g, void* out, float* scales, const void* x
   auto* wp = static_cast<const S*>(w);
   auto* rp = static_cast<S*>(res);
 #define MCOP_LAUNCH(NVV)                                                                   \
-  hipLaunchKernelGGL((k_rms_norm_quant<E, VEC, NVV, FP8, RES>), grid, block, 0, st, o,     \
+  hipLaunchKernelGGL((k_rms_norm_quant<E, VEC, NVV, FP8, RES, MODE>), grid, block, 0, st, o, \
                      scales, xp, wp, scale_ub, rp, rows, hidden, g.tpr, eps)
   if constexpr (VEC == 1) {
     if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
@@ -163,47 +190,59 @@ static void launch_nv(const Geometry& g, void* out, float* scales, const void* x
 #undef MCOP_LAUNCH
 }
 
-template <class E, int VEC, bool FP8, bool RES>
+template <class E, int VEC, bool FP8, bool RES, int MODE>
 static const void* kernel_of(int nv) {
   if constexpr (VEC == 1) {
-    return nv == 4 ? reinterpret_cast<const void*>(&k_rms_norm_quant<E, 1, 4, FP8, RES>)
-                   : reinterpret_cast<const void*>(&k_rms_norm_quant<E, 1, 16, FP8, RES>);
+    return nv == 4 ? reinterpret_cast<const void*>(&k_rms_norm_quant<E, 1, 4, FP8, RES, MODE>)
+                   : reinterpret_cast<const void*>(&k_rms_norm_quant<E, 1, 16, FP8, RES, MODE>);
   } else {
     switch (nv) {
-      case 1: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 1, FP8, RES>);
-      case 2: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 2, FP8, RES>);
-      case 4: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 4, FP8, RES>);
-      case 8: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 8, FP8, RES>);
-      default: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 16, FP8, RES>);
+      case 1: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 1, FP8, RES, MODE>);
+      case 2: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 2, FP8, RES, MODE>);
+      case 4: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 4, FP8, RES, MODE>);
+      case 8: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 8, FP8, RES, MODE>);
+      default: return reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, 16, FP8, RES, MODE>);
     }
   }
 }
 
-template <class E, bool FP8>
-static int dispatch(void* out, float* scales, const void* x, const void* w,
+template <class E, bool FP8, int MODE>
+static int dispatch(const char* name, void* out, float* scales, const void* x, const void* w,
                     const float* scale_ub, void* res, int64_t rows, int64_t hidden, float eps,
                     hipStream_t st) {
   constexpr int V = E::VEC;
   const bool vec_ok = hidden % V == 0 && aligned(16, x, w, res) && aligned(V, out);
-  const KernelOfNv kernels = vec_ok ? (res ? &kernel_of<E, V, FP8, true> : &kernel_of<E, V, FP8, false>)
-                                    : (res ? &kernel_of<E, 1, FP8, true> : &kernel_of<E, 1, FP8, false>);
+  const KernelOfNv kernels =
+      vec_ok ? (res ? &kernel_of<E, V, FP8, true, MODE> : &kernel_of<E, V, FP8, false, MODE>)
+             : (res ? &kernel_of<E, 1, FP8, true, MODE> : &kernel_of<E, 1, FP8, false, MODE>);
   Geometry g;
-  if (!choose_geometry("rms_norm_dynamic_per_token_quant", rows, hidden, vec_ok ? V : 1, kernels,
-                       &g, 16, /*wide_nv4=*/false)) {
+  if (!choose_geometry(name, rows, hidden, vec_ok ? V : 1, kernels, &g, 16,
+                       /*wide_nv4=*/false)) {
     return set_error(MCOP_E_UNSUPPORTED,
-                     "rms_norm_dynamic_per_token_quant: hidden_size %lld is larger than the "
-                     "register-resident kernels support",
-                     (long long)hidden);
+                     "%s: hidden_size %lld is larger than the register-resident kernels support",
+                     name, (long long)hidden);
   }
   const int h = (int)hidden;
   if (g.vec == 1) {
-    if (res) launch_nv<E, 1, FP8, true>(g, out, scales, x, w, scale_ub, res, rows, h, eps, st);
-    else launch_nv<E, 1, FP8, false>(g, out, scales, x, w, scale_ub, res, rows, h, eps, st);
+    if (res) launch_nv<E, 1, FP8, true, MODE>(g, out, scales, x, w, scale_ub, res, rows, h, eps, st);
+    else launch_nv<E, 1, FP8, false, MODE>(g, out, scales, x, w, scale_ub, res, rows, h, eps, st);
   } else {
-    if (res) launch_nv<E, V, FP8, true>(g, out, scales, x, w, scale_ub, res, rows, h, eps, st);
-    else launch_nv<E, V, FP8, false>(g, out, scales, x, w, scale_ub, res, rows, h, eps, st);
+    if (res) launch_nv<E, V, FP8, true, MODE>(g, out, scales, x, w, scale_ub, res, rows, h, eps, st);
+    else launch_nv<E, V, FP8, false, MODE>(g, out, scales, x, w, scale_ub, res, rows, h, eps, st);
   }
-  return check_launch("rms_norm_dynamic_per_token_quant");
+  return check_launch(name);
+}
+
+static int check_args(const char* name, const void* out, const float* scales, const void* input,
+                      const void* weight, int64_t num_tokens, int64_t hidden_size) {
+  if (num_tokens < 0 || hidden_size <= 0 || hidden_size > INT32_MAX) {
+    return set_error(MCOP_E_INVALID, "%s: bad shape num_tokens=%lld hidden_size=%lld", name,
+                     (long long)num_tokens, (long long)hidden_size);
+  }
+  if (num_tokens > 0 && (!out || !scales || !input || !weight)) {
+    return set_error(MCOP_E_INVALID, "%s: null pointer", name);
+  }
+  return MCOP_OK;
 }
 
 }  // namespace mcop
@@ -215,41 +254,55 @@ extern "C" int mcop_rms_norm_dynamic_per_token_quant(void* out, mcop_dtype out_d
                                                      int64_t hidden_size, mcop_dtype in_dtype,
                                                      float epsilon, void* stream) {
   using namespace mcop;
-  if (num_tokens < 0 || hidden_size <= 0 || hidden_size > INT32_MAX) {
-    return set_error(MCOP_E_INVALID,
-                     "rms_norm_dynamic_per_token_quant: bad shape num_tokens=%lld "
-                     "hidden_size=%lld",
-                     (long long)num_tokens, (long long)hidden_size);
-  }
+  const char* name = "rms_norm_dynamic_per_token_quant";
+  if (int rc = check_args(name, out, scales, input, weight, num_tokens, hidden_size)) return rc;
   if (num_tokens == 0) return MCOP_OK;
-  if (!out || !scales || !input || !weight) {
-    return set_error(MCOP_E_INVALID, "rms_norm_dynamic_per_token_quant: null pointer");
-  }
   if (out_dtype != MCOP_I8 && out_dtype != MCOP_FP8_E4M3FN) {
-    return set_error(MCOP_E_INVALID, "rms_norm_dynamic_per_token_quant: out dtype %d is not int8 "
-                     "or fp8_e4m3fn", (int)out_dtype);
+    return set_error(MCOP_E_INVALID, "%s: out dtype %d is not int8 or fp8_e4m3fn", name,
+                     (int)out_dtype);
   }
   const bool fp8 = out_dtype == MCOP_FP8_E4M3FN;
   auto st = static_cast<hipStream_t>(stream);
+#define MCOP_CASE(E)                                                                         \
+  return fp8 ? dispatch<E, true, QM_VLLM>(name, out, scales, input, weight, scale_ub,         \
+                                          residual, num_tokens, hidden_size, epsilon, st)     \
+             : dispatch<E, false, QM_VLLM>(name, out, scales, input, weight, scale_ub,        \
+                                           residual, num_tokens, hidden_size, epsilon, st)
   switch (in_dtype) {
-    case MCOP_BF16:
-      return fp8 ? dispatch<BF16, true>(out, scales, input, weight, scale_ub, residual,
-                                        num_tokens, hidden_size, epsilon, st)
-                 : dispatch<BF16, false>(out, scales, input, weight, scale_ub, residual,
-                                         num_tokens, hidden_size, epsilon, st);
-    case MCOP_F16:
-      return fp8 ? dispatch<F16, true>(out, scales, input, weight, scale_ub, residual,
-                                       num_tokens, hidden_size, epsilon, st)
-                 : dispatch<F16, false>(out, scales, input, weight, scale_ub, residual,
-                                        num_tokens, hidden_size, epsilon, st);
-    case MCOP_F32:
-      return fp8 ? dispatch<F32, true>(out, scales, input, weight, scale_ub, residual,
-                                       num_tokens, hidden_size, epsilon, st)
-                 : dispatch<F32, false>(out, scales, input, weight, scale_ub, residual,
-                                        num_tokens, hidden_size, epsilon, st);
+    case MCOP_BF16: MCOP_CASE(BF16);
+    case MCOP_F16: MCOP_CASE(F16);
+    case MCOP_F32: MCOP_CASE(F32);
     default:
-      return set_error(MCOP_E_INVALID,
-                       "rms_norm_dynamic_per_token_quant: input dtype %d is not bf16/fp16/fp32",
+      return set_error(MCOP_E_INVALID, "%s: input dtype %d is not bf16/fp16/fp32", name,
                        (int)in_dtype);
   }
+#undef MCOP_CASE
+}
+
+extern "C" int mcop_rms_norm_dynamic_per_token_quant_custom(
+    int8_t* out, float* scales, const void* input, const void* weight, const float* scale_ub,
+    void* residual, int64_t num_tokens, int64_t hidden_size, mcop_dtype in_dtype, float epsilon,
+    void* stream) {
+  using namespace mcop;
+  const char* name = "rms_norm_dynamic_per_token_quant_custom";
+  if (int rc = check_args(name, out, scales, input, weight, num_tokens, hidden_size)) return rc;
+  if (num_tokens == 0) return MCOP_OK;
+  auto st = static_cast<hipStream_t>(stream);
+  // the reference's dispatch: its fp32-chain kernel for H == 7168, the generic one otherwise
+  const bool h7168 = hidden_size == 7168;
+#define MCOP_CASE(E)                                                                         \
+  return h7168 ? dispatch<E, false, QM_MC_7168>(name, out, scales, input, weight, scale_ub,   \
+                                                residual, num_tokens, hidden_size, epsilon,   \
+                                                st)                                           \
+               : dispatch<E, false, QM_MC>(name, out, scales, input, weight, scale_ub,        \
+                                           residual, num_tokens, hidden_size, epsilon, st)
+  switch (in_dtype) {
+    case MCOP_BF16: MCOP_CASE(BF16);
+    case MCOP_F16: MCOP_CASE(F16);
+    case MCOP_F32: MCOP_CASE(F32);
+    default:
+      return set_error(MCOP_E_INVALID, "%s: input dtype %d is not bf16/fp16/fp32", name,
+                       (int)in_dtype);
+  }
+#undef MCOP_CASE
 }

@@ -86,22 +86,25 @@ def rms_norm_dynamic_per_token_quant_custom(out: torch.Tensor, input: torch.Tens
                                             var_epsilon: float,
                                             scale_ub: Optional[torch.Tensor] = None,
                                             residual: Optional[torch.Tensor] = None) -> None:
-    """(Residual add +) RMSNorm + dynamic per-token int8 quantization (reference entry
-    op/rms_norm_dynamic_per_token_quant.cu:266-285).  ``residual`` is updated in place to
-    input + residual; out and scales ([T] or [T, 1] fp32) are written."""
+    """(Residual add +) RMSNorm + dynamic per-token int8 quantization with mcoplib's own
+    arithmetic (reference entry op/rms_norm_dynamic_per_token_quant.cu:266-285): scale floor
+    1.5e-6 and codes in [-127, 127]; at H == 7168 the reference's fp32 chain (codes from
+    (x [+ r]) * w * rsqrt(...) without bf16 rounding, scale_ub unused).  ``residual`` is
+    updated in place to input + residual; out and scales ([T] or [T, 1] fp32) are written."""
     name = "rms_norm_dynamic_per_token_quant_custom"
     torch_check(out.dtype == torch.int8, "out.dtype() == torch::kInt8")
     torch_check(out.is_contiguous() and input.is_contiguous(),
                 "out.is_contiguous() && input.is_contiguous()")
     torch_check(scales.dtype == torch.float32, "scales.dtype() == torch::kFloat32")
     dispatch_check(input.dtype, " rms_norm_dynamic_per_token_quant_dispatch_")
-    _norm_quant(name, out, input, weight, scales, var_epsilon, scale_ub, residual)
+    _norm_quant(name, out, input, weight, scales, var_epsilon, scale_ub, residual, custom=True)
 
 
 def _norm_quant(name: str, out: torch.Tensor, input: torch.Tensor, weight: torch.Tensor,
                 scales: torch.Tensor, eps: float, scale_ub: Optional[torch.Tensor],
-                residual: Optional[torch.Tensor]) -> None:
-    """Shared launcher of the (residual add +) RMSNorm + per-token quant kernel."""
+                residual: Optional[torch.Tensor], custom: bool = False) -> None:
+    """Shared launcher of the (residual add +) RMSNorm + per-token quant kernel (vLLM's
+    arithmetic, or mcoplib's own with ``custom``)."""
     on_cuda(name, out, input, weight, scales, scale_ub, residual)
     T, H = rows_of(input)
     numel_check(name, "out", out, T * H)
@@ -119,12 +122,18 @@ def _norm_quant(name: str, out: torch.Tensor, input: torch.Tensor, weight: torch
     if scale_ub is not None:
         if scale_ub.dtype != torch.float32 or scale_ub.numel() < 1:
             raise RuntimeError(f"{name}: scale_ub must be a float32 tensor with one element")
+    ub = None if scale_ub is None else scale_ub.data_ptr()
+    rp = None if residual is None else residual.data_ptr()
     with _lib.device_of(input):
-        _lib.check(_lib.lib.mcop_rms_norm_dynamic_per_token_quant(
-            out.data_ptr(), _lib.DTYPE_CODE[out.dtype], scales.data_ptr(), input.data_ptr(),
-            weight.data_ptr(), None if scale_ub is None else scale_ub.data_ptr(),
-            None if residual is None else residual.data_ptr(), T, H,
-            _lib.DTYPE_CODE[input.dtype], float(eps), _lib.stream_of(input)))
+        if custom:
+            _lib.check(_lib.lib.mcop_rms_norm_dynamic_per_token_quant_custom(
+                out.data_ptr(), scales.data_ptr(), input.data_ptr(), weight.data_ptr(), ub, rp,
+                T, H, _lib.DTYPE_CODE[input.dtype], float(eps), _lib.stream_of(input)))
+        else:
+            _lib.check(_lib.lib.mcop_rms_norm_dynamic_per_token_quant(
+                out.data_ptr(), _lib.DTYPE_CODE[out.dtype], scales.data_ptr(),
+                input.data_ptr(), weight.data_ptr(), ub, rp, T, H,
+                _lib.DTYPE_CODE[input.dtype], float(eps), _lib.stream_of(input)))
 
 
 def scale_dynamic_quant(hidden_states: torch.Tensor, smooth_scales: torch.Tensor,

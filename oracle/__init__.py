@@ -49,6 +49,7 @@ def _load() -> ctypes.CDLL:
     lib.oracle_add_rms_norm_quant_padded.argtypes = [P, I64, P, P, P, P, P, P, I64, I64, F]
     lib.oracle_rms_norm_per_block_quant.argtypes = [P, I, P, P, P, P, P, I64, I64, I, F, I64, I]
     lib.oracle_rms_norm.argtypes = [P, P, P, I, P, P, I64, I64, I, F, I]
+    lib.oracle_rms_norm_quant_custom.argtypes = [P, P, P, P, P, P, I64, I64, I, F]
     lib.oracle_head_rms_norm.argtypes = [P, P, P, I, I64, I64, I64, I64, I64, I, F]
     lib.oracle_vllm_rms_norm.argtypes = [P, P, P, I64, I64, I, F]
     for name in ("oracle_f32_to_bf16_array", "oracle_f32_to_f16_array",
@@ -61,7 +62,7 @@ def _load() -> ctypes.CDLL:
                  "oracle_dynamic_scaled_int8_quant", "oracle_dynamic_scaled_int8_azp_quant",
                  "oracle_dynamic_per_token_fp8_quant", "oracle_add_rms_norm_quant_padded",
                  "oracle_rms_norm_per_block_quant", "oracle_rms_norm", "oracle_head_rms_norm",
-                 "oracle_vllm_rms_norm"):
+                 "oracle_vllm_rms_norm", "oracle_rms_norm_quant_custom"):
         getattr(lib, name).restype = None
     lib.oracle_set_threads.argtypes = [I]
     lib.oracle_num_threads.restype = I
@@ -158,6 +159,26 @@ def rms_norm_per_block_quant(
                                           xc.data_ptr(), w.data_ptr(), ub, _ptr(ro), T, H,
                                           _DT[x.dtype], float(eps), int(group_size),
                                           1 if is_scale_transposed else 0)
+    return out, scales, ro
+
+
+def rms_norm_dynamic_per_token_quant_custom(
+        x: torch.Tensor, weight: torch.Tensor, eps: float, scale_ub: Optional[float] = None,
+        residual: Optional[torch.Tensor] = None
+) -> tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """mcoplib ``op.rms_norm_dynamic_per_token_quant_custom`` (op/rms_norm_dynamic_per_token_quant.cu
+    :52-285, kernel/rms_norm_vllm.cuh:330-454), int8 only.
+
+    Returns (int8 codes, scales [T, 1] fp32, new residual or None)."""
+    xc, w = _cpu(x), _cpu(weight)
+    T, H = _rows(xc)
+    out = torch.empty(xc.shape, dtype=torch.int8)
+    scales = torch.empty((T, 1), dtype=torch.float32)
+    ro = None if residual is None else _cpu(residual).clone()
+    ub = None if scale_ub is None else ctypes.byref(ctypes.c_float(float(scale_ub)))
+    lib().oracle_rms_norm_quant_custom(out.data_ptr(), scales.data_ptr(), xc.data_ptr(),
+                                       w.data_ptr(), ub, _ptr(ro), T, H, _DT[x.dtype],
+                                       float(eps))
     return out, scales, ro
 
 
@@ -333,7 +354,8 @@ def f32_to_e4m3fn_bits(x: torch.Tensor) -> torch.Tensor:
 
 __all__ = [
     "build", "set_threads", "num_threads", "fused_add_rms_norm",
-    "rms_norm_dynamic_per_token_quant", "rms_norm_smooth_quant", "scale_dynamic_quant",
+    "rms_norm_dynamic_per_token_quant", "rms_norm_dynamic_per_token_quant_custom",
+    "rms_norm_smooth_quant", "scale_dynamic_quant",
     "dynamic_scaled_int8_quant", "dynamic_per_token_scaled_fp8_quant",
     "add_rms_norm_quant_padded", "rms_norm_per_block_quant", "rms_norm", "head_rms_norm",
     "vllm_rms_norm", "fp8_e4m3fn_from_f32", "f32_to_bf16_bits", "f32_to_f16_bits", "f32_to_e4m3fn_bits",

@@ -275,6 +275,55 @@ void oracle_rms_norm_per_block_quant(void* out, int out_dt, float* scales, const
   }
 }
 
+/* mcoplib rms_norm_dynamic_per_token_quant_custom (int8 only),
+   op/rms_norm_dynamic_per_token_quant.cu:266-285 with its two kernels:
+   H != 7168 (:52-92; kernel/rms_norm_vllm.cuh:330-454): y = b(b(a*rho) * w) as above;
+     A = max|y| (min with ub); s = max(A / 127, 1.5e-6) evaluated as the reference writes it
+     (a float quotient against a double literal, :382); inv = 1.0f / s (:89);
+     q = sat[-127,127](rne(y * inv)) (float_to_int8_rn of kernel/utils.h:219-226);
+   H == 7168 (:94-186): p = a * w (fp32, :146-149); A = max|p|; s = max((A * rho) / 127,
+     FLT_EPSILON) (:170-171); inv = 1.0f / s (:172); q = sat[-127,127](rne((p * rho) * inv))
+     (:179-182); ub is not read.  r <- b(a) in both. */
+void oracle_rms_norm_quant_custom(int8_t* out, float* scales, const void* x, const void* w,
+                                  const float* scale_ub, void* r, int64_t T, int64_t H, int dt,
+                                  float eps) {
+  const int h7168 = H == 7168;
+#pragma omp parallel
+  {
+    float* a = (float*)malloc((size_t)H * sizeof(float));
+#pragma omp for schedule(static)
+    for (int64_t t = 0; t < T; ++t) {
+      acc64 S = {0.0, 0.0};
+      for (int64_t i = 0; i < H; ++i) {
+        float v = load_el(x, dt, t * H + i);
+        if (r) v += load_el(r, dt, t * H + i);
+        a[i] = v;
+        acc_add(&S, (double)v * (double)v);
+      }
+      if (r) for (int64_t i = 0; i < H; ++i) store_el(r, dt, t * H + i, a[i]);
+      const float rho = inv_rms(acc_val(&S), H, eps);
+      float amax = 0.0f;
+      for (int64_t i = 0; i < H; ++i) {
+        const float wf = load_el(w, dt, i);
+        a[i] = h7168 ? a[i] * wf : rnd_el(rnd_el(a[i] * rho, dt) * wf, dt);
+        amax = fmaxf(amax, fabsf(a[i]));
+      }
+      float s;
+      if (h7168) {
+        s = fmaxf((amax * rho) / 127.0f, FLT_EPSILON);
+      } else {
+        if (scale_ub) amax = fminf(amax, *scale_ub);
+        s = (float)fmax((double)(amax / 127.0f), 1.5e-6);
+      }
+      const float inv = 1.0f / s;
+      scales[t] = s;
+      for (int64_t i = 0; i < H; ++i)
+        out[t * H + i] = q_int8((h7168 ? a[i] * rho : a[i]) * inv, -127);
+    }
+    free(a);
+  }
+}
+
 /* ---------------------------------------------------------------- H4 */
 
 /* mcoplib rms_norm_dynamic_per_token_quant (fused_rms_norm_dq), op/fused_rms_norm_dq.cu:260-303

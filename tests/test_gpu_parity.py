@@ -76,8 +76,8 @@ def test_config3_add_norm_int8_outliers():
     x = _outlier_x(T, H, 3)
     r = randn((T, H), 30, torch.bfloat16)
     w = weight(H, 31, torch.bfloat16)
-    q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant(x, w, 1e-5, torch.int8,
-                                                                 residual=r)
+    q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant_custom(x, w, 1e-5,
+                                                                        residual=r)
     xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
     q, s = custom_ops.rms_norm_dynamic_per_token_quant(xd, wd, 1e-5, torch.int8, residual=rd)
     torch.cuda.synchronize()
@@ -219,8 +219,8 @@ def test_config5_large_sampled_rows():
     x_s, r_s = xd[rows.to(DEV)].cpu(), rd[rows.to(DEV)].cpu()
     q, s = custom_ops.rms_norm_dynamic_per_token_quant(xd, wd, 1e-6, torch.int8, residual=rd)
     torch.cuda.synchronize()
-    q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant(x_s, wd.cpu(), 1e-6,
-                                                                 torch.int8, residual=r_s)
+    q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant_custom(x_s, wd.cpu(), 1e-6,
+                                                                        residual=r_s)
     idx = rows.to(DEV)
     assert_exact(rd[idx], r_ref, "cfg5 residual (sampled rows)")
     assert_scales(s[idx], s_ref, "cfg5 scales (sampled rows)")
@@ -298,8 +298,8 @@ def test_misaligned_views_take_the_scalar_path():
     w = weight(H, 82, torch.bfloat16)
     x = buf_x[1:].view(T, H)
     r = buf_r[3:].view(T, H)
-    q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant(x, w, 1e-6, torch.int8,
-                                                                 residual=r)
+    q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant_custom(x, w, 1e-6,
+                                                                        residual=r)
     bxd, brd = buf_x.to(DEV), buf_r.to(DEV)
     xd, rd = bxd[1:].view(T, H), brd[3:].view(T, H)
     q = torch.empty((T, H), dtype=torch.int8, device=DEV)
@@ -370,3 +370,50 @@ def test_fp8_conversion_matches_ocp_definition():
         torch.cuda.synchronize()
         bad = (out.cpu() != ref)
         assert int(bad.sum()) == 0, (x[bad][:8], out.cpu()[bad][:8], ref[bad][:8])
+
+
+@pytest.mark.parametrize("T,H", [(1, 7168), (83, 7168), (2048, 7168), (3, 64), (83, 1033),
+                                 (256, 4096), (7, 16384), (5, 7176)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_h3_custom_op_shapes(T, H, dtype):
+    """mcoplib's rms_norm_dynamic_per_token_quant_custom: its fp32 chain at H == 7168 and its
+    generic chain (1.5e-6 floor, codes in [-127, 127]) elsewhere, with and without residual
+    and scale_ub (which the 7168 chain ignores)."""
+    say(f"h3 custom T={T} H={H} {dtype}")
+    for with_res in (False, True):
+        for ub in (None, 0.05):
+            x = randn((T, H), T + H, dtype, scale=2.0)
+            w = weight(H, T + H + 1, dtype)
+            r = randn((T, H), T + H + 2, dtype) if with_res else None
+            q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant_custom(
+                x, w, 1e-6, scale_ub=ub, residual=r)
+            rd = r.to(DEV) if with_res else None
+            q = torch.empty((T, H), dtype=torch.int8, device=DEV)
+            s = torch.empty((T, 1), dtype=torch.float32, device=DEV)
+            ubd = None if ub is None else torch.tensor([ub], device=DEV)
+            op.rms_norm_dynamic_per_token_quant_custom(q, x.to(DEV), w.to(DEV), s, 1e-6, ubd, rd)
+            torch.cuda.synchronize()
+            tag = f"h3 T={T} H={H} {dtype} res={with_res} ub={ub}"
+            assert_scales(s, s_ref, tag + " scales")
+            assert_codes(q, q_ref, tag + " codes")
+            if with_res:
+                assert_exact(rd, r_ref, tag + " residual")
+
+
+def test_h3_custom_op_zero_rows_and_specials():
+    say("h3 custom special rows")
+    for H in (7168, 4096):
+        rows = [torch.zeros(H), torch.randn(H, generator=gen(95)) * 1e-30,
+                torch.randn(H, generator=gen(96)) * 1e30]
+        t = torch.randn(H, generator=gen(97))
+        t[9] = float("nan")
+        rows.append(t)
+        x = torch.stack(rows).to(torch.bfloat16)
+        w = weight(H, 98, torch.bfloat16)
+        q_ref, s_ref, _ = oracle.rms_norm_dynamic_per_token_quant_custom(x, w, 1e-6)
+        q = torch.empty(x.shape, dtype=torch.int8, device=DEV)
+        s = torch.empty((x.shape[0], 1), dtype=torch.float32, device=DEV)
+        op.rms_norm_dynamic_per_token_quant_custom(q, x.to(DEV), w.to(DEV), s, 1e-6, None, None)
+        torch.cuda.synchronize()
+        assert_scales(s, s_ref, f"h3 specials H={H} scales")
+        assert_codes(q, q_ref, f"h3 specials H={H} codes")

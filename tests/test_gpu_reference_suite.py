@@ -14,6 +14,8 @@
 import pytest
 import torch
 
+import oracle
+
 import mcoplib_amd._C  # noqa: F401
 from mcoplib_amd import custom_ops, op
 from gpu_util import DEV, say
@@ -147,6 +149,10 @@ def test_rms_norm_custom_7168():
     yq, ys = _per_token_int8(y)
     assert torch.allclose(s, ys, rtol=2 ** -6)
     assert (q.float() - yq.float()).abs().max() <= 2
+    # and exactly the reference kernel's own (fp32) chain at this width
+    q_ref, s_ref, _ = oracle.rms_norm_dynamic_per_token_quant_custom(
+        x.cpu(), w.cpu(), 1e-6, residual=res_in.cpu())
+    assert torch.equal(q.cpu(), q_ref) and torch.equal(s.cpu(), s_ref)
 
 
 # ------------------------------------------------------------ test_rms_norm.py
