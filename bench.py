@@ -44,7 +44,7 @@ def parse():
                     choices=["cfg2", "cfg3", "cfg4", "cfg5-large", "cfg5-decode1",
                              "cfg5-decode4", "cfg5-decode16", "cfg5-decode64", "ptq-int8",
                              "ptq-int8-azp", "ptq-fp8", "padded", "block-fp8", "norm-res",
-                             "vllm-norm", "head-norm"])
+                             "vllm-norm", "head-norm", "sdq"])
     ap.add_argument("--sets", type=int, default=0,
                     help="rotated input sets (default: enough for > 1 GiB, at least 3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -72,6 +72,8 @@ class Workload:
             return 8 * T * H + 2 * H
         if self.kind == "smooth_fp8":      # read x; write q, after_res, after_norm; w, smooth, s
             return 2 * T * H + T * H + 4 * T * H + 2 * H + 4 * H + 4 * T
+        if self.kind == "sdq":             # read h, smooth (fp32); write q, s
+            return 3 * T * H + 4 * H + 4 * T
         if self.kind in ("ptq_int8", "ptq_fp8"):  # read x; write q, s
             return 3 * T * H + 4 * T
         if self.kind == "ptq_int8_azp":    # read x; write q, s, azp
@@ -122,6 +124,8 @@ class Workload:
             d["s"] = torch.empty(T, 1, dtype=torch.float32, device=dev)
             d["azp"] = (torch.empty(T, 1, dtype=torch.int32, device=dev)
                         if self.kind == "ptq_int8_azp" else None)
+        if self.kind == "sdq":
+            d["sm"] = 0.5 + 1.5 * torch.rand(H, generator=g, device=dev)
         if self.kind == "smooth_fp8":
             d["sm"] = 0.5 + 1.5 * torch.rand(H, generator=g, device=dev)
             d["q"] = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=dev)
@@ -151,6 +155,8 @@ class Workload:
         if self.kind == "padded":
             return lambda: op.fused_add_rms_norm_dynamic_per_token_quant_padding_output(
                 d["p"], d["rms"], d["q"], d["s"], d["x"], d["r"], d["w"], PAD_SIZE, self.eps)
+        if self.kind == "sdq":  # returns new tensors, as the reference's op does
+            return lambda: op.scale_dynamic_quant(d["x"], d["sm"], torch.int8)
         if self.kind == "ptq_fp8":
             return lambda: torch.ops._C.dynamic_per_token_scaled_fp8_quant(d["q"], d["x"], d["s"],
                                                                          None)
@@ -180,12 +186,15 @@ WORKLOADS = {
     "norm-res": Workload("norm-res", 8192, 8192, 1e-6, "norm_res"),
     "vllm-norm": Workload("vllm-norm", 8192, 8192, 1e-6, "vllm_norm"),
     "head-norm": Workload("head-norm", 65536 * 8, 128, 1e-6, "head_norm"),
+    # the un-normed SmoothQuant sibling (scale_dynamic_quant) at SmoothQuant's shape
+    "sdq": Workload("sdq", 16384, 7168, 0.0, "sdq"),
 }
 KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "fused_add": "k_fused_add_rms_norm",
                "smooth_fp8": "k_rms_norm_smooth_quant", "ptq_int8": "k_per_token_quant",
                "ptq_int8_azp": "k_per_token_quant", "ptq_fp8": "k_per_token_quant",
                "padded": "k_add_rms_norm_quant_padded", "block_fp8": "k_rms_norm_group_quant",
-               "norm_res": "k_rms_norm", "vllm_norm": "k_rms_norm", "head_norm": "k_rms_norm"}
+               "norm_res": "k_rms_norm", "vllm_norm": "k_rms_norm", "head_norm": "k_rms_norm",
+               "sdq": "k_scale_dynamic_quant"}
 
 
 # ------------------------------------------------------------------------------ pieces
@@ -231,6 +240,8 @@ def cpu_baseline(wl: Workload, seconds: float) -> dict:
                                             residual=r)
         elif wl.kind == "padded":
             oracle.add_rms_norm_quant_padded(x, r, w, PAD_SIZE, wl.eps)
+        elif wl.kind == "sdq":
+            oracle.scale_dynamic_quant(x, sm)
         elif wl.kind == "ptq_fp8":
             oracle.dynamic_per_token_scaled_fp8_quant(x)
         elif wl.kind.startswith("ptq_int8"):
@@ -369,7 +380,7 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": f"{wl.name}: {wl.kind} T={wl.T} H={wl.H} bf16 in"
-                               + ("" if wl.kind.startswith("ptq_") else f", eps={wl.eps}")
+                               + ("" if wl.kind.startswith("ptq_") or wl.kind == "sdq" else f", eps={wl.eps}")
                                + (", 1% outlier channels x20" if wl.name == "cfg3" else ""),
                    "tokens": wl.T, "hidden": wl.H, "io": "bf16 -> int8/fp8 + fp32 scales",
                    "rotated_input_sets": len(sets)},

@@ -310,6 +310,25 @@ __device__ __forceinline__ RowPos row_pos(int64_t num_rows, int tpr) {
   return p;
 }
 
+// Position of the k-th of R rows that each lane handles: workgroup b covers R runs of rpb
+// adjacent rows (run k = rows [(b*R + k) * rpb, +rpb)), so each load instruction of a wave reads
+// rows that sit next to each other.  row_pos_of(n, tpr, 0, 1) == row_pos(n, tpr).
+__device__ __forceinline__ RowPos row_pos_of(int64_t num_rows, int tpr, int k, int R) {
+  RowPos p;
+  if ((int)blockDim.x == tpr) {
+    p.row = (int64_t)blockIdx.x * R + k;
+    p.lt = threadIdx.x;
+  } else {
+    const int sh = 31 - __builtin_clz((unsigned)tpr);
+    const int lg_rpb = 31 - __builtin_clz(blockDim.x >> sh);
+    p.row = (((int64_t)blockIdx.x * R + k) << lg_rpb) + (threadIdx.x >> sh);
+    p.lt = threadIdx.x & (tpr - 1);
+  }
+  p.live = p.row < num_rows;
+  p.lrow = p.live ? p.row : num_rows - 1;
+  return p;
+}
+
 // Vector index of a lane's v-th vector, and the index its loads use (0 when past the row end,
 // so the load stays inside the row and is discarded).
 __device__ __forceinline__ int vec_index(int v, int tpr, int lt) { return v * tpr + lt; }

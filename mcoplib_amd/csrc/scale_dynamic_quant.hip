@@ -13,68 +13,105 @@
 
 namespace mcop {
 
-template <int VEC, int NV>
+// R rows per lane (1, or 2 for many rows): the lane's smooth vectors, loaded once, serve R rows.
+// The smooth scales are fp32, two loads per 16-byte input vector; even as cache hits they took
+// 20% of the kernel's time in a compute-free model of this access pattern at 16384 x 7168, and
+// sharing them between two rows recovers about half of that.
+template <int VEC, int NV, int R>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
 k_scale_dynamic_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
                       const uint16_t* __restrict__ x, const float* __restrict__ sm, int64_t rows,
                       int hidden, int tpr) {
-  __shared__ float red_max[16];
-  const RowPos p = row_pos(rows, tpr);
+  __shared__ float red_max[16 * R];
   const int nvec = hidden / VEC;
-  const int64_t base = p.row * (int64_t)hidden;
-  const int64_t lbase = p.lrow * (int64_t)hidden;
+  RowPos p[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) p[k] = row_pos_of(rows, tpr, k, R);
 
-  Pack<uint16_t, VEC> xv[NV];
   Pack<float, VEC> sv[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    sv[v] = ld<float, VEC>(sm + (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC);
+    sv[v] = ld<float, VEC>(sm + (int64_t)load_index(vec_index(v, tpr, p[0].lt), nvec) * VEC);
   }
   shared_loads_first();
+  Pack<uint16_t, VEC> xv[R][NV];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    xv[v] = ld_nt<uint16_t, VEC>(x + lbase +
-                                 (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC);
+  for (int k = 0; k < R; ++k) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      xv[k][v] = ld_nt<uint16_t, VEC>(x + p[k].lrow * (int64_t)hidden +
+                                      (int64_t)load_index(vec_index(v, tpr, p[k].lt), nvec) * VEC);
+    }
   }
 
-  float a[NV][VEC];
-  float amax = 0.0f;
+  float a[R][NV][VEC];
+  float amax[R];
   // Lanes past the row end hold a copy of vector 0, which does not change the max.
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
+  for (int k = 0; k < R; ++k) {
+    amax[k] = 0.0f;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const float t = BF16::to_f(xv[v].v[e]) * sv[v].v[e];
-      a[v][e] = t;
-      amax = __builtin_fmaxf(amax, __builtin_fabsf(t));
+    for (int v = 0; v < NV; ++v) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float t = BF16::to_f(xv[k][v].v[e]) * sv[v].v[e];
+        a[k][v][e] = t;
+        amax[k] = __builtin_fmaxf(amax[k], __builtin_fabsf(t));
+      }
     }
   }
-  amax = row_reduce(amax, red_max, tpr, MaxOp());
-
-  if (p.live && p.lt == 0) scales[p.row] = amax * 0.00787401574803f;
-  const float inv = amax > 0.0f ? mcop_div_rn(127.0f, amax) : 0.0f;
+#pragma unroll
+  for (int k = 0; k < R; ++k) amax[k] = row_reduce(amax[k], red_max + 16 * k, tpr, MaxOp());
 
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int j = vec_index(v, tpr, p.lt);
-    if (p.live && j < nvec) {
-      Pack<uint8_t, VEC> q;
+  for (int k = 0; k < R; ++k) {
+    if (p[k].live && p[k].lt == 0) scales[p[k].row] = amax[k] * 0.00787401574803f;
+    const float inv = amax[k] > 0.0f ? mcop_div_rn(127.0f, amax[k]) : 0.0f;
+    const int64_t base = p[k].row * (int64_t)hidden;
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(a[v][e] * inv);
-      st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
+    for (int v = 0; v < NV; ++v) {
+      const int j = vec_index(v, tpr, p[k].lt);
+      if (p[k].live && j < nvec) {
+        Pack<uint8_t, VEC> q;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(a[k][v][e] * inv);
+        st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
+      }
     }
   }
+}
+
+// Two rows per lane when the vector path has at least 2048 rows and at most four vectors per
+// lane (more would spill); one otherwise (fewer rows: every row is already in flight).
+static int rows_per_lane(const Geometry& g, int64_t rows) {
+  return g.vec > 1 && g.nv <= 4 && rows >= 2048 ? 2 : 1;
 }
 
 template <int VEC>
 static void launch_nv(const Geometry& g, int8_t* out, float* scales, const void* x,
                       const float* sm, int64_t rows, int hidden, hipStream_t st) {
-  const dim3 grid((unsigned)g.blocks), block((unsigned)(g.tpr * g.rpb));
+  const dim3 block((unsigned)(g.tpr * g.rpb));
   auto* o = reinterpret_cast<uint8_t*>(out);
   auto* xp = static_cast<const uint16_t*>(x);
-#define MCOP_LAUNCH(NVV)                                                                     \
-  hipLaunchKernelGGL((k_scale_dynamic_quant<VEC, NVV>), grid, block, 0, st, o, scales, xp, sm, \
-                     rows, hidden, g.tpr)
+  if constexpr (VEC > 1) {
+    if (rows_per_lane(g, rows) == 2) {
+      const dim3 grid((unsigned)((rows + 2 * g.rpb - 1) / (2 * g.rpb)));
+#define MCOP_LAUNCH(NVV)                                                                       \
+  hipLaunchKernelGGL((k_scale_dynamic_quant<VEC, NVV, 2>), grid, block, 0, st, o, scales, xp,   \
+                     sm, rows, hidden, g.tpr)
+      switch (g.nv) {
+        case 1: MCOP_LAUNCH(1); break;
+        case 2: MCOP_LAUNCH(2); break;
+        default: MCOP_LAUNCH(4); break;
+      }
+#undef MCOP_LAUNCH
+      return;
+    }
+  }
+  const dim3 grid((unsigned)g.blocks);
+#define MCOP_LAUNCH(NVV)                                                                       \
+  hipLaunchKernelGGL((k_scale_dynamic_quant<VEC, NVV, 1>), grid, block, 0, st, o, scales, xp,   \
+                     sm, rows, hidden, g.tpr)
   if constexpr (VEC == 1) {
     if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
   } else {
@@ -92,15 +129,15 @@ static void launch_nv(const Geometry& g, int8_t* out, float* scales, const void*
 template <int VEC>
 static const void* kernel_of(int nv) {
   if constexpr (VEC == 1) {
-    return nv == 4 ? reinterpret_cast<const void*>(&k_scale_dynamic_quant<1, 4>)
-                   : reinterpret_cast<const void*>(&k_scale_dynamic_quant<1, 16>);
+    return nv == 4 ? reinterpret_cast<const void*>(&k_scale_dynamic_quant<1, 4, 1>)
+                   : reinterpret_cast<const void*>(&k_scale_dynamic_quant<1, 16, 1>);
   } else {
     switch (nv) {
-      case 1: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 1>);
-      case 2: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 2>);
-      case 4: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 4>);
-      case 8: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 8>);
-      default: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 16>);
+      case 1: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 1, 1>);
+      case 2: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 2, 1>);
+      case 4: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 4, 1>);
+      case 8: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 8, 1>);
+      default: return reinterpret_cast<const void*>(&k_scale_dynamic_quant<VEC, 16, 1>);
     }
   }
 }

@@ -193,10 +193,27 @@ def test_config4_smooth_quant_fp8():
     (torch.float32, torch.float32, torch.float32, torch.int8, True, True),
 ])
 def test_h4_many_rows_row_loop(dtype, wdt, sdt, qdt, with_res, standard):
-    """Enough rows (> 4 per resident workgroup) for the row-walking launch of the smooth-quant
-    kernel, which keeps weight and smooth vectors in registers across rows."""
-    say(f"h4 row loop 8192x4096 {dtype} {qdt} res={with_res} std={standard}")
+    """Many rows (8192 x 4096: more workgroups than stay resident) with mixed dtypes."""
+    say(f"h4 many rows 8192x4096 {dtype} {qdt} res={with_res} std={standard}")
     _h4_case(8192, 4096, dtype, wdt, sdt, qdt, with_res, standard, 21, x_scale=2.0)
+
+
+@pytest.mark.parametrize("T,H,ov", [(2049, 7168, (0, 0)), (2051, 7168, (1, 0)),
+                                    (2053, 4096, (4, 0)), (3001, 128, (0, 0)),
+                                    (2050, 200, (0, 0)), (4097, 1024, (0, 0)),
+                                    (2048, 16384, (0, 0))])
+def test_h4_large_row_counts(T, H, ov):
+    """Odd row counts past 2048, several rows per workgroup (short rows), forced one / four
+    vectors per lane and a 16384-wide row, against the oracle bit for bit."""
+    say(f"h4 large row counts T={T} H={H} override={ov}")
+    try:
+        _lib.set_launch_override(*ov)
+        _h4_case(T, H, torch.bfloat16, torch.bfloat16, torch.float32, torch.float8_e4m3fn,
+                 False, False, T + H, x_scale=2.0)
+        _h4_case(T, H, torch.bfloat16, torch.float32, torch.bfloat16, torch.int8, True, True,
+                 T + H + 1, x_scale=3.0)
+    finally:
+        _lib.set_launch_override(0, 0)
 
 
 @pytest.mark.parametrize("T", [1, 4, 16, 64])
@@ -240,6 +257,29 @@ def test_h5_parity_shapes():
         assert q.shape == h.shape and s.shape == (h.numel() // shape[-1],)
         assert_scales(s, s_ref, "h5 scales")
         assert_codes(q, q_ref, "h5 codes")
+
+
+@pytest.mark.parametrize("T,H,ov", [(2049, 7168, (0, 0)), (2048, 7168, (2, 0)),
+                                    (2051, 4096, (1, 0)), (4099, 1024, (0, 0)),
+                                    (3001, 128, (0, 0)), (2050, 200, (0, 0)),
+                                    (2053, 8192, (4, 0))])
+def test_h5_two_rows_per_lane(T, H, ov):
+    """From 2048 rows on, each lane quantizes two rows with one load of the smooth scales:
+    odd row counts (a workgroup's second row past the end), several rows per workgroup (short
+    rows) and forced vectors per lane, against the oracle bit for bit."""
+    say(f"h5 two rows per lane T={T} H={H} override={ov}")
+    h = randn((T, H), T + H, torch.bfloat16)
+    h[T // 2].zero_()
+    sm = 0.5 + 1.5 * torch.rand(H, generator=gen(T))
+    q_ref, s_ref = oracle.scale_dynamic_quant(h, sm)
+    try:
+        _lib.set_launch_override(*ov)
+        q, s = op.scale_dynamic_quant(h.to(DEV), sm.to(DEV), torch.int8)
+        torch.cuda.synchronize()
+    finally:
+        _lib.set_launch_override(0, 0)
+    assert_scales(s, s_ref, "h5 scales")
+    assert_codes(q, q_ref, "h5 codes")
 
 
 @pytest.mark.parametrize("T", [512, 517])
