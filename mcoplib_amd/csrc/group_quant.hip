@@ -28,9 +28,16 @@
 
 namespace mcop {
 
-// max over aligned runs of `lanes` consecutive lanes (a power of two <= 64) of one wave
+// max over aligned runs of `lanes` consecutive lanes (a power of two <= 64) of one wave: DPP
+// moves within 16-lane rows, LDS-routed shuffles across them
 __device__ __forceinline__ float group_max(float v, int lanes) {
-  for (int m = 1; m < lanes; m <<= 1) v = __builtin_fmaxf(v, __shfl_xor(v, m, 64));
+  const MaxOp op;
+  if (lanes >= 2) v = op(v, dpp_mov<kDppXor1>(v));
+  if (lanes >= 4) v = op(v, dpp_mov<kDppXor2>(v));
+  if (lanes >= 8) v = op(v, dpp_mov<kDppHalfMirror>(v));
+  if (lanes >= 16) v = op(v, dpp_mov<kDppMirror>(v));
+  if (lanes >= 32) v = op(v, __shfl_xor(v, 16, 64));
+  if (lanes >= 64) v = op(v, __shfl_xor(v, 32, 64));
   return v;
 }
 

@@ -44,16 +44,27 @@ struct RowOffsets {
   int64_t in, out, w;
 };
 
+// q = r / n, r % n for a row index r >= 0 and an extent n >= 1 that is the same for every lane:
+// a shift for powers of two (head counts usually are), 32-bit division when both fit, else
+// 64-bit division.
+__device__ __forceinline__ int64_t div_extent(int64_t r, int64_t n, int64_t* rem) {
+  if ((n & (n - 1)) == 0) {
+    *rem = r & (n - 1);
+    return r >> __builtin_ctzll((uint64_t)n);
+  }
+  if (((uint64_t)r | (uint64_t)n) <= 0xffffffffull) {
+    const uint32_t q = (uint32_t)r / (uint32_t)n;
+    *rem = (int64_t)((uint32_t)r - q * (uint32_t)n);
+    return q;
+  }
+  *rem = r % n;
+  return r / n;
+}
+
 __device__ __forceinline__ RowOffsets row_offsets(const RowMap& m, int64_t r) {
   int64_t i0 = r, i1 = 0, i2 = 0;
-  if (m.n2 != 1) {
-    i2 = r % m.n2;
-    i0 = r / m.n2;
-  }
-  if (m.n1 != 1) {
-    i1 = i0 % m.n1;
-    i0 = i0 / m.n1;
-  }
+  if (m.n2 != 1) i0 = div_extent(r, m.n2, &i2);
+  if (m.n1 != 1) i0 = div_extent(i0, m.n1, &i1);
   return {i0 * m.s0 + i1 * m.s1 + i2 * m.s2, i0 * m.o0 + i1 * m.o1 + i2 * m.o2, i2 * m.w2};
 }
 

@@ -245,17 +245,48 @@ struct MaxOp {
   }
 };
 
+// A lane's partner value under a DPP lane pattern (a register move inside each 16-lane row,
+// no LDS round trip), for 32- and 64-bit values.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, true);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, true);
+  return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <- 7 - i within each 8 lanes
+constexpr int kDppMirror = 0x140;      // lane i <- 15 - i within each 16 lanes
+
+// All-reduce within each aligned 16-lane segment: after the quad steps every lane holds its
+// quad's value, the half-row mirror pairs quad 0 with 1 and 2 with 3, the row mirror pairs the
+// two halves.
+template <class T, class Op>
+__device__ __forceinline__ T reduce16(T v, Op op) {
+  v = op(v, dpp_mov<kDppXor1>(v));
+  v = op(v, dpp_mov<kDppXor2>(v));
+  v = op(v, dpp_mov<kDppHalfMirror>(v));
+  return op(v, dpp_mov<kDppMirror>(v));
+}
+
 template <class T, class Op>
 __device__ __forceinline__ T wave_reduce(T v, Op op) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = op(v, __shfl_xor(v, m, 64));
-  return v;
+  v = reduce16(v, op);
+  v = op(v, __shfl_xor(v, 16, 64));
+  return op(v, __shfl_xor(v, 32, 64));
 }
 
 template <class T, class Op>
 __device__ __forceinline__ T row_reduce(T v, T* lds, int tpr, Op op) {
-  if (tpr < 64) {  // several rows per wave: butterfly within each row's aligned lane segment
-    for (int m = tpr >> 1; m >= 1; m >>= 1) v = op(v, __shfl_xor(v, m, 64));
+  if (tpr < 64) {  // several rows per wave: all-reduce within each row's aligned lane segment
+    v = reduce16(v, op);
+    if (tpr == 32) v = op(v, __shfl_xor(v, 16, 64));
     return v;
   }
   v = wave_reduce(v, op);
