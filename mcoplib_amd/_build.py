@@ -1,10 +1,13 @@
-"""Build libmcop_norm.so (the gfx950 kernels and their C ABI) in-tree with hipcc.
+"""Build libmcop_norm.so (the gfx950 kernels and their C ABI) in-tree with hipcc, and the C++
+torch extension _torch_ops.so (the mcoplib.op / torch.ops._C surfaces over that ABI) with g++.
 
 Usage: python mcoplib_amd/_build.py [--jobs N]
 (run as a script: importing the package would load the library this builds)
 
 Each csrc/*.hip translation unit is compiled for gfx950 only, in parallel, then linked into
 mcoplib_amd/libmcop_norm.so next to this file. Objects go to mcoplib_amd/_build/.
+csrc/torch_ops.cpp is host C++ against torch's headers (ROCm build) and links
+libmcop_norm.so through an $ORIGIN run path.
 """
 
 from __future__ import annotations
@@ -21,6 +24,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libmcop_norm.so"
+EXT = PKG / "_torch_ops.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -66,7 +70,8 @@ def build(jobs: int | None = None, verbose: bool = True, out: Path = LIB,
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda s: _compile(s, build_dir, defines), srcs))
     tmp = out.with_suffix(".so.tmp")
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", f"-Wl,-soname,{LIB.name}", "-o",
+           str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
@@ -76,11 +81,42 @@ def build(jobs: int | None = None, verbose: bool = True, out: Path = LIB,
     return out
 
 
+def build_extension(verbose: bool = True) -> Path:
+    """Compile csrc/torch_ops.cpp into mcoplib_amd/_torch_ops.so (always rebuilds)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    tdir = Path(torch.__file__).resolve().parent
+    cxx = os.environ.get("CXX", "g++")
+    abi = int(torch.compiled_with_cxx11_abi())
+    incs = [*cpp_extension.include_paths(), sysconfig.get_paths()["include"]]
+    if "/opt/rocm/include" not in incs:
+        incs.append("/opt/rocm/include")
+    tmp = EXT.with_suffix(".so.tmp")
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wno-unused-function",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-DTORCH_EXTENSION_NAME=_torch_ops",
+           "-DTORCH_API_INCLUDE_EXTENSION_H", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           *[f"-I{p}" for p in incs], str(CSRC / "torch_ops.cpp"), "-o", str(tmp),
+           f"-L{tdir / 'lib'}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+           "-ltorch_python", f"-L{PKG}", "-lmcop_norm", "-Wl,-rpath,$ORIGIN",
+           f"-Wl,-rpath,{tdir / 'lib'}"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"{cxx} failed for torch_ops.cpp:\n{proc.stderr}")
+    os.replace(tmp, EXT)
+    if verbose:
+        print(f"built {EXT}", file=sys.stderr)
+    return EXT
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     args = ap.parse_args()
     build(args.jobs)
+    build_extension()
 
 
 if __name__ == "__main__":

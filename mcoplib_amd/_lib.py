@@ -1,8 +1,11 @@
 """ctypes binding of libmcop_norm.so (the gfx950 kernels and their C ABI, include/mcop_norm.h).
 
-The library is loaded once at import.  There is no fallback: if the library is missing or does
-not export the expected ABI, importing this module raises ImportError, and every operator of the
-package therefore fails loudly instead of computing anything elsewhere.
+The library is loaded once at import, before the C++ operator surfaces (_torch_ops.so, which
+links the same library).  There is no fallback: if the library is missing or does not export the
+expected ABI, importing this module raises ImportError, and every operator of the package
+therefore fails loudly instead of computing anything elsewhere.  The binding itself serves the
+launch-shape override, the ABI checks of the tests, and callers that want the raw ABI from
+Python.
 """
 
 from __future__ import annotations
@@ -17,14 +20,6 @@ ABI_VERSION = 1
 
 # mcop_dtype codes (include/mcop_norm.h)
 BF16, F16, F32, I8, FP8_E4M3FN = 0, 1, 2, 3, 4
-DTYPE_CODE = {
-    torch.bfloat16: BF16,
-    torch.float16: F16,
-    torch.float32: F32,
-    torch.int8: I8,
-    torch.float8_e4m3fn: FP8_E4M3FN,
-}
-SQ_STANDARD_NORM = 1
 
 
 def _load() -> ctypes.CDLL:
@@ -89,29 +84,6 @@ def stream_of(t: torch.Tensor) -> int:
     if _raw_stream is not None:
         return _raw_stream(idx)
     return torch.cuda.current_stream(t.device).cuda_stream
-
-
-class device_of:
-    """Make t's device current for the duration of a call (the reference's device guard)."""
-
-    __slots__ = ("idx", "prev")
-
-    def __init__(self, t: torch.Tensor):
-        self.idx = t.device.index
-        self.prev = None
-
-    def __enter__(self):
-        if self.idx is not None:
-            cur = torch.cuda.current_device()
-            if cur != self.idx:
-                self.prev = cur
-                torch.cuda.set_device(self.idx)
-        return self
-
-    def __exit__(self, *exc):
-        if self.prev is not None:
-            torch.cuda.set_device(self.prev)
-        return False
 
 
 def set_launch_override(vectors_per_lane: int = 0, lanes_per_row: int = 0) -> None:
