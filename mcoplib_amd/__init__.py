@@ -14,8 +14,10 @@ Surfaces (same names, argument order and in-place conventions as the reference):
                              torch.ops._C.dynamic_scaled_int8_quant and
                              torch.ops._C.dynamic_per_token_scaled_fp8_quant
 
-All of them call libmcop_norm.so (hand-written HIP kernels, C ABI in include/mcop_norm.h).
-Importing the package fails if that library is not built: there is no other implementation.
+op and _C are C++ (csrc/torch_ops.cpp, built into _torch_ops.so) and custom_ops is Python, as
+in the reference; all of them call libmcop_norm.so (hand-written HIP kernels, C ABI in
+include/mcop_norm.h).  Importing the package fails if either library is not built: there is no
+other implementation.
 """
 
 from . import _lib  # noqa: F401  (loads libmcop_norm.so; raises ImportError if missing)

@@ -77,7 +77,7 @@ def test_c_abi_rejects_bad_arguments_without_a_device():
     assert L.mcop_set_launch_override(0, 0) == 0
 
 
-def test_reference_checks_on_the_python_surfaces():
+def test_reference_checks_on_the_operator_surfaces():
     x = torch.zeros(4, 64, dtype=torch.bfloat16)
     w = torch.ones(64, dtype=torch.bfloat16)
     s = torch.zeros(4, 1)
