@@ -340,6 +340,29 @@ def main() -> int:
     # kernel's average launch duration over the timed region is total / K
     kernel_ms = ms_per_step
 
+    # (2b) the same K steps on one input set only (hot: small sets stay in the 256 MB MALL)
+    h0, h1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    h0.record()
+    for i in range(K):
+        launches[0]()
+    h1.record()
+    torch.cuda.synchronize()
+    hot_ms = h0.elapsed_time(h1) / K
+    # (2c) this GPU's device-copy bandwidth (1 GiB copy_, read + write bytes): the practical
+    # ceiling of a streaming kernel, reported next to the 8 TB/s peak
+    csrc = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    cdst = torch.empty_like(csrc)
+    for _ in range(3):
+        cdst.copy_(csrc)
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    c0.record()
+    for _ in range(5):
+        cdst.copy_(csrc)
+    c1.record()
+    torch.cuda.synchronize()
+    copy_gbs = 2 * 5 * (1 << 30) / (c0.elapsed_time(c1) * 1e-3) / 1e9
+    del csrc, cdst
+
     # (3) decode shapes are launch-bound: also time the same steps replayed from a HIP graph
     graph_us = None
     if wl.T <= 256:
@@ -394,6 +417,10 @@ def main() -> int:
                      "single_launch_us_p10_p50_p90": [
                          round(per_launch_ms[int(q * (K - 1))] * 1e3, 3) for q in (0.1, 0.5, 0.9)],
                      "algorithmic_bytes_per_launch": wl.bytes},
+        "device_copy": {"GBs": round(copy_gbs, 1), "frac": round(value / copy_gbs, 4),
+                        "what": "1 GiB torch copy_ on this GPU, read + write bytes"},
+        "hot_value": round(wl.bytes / (hot_ms * 1e-3) / 1e9, 2),
+        "hot_note": "the same steps on one input set (not rotated)",
         "host_wall_s": round(wall, 4),
         "us_per_call": round(ms_per_step * 1e3, 3),
         "us_per_call_graph": None if graph_us is None else round(graph_us, 3),
