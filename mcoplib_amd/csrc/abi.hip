@@ -171,12 +171,23 @@ bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, Kern
       tpr = fallback_tpr;
     }
   }
-  if (nv == 0) return false;
+  if (nv == 0) {
+    set_error(MCOP_E_UNSUPPORTED,
+              "%s: hidden_size %lld is larger than the register-resident kernels support",
+              op, (long long)hidden);
+    return false;
+  }
   g->vec = vec;
   g->nv = nv;
   g->tpr = (int)tpr;
   g->rpb = tpr < 256 ? (int)(256 / tpr) : 1;
   g->blocks = ceil_div(rows, g->rpb);
+  if (g->blocks > 0x7fffffffLL) {  // a launch's grid holds at most 2^31 - 1 workgroups
+    set_error(MCOP_E_UNSUPPORTED,
+              "%s: %lld rows need %lld workgroups, more than the 2147483647 one launch allows",
+              op, (long long)rows, (long long)g->blocks);
+    return false;
+  }
   if (trace_enabled()) {
     fprintf(stdout, "[mcop] %s rows=%lld hidden=%lld vec=%d nv=%d tpr=%d rows/wg=%d wgs=%lld\n",
             op, (long long)rows, (long long)hidden, g->vec, g->nv, g->tpr, g->rpb,

@@ -125,10 +125,7 @@ static int dispatch(void* x, int64_t xs, void* res, const void* w, int64_t rows,
   Geometry g;
   if (!choose_geometry("fused_add_rms_norm", rows, hidden, vec_ok ? V : 1, vec_ok ? &kernel_of<E, V> : &kernel_of<E, 1>,
                        &g)) {
-    return set_error(MCOP_E_UNSUPPORTED,
-                     "fused_add_rms_norm: hidden_size %lld is larger than the register-resident "
-                     "kernels support",
-                     (long long)hidden);
+    return MCOP_E_UNSUPPORTED;
   }
   if (g.vec == 1) {
     launch_nv<E, 1>(g, x, xs, res, w, rows, (int)hidden, eps, st);

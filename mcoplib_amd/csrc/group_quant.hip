@@ -218,9 +218,7 @@ static int dispatch(const GqArgs& a, hipStream_t st) {
   Geometry g;
   // whole waves per row: a group's lanes must lie inside one row slice of the lane mapping
   if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? V : 1, kernels, &g, 64)) {
-    return set_error(MCOP_E_UNSUPPORTED,
-                     "%s: hidden_size %d is larger than the register-resident kernels support",
-                     name, a.hidden);
+    return MCOP_E_UNSUPPORTED;
   }
   if (g.vec == 1) {
     if (a.res) launch_nv<E, 1, FP8, true>(g, a, st);

@@ -234,9 +234,7 @@ static int norm_dispatch(const char* name, const NormArgs& a, hipStream_t st) {
              : (r ? &norm_kernel_of<E, EW, 1, true> : &norm_kernel_of<E, EW, 1, false>);
   Geometry g;
   if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? V : 1, kernels, &g)) {
-    return set_error(MCOP_E_UNSUPPORTED,
-                     "%s: hidden_size %d is larger than the register-resident kernels support",
-                     name, a.hidden);
+    return MCOP_E_UNSUPPORTED;
   }
   if (g.vec == 1) {
     if (r) norm_launch_nv<E, EW, 1, true>(g, a, st);

@@ -189,9 +189,7 @@ static int dispatch(const PadArgs& a, hipStream_t st) {
   Geometry g;
   if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? 8 : 1,
                        vec_ok ? &kernel_of<8, OPT> : &kernel_of<1, OPT>, &g)) {
-    return set_error(MCOP_E_UNSUPPORTED,
-                     "%s: hidden_size %d is larger than the register-resident kernels support",
-                     name, a.hidden);
+    return MCOP_E_UNSUPPORTED;
   }
   if (g.vec == 1) launch_nv<1, OPT>(g, a, st);
   else launch_nv<8, OPT>(g, a, st);

@@ -198,9 +198,7 @@ static int dispatch(const char* name, const PtqArgs& a, hipStream_t st) {
   Geometry g;
   if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? V : 1,
                        vec_ok ? &kernel_of<E, V, MODE> : &kernel_of<E, 1, MODE>, &g)) {
-    return set_error(MCOP_E_UNSUPPORTED,
-                     "%s: hidden_size %d is larger than the register-resident kernels support",
-                     name, a.hidden);
+    return MCOP_E_UNSUPPORTED;
   }
   if (g.vec == 1) launch_nv<E, 1, MODE>(g, a, st);
   else launch_nv<E, V, MODE>(g, a, st);

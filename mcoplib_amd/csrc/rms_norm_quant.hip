@@ -218,9 +218,7 @@ static int dispatch(const char* name, void* out, float* scales, const void* x, c
   Geometry g;
   if (!choose_geometry(name, rows, hidden, vec_ok ? V : 1, kernels, &g, 16,
                        /*wide_nv4=*/false)) {
-    return set_error(MCOP_E_UNSUPPORTED,
-                     "%s: hidden_size %lld is larger than the register-resident kernels support",
-                     name, (long long)hidden);
+    return MCOP_E_UNSUPPORTED;
   }
   const int h = (int)hidden;
   if (g.vec == 1) {

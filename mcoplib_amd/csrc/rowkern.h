@@ -387,8 +387,9 @@ struct Geometry {
 // The kernel instantiation used for a given number of vectors per lane (for occupancy queries).
 using KernelOfNv = const void* (*)(int nv);
 
-// Picks the launch shape of a row kernel. `vec` is 1 or the 16-byte vector width; returns false
-// when the row does not fit (hidden too large for the register-resident kernels).  Rows of at
+// Picks the launch shape of a row kernel. `vec` is 1 or the 16-byte vector width.  Returns false,
+// with the message set (mcop_last_error), when the row does not fit the register-resident
+// kernels or the rows need more workgroups than one launch allows.  Rows of at
 // most 32 lanes may take 16 or 32 lanes (several rows per wave) unless `min_tpr` is 64.
 // `wide_nv4`: take four vectors per lane as soon as the row fills a 4-wave workgroup with them
 // (the default; the per-token norm-quant kernel measured faster at two for 8192-wide rows).

@@ -162,10 +162,7 @@ extern "C" int mcop_scale_dynamic_quant(int8_t* out, float* scales, const void* 
   Geometry g;
   if (!choose_geometry("scale_dynamic_quant", num_tokens, hidden_size, vec_ok ? V : 1,
                        vec_ok ? &kernel_of<V> : &kernel_of<1>, &g)) {
-    return set_error(MCOP_E_UNSUPPORTED,
-                     "scale_dynamic_quant: hidden_size %lld is larger than the register-resident "
-                     "kernels support",
-                     (long long)hidden_size);
+    return MCOP_E_UNSUPPORTED;
   }
   auto st = static_cast<hipStream_t>(stream);
   if (g.vec == 1) {

@@ -230,11 +230,9 @@ static int dispatch(const Args& a, hipStream_t st) {
       vec_ok ? (r ? &kernel_of<E, EW, ES, V, FP8, true> : &kernel_of<E, EW, ES, V, FP8, false>)
              : (r ? &kernel_of<E, EW, ES, 1, FP8, true> : &kernel_of<E, EW, ES, 1, FP8, false>);
   Geometry g;
-  if (!choose_geometry("rms_norm_smooth_quant", a.rows, a.hidden, vec_ok ? V : 1, kernels, &g)) {
-    return set_error(MCOP_E_UNSUPPORTED,
-                     "rms_norm_dynamic_per_token_quant (smooth): hidden_size %d is larger than "
-                     "the register-resident kernels support",
-                     a.hidden);
+  if (!choose_geometry("rms_norm_dynamic_per_token_quant (smooth)", a.rows, a.hidden,
+                       vec_ok ? V : 1, kernels, &g)) {
+    return MCOP_E_UNSUPPORTED;
   }
   const bool has_res = a.res != nullptr;
   if (g.vec == 1) {
