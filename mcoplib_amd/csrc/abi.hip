@@ -110,6 +110,32 @@ static bool valid_tpr(int64_t t, int min_tpr) {
   return (t >= min_tpr && (t == 16 || t == 32)) || (t > 0 && t % 64 == 0);
 }
 
+bool row_fits(int64_t hidden, int vec, int min_tpr) {
+  static const int kVecNv[] = {1, 2, 4, 8, 16};
+  static const int kScalarNv[] = {4, 16};
+  const int64_t nvec = hidden / vec;
+  const int* cands = vec > 1 ? kVecNv : kScalarNv;
+  const int ncand = vec > 1 ? 5 : 2;
+  for (int c = 0; c < ncand; ++c) {
+    if (row_lanes(ceil_div(nvec, cands[c]), min_tpr) <= max_tpr(vec, cands[c])) return true;
+  }
+  return false;
+}
+
+bool wide_rows_ok(const char* op, int64_t rows) {
+  if (rows > 0x7fffffffLL) {
+    set_error(MCOP_E_UNSUPPORTED, "%s: %lld rows need more than the 2147483647 workgroups one "
+              "launch allows", op, (long long)rows);
+    return false;
+  }
+  if (trace_enabled()) {
+    fprintf(stdout, "[mcop] %s rows=%lld: multi-pass kernel, one %d-lane workgroup per row\n",
+            op, (long long)rows, kWideLanes);
+    fflush(stdout);
+  }
+  return true;
+}
+
 bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, KernelOfNv kernels,
                      Geometry* g, int min_tpr, bool wide_nv4) {
   const int64_t nvec = hidden / vec;

@@ -7,6 +7,9 @@
 //   x <- b(b(z * rho) * w)                            (:136-143: scale then weight multiply)
 // One pass over HBM: x, residual and weight are loaded once into VGPRs, residual is written
 // from registers before the reduction, x after it (8*H bytes per bf16 row, plus the weight).
+// Rows too wide for the registers take k_fused_add_rms_norm_wide: one 1024-lane workgroup per
+// row and two passes over the row (sum of squares; then residual and output), the second
+// re-reading x and residual, which each lane then overwrites at the same addresses.
 #include <hip/hip_runtime.h>
 
 #include "../../include/mcop_norm.h"
@@ -77,6 +80,44 @@ k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
 }
 
 template <class E, int VEC>
+__global__ void __launch_bounds__(kWideLanes)
+k_fused_add_rms_norm_wide(typename E::S* __restrict__ x, int64_t x_stride,
+                          typename E::S* __restrict__ res, const typename E::S* __restrict__ w,
+                          int hidden, float eps) {
+  using S = typename E::S;
+  __shared__ double red_sum[16];
+  const int nvec = hidden / VEC;
+  S* xr = x + (int64_t)blockIdx.x * x_stride;
+  S* rr = res + (int64_t)blockIdx.x * hidden;
+  double ss = 0.0;
+  for (int j = threadIdx.x; j < nvec; j += blockDim.x) {
+    const Pack<S, VEC> xv = ld<S, VEC>(xr + (int64_t)j * VEC);
+    const Pack<S, VEC> rv = ld<S, VEC>(rr + (int64_t)j * VEC);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const double d = (double)rnd<E>(E::to_f(xv.v[e]) + E::to_f(rv.v[e]));
+      ss = __builtin_fma(d, d, ss);
+    }
+  }
+  ss = row_reduce(ss, red_sum, (int)blockDim.x, SumOp());
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+  for (int j = threadIdx.x; j < nvec; j += blockDim.x) {
+    const int64_t o = (int64_t)j * VEC;
+    const Pack<S, VEC> xv = ld<S, VEC>(xr + o);
+    const Pack<S, VEC> rv = ld<S, VEC>(rr + o);
+    const Pack<S, VEC> wv = ld<S, VEC>(w + o);
+    Pack<S, VEC> zo, yo;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      zo.v[e] = E::from_f(E::to_f(xv.v[e]) + E::to_f(rv.v[e]));
+      yo.v[e] = E::from_f(rnd<E>(E::to_f(zo.v[e]) * rho) * E::to_f(wv.v[e]));
+    }
+    st<S, VEC>(rr + o, zo);
+    st<S, VEC>(xr + o, yo);
+  }
+}
+
+template <class E, int VEC>
 static void launch_nv(const Geometry& g, void* x, int64_t xs, void* res, const void* w,
                       int64_t rows, int hidden, float eps, hipStream_t st) {
   using S = typename E::S;
@@ -122,6 +163,21 @@ static int dispatch(void* x, int64_t xs, void* res, const void* w, int64_t rows,
                     float eps, hipStream_t st) {
   constexpr int V = E::VEC;
   const bool vec_ok = hidden % V == 0 && xs % V == 0 && aligned(16, x, res, w);
+  if (!row_fits(hidden, vec_ok ? V : 1)) {
+    if (!wide_rows_ok("fused_add_rms_norm", rows)) return MCOP_E_UNSUPPORTED;
+    using S = typename E::S;
+    auto* xp = static_cast<S*>(x);
+    auto* rp = static_cast<S*>(res);
+    auto* wp = static_cast<const S*>(w);
+    if (vec_ok) {
+      hipLaunchKernelGGL((k_fused_add_rms_norm_wide<E, V>), dim3((unsigned)rows),
+                         dim3(kWideLanes), 0, st, xp, xs, rp, wp, (int)hidden, eps);
+    } else {
+      hipLaunchKernelGGL((k_fused_add_rms_norm_wide<E, 1>), dim3((unsigned)rows),
+                         dim3(kWideLanes), 0, st, xp, xs, rp, wp, (int)hidden, eps);
+    }
+    return check_launch("fused_add_rms_norm");
+  }
   Geometry g;
   if (!choose_geometry("fused_add_rms_norm", rows, hidden, vec_ok ? V : 1, vec_ok ? &kernel_of<E, V> : &kernel_of<E, 1>,
                        &g)) {

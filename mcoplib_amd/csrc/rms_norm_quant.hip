@@ -36,6 +36,52 @@ namespace mcop {
 
 enum QuantMode { QM_VLLM = 0, QM_MC = 1, QM_MC_7168 = 2 };
 
+// The row's scale from its absmax (and rho for QM_MC_7168); *A receives the absmax after the
+// scale bound.
+template <bool FP8, int MODE>
+__device__ __forceinline__ float row_scale(float amax, float rho, const float* scale_ub,
+                                           float* A) {
+  float a = amax;
+  if (MODE != QM_MC_7168 && scale_ub != nullptr) a = __builtin_fminf(a, *scale_ub);
+  *A = a;
+  if constexpr (FP8) {
+    return __builtin_fmaxf(mcop_div_rn(a, 448.0f), 1.0f / 229376.0f);
+  } else if constexpr (MODE == QM_MC_7168) {
+    return __builtin_fmaxf(mcop_div_rn(a * rho, 127.0f), FLT_EPSILON);
+  } else {
+    return __builtin_fmaxf(mcop_div_rn(a, 127.0f), MODE == QM_MC ? 1.5e-6f : FLT_EPSILON);
+  }
+}
+
+// Codes of one vector of y (of p = a * w for QM_MC_7168).  `bounded`: no scale bound cut the
+// row's absmax; `has_ub`: a scale bound was given.
+template <class E, int VEC, bool FP8, int MODE>
+__device__ __forceinline__ Pack<uint8_t, VEC> row_codes(const float* y, float rho, float s,
+                                                        float inv, bool s_ok, bool bounded,
+                                                        bool has_ub) {
+  Pack<uint8_t, VEC> q;
+  constexpr int LO = MODE == QM_VLLM ? -128 : -127;
+  if constexpr (FP8) {
+    q = fp8_quotient_codes<VEC>(y, s, inv, s_ok, bounded);
+  } else if (std::is_same_v<E, F32> || (MODE != QM_MC_7168 && has_ub)) {
+    // fp32 inputs can carry NaN payloads in the low byte, and a scale bound lets |y * inv|
+    // exceed 127: round, convert and saturate
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float t = MODE == QM_MC_7168 ? y[e] * rho : y[e];
+      q.v[e] = q_i8<LO>(t * inv);
+    }
+  } else {
+    // |t * inv| < 127.5: the code cannot saturate (nor reach -128)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float t = MODE == QM_MC_7168 ? y[e] * rho : y[e];
+      q.v[e] = q_i8_in_range(t, inv);
+    }
+  }
+  return q;
+}
+
 template <class E, int VEC, int NV, bool FP8, bool RES, int MODE>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
 k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
@@ -119,16 +165,8 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   }
   amax = row_reduce(amax, red_max, tpr, MaxOp());
 
-  float A = amax;
-  if (MODE != QM_MC_7168 && scale_ub != nullptr) A = __builtin_fminf(A, *scale_ub);
-  float s;
-  if constexpr (FP8) {
-    s = __builtin_fmaxf(mcop_div_rn(A, 448.0f), 1.0f / 229376.0f);
-  } else if constexpr (MODE == QM_MC_7168) {
-    s = __builtin_fmaxf(mcop_div_rn(A * rho, 127.0f), FLT_EPSILON);
-  } else {
-    s = __builtin_fmaxf(mcop_div_rn(A, 127.0f), MODE == QM_MC ? 1.5e-6f : FLT_EPSILON);
-  }
+  float A;
+  const float s = row_scale<FP8, MODE>(amax, rho, scale_ub, &A);
   if (p.live && p.lt == 0) scales[p.row] = s;
   const float inv = mcop_div_rn(1.0f, s);
   const bool s_ok = mcop_divisor_ok(s);
@@ -138,28 +176,83 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
     if (p.live && j < nvec) {
-      Pack<uint8_t, VEC> q;
-      constexpr int LO = MODE == QM_VLLM ? -128 : -127;
-      if constexpr (FP8) {
-        q = fp8_quotient_codes<VEC>(a[v], s, inv, s_ok, bounded);
-      } else if (std::is_same_v<E, F32> || (MODE != QM_MC_7168 && scale_ub != nullptr)) {
-        // fp32 inputs can carry NaN payloads in the low byte, and a scale bound lets |y * inv|
-        // exceed 127: round, convert and saturate
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float t = MODE == QM_MC_7168 ? a[v][e] * rho : a[v][e];
-          q.v[e] = q_i8<LO>(t * inv);
-        }
-      } else {
-        // |t * inv| < 127.5: the code cannot saturate (nor reach -128)
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          const float t = MODE == QM_MC_7168 ? a[v][e] * rho : a[v][e];
-          q.v[e] = q_i8_in_range(t, inv);
-        }
-      }
+      const Pack<uint8_t, VEC> q =
+          row_codes<E, VEC, FP8, MODE>(a[v], rho, s, inv, s_ok, bounded, scale_ub != nullptr);
       st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
     }
+  }
+}
+
+// Rows too wide for the registers (QM_VLLM and QM_MC; QM_MC_7168 rows always fit): one
+// 1024-lane workgroup per row and three passes over it -- sum of squares; absmax of y; codes and
+// the residual -- each re-reading x and residual (the residual is written in the last pass
+// only, by the lane that read it, as the reference's multi-pass kernels do).
+template <class E, int VEC, bool FP8, bool RES, int MODE>
+__global__ void __launch_bounds__(kWideLanes)
+k_rms_norm_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
+                      const typename E::S* __restrict__ x, const typename E::S* __restrict__ w,
+                      const float* __restrict__ scale_ub, typename E::S* __restrict__ res,
+                      int hidden, float eps) {
+  static_assert(MODE != QM_MC_7168, "7168-wide rows fit the register-resident kernel");
+  using S = typename E::S;
+  __shared__ double red_sum[16];
+  __shared__ float red_max[16];
+  const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x;
+  const int64_t base = (int64_t)blockIdx.x * hidden;
+  auto a_of = [&](int64_t o, float* a) {
+    const Pack<S, VEC> xv = ld<S, VEC>(x + base + o);
+    Pack<S, VEC> rv;
+    if constexpr (RES) rv = ld<S, VEC>(res + base + o);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      a[e] = E::to_f(xv.v[e]);
+      if constexpr (RES) a[e] += E::to_f(rv.v[e]);
+    }
+  };
+  double ss = 0.0;
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    float a[VEC];
+    a_of((int64_t)j * VEC, a);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) ss = __builtin_fma((double)a[e], (double)a[e], ss);
+  }
+  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+  auto y_of = [&](int64_t o, const float* a, float* y) {
+    const Pack<S, VEC> wv = ld<S, VEC>(w + o);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) y[e] = rnd<E>(rnd<E>(a[e] * rho) * E::to_f(wv.v[e]));
+  };
+  float amax = 0.0f;
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    float a[VEC], y[VEC];
+    a_of((int64_t)j * VEC, a);
+    y_of((int64_t)j * VEC, a, y);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) amax = __builtin_fmaxf(amax, __builtin_fabsf(y[e]));
+  }
+  amax = row_reduce(amax, red_max, tpr, MaxOp());
+  float A;
+  const float s = row_scale<FP8, MODE>(amax, rho, scale_ub, &A);
+  if (threadIdx.x == 0) scales[blockIdx.x] = s;
+  const float inv = mcop_div_rn(1.0f, s);
+  const bool s_ok = mcop_divisor_ok(s);
+  const bool bounded = A == amax && s <= 0x1p100f;
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    const int64_t o = (int64_t)j * VEC;
+    float a[VEC], y[VEC];
+    a_of(o, a);
+    if constexpr (RES) {
+      Pack<S, VEC> r;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) r.v[e] = E::from_f(a[e]);
+      st<S, VEC>(res + base + o, r);
+    }
+    y_of(o, a, y);
+    st<uint8_t, VEC>(out + base + o,
+                     row_codes<E, VEC, FP8, MODE>(y, rho, s, inv, s_ok, bounded,
+                                                  scale_ub != nullptr));
   }
 }
 
@@ -212,6 +305,27 @@ static int dispatch(const char* name, void* out, float* scales, const void* x, c
                     hipStream_t st) {
   constexpr int V = E::VEC;
   const bool vec_ok = hidden % V == 0 && aligned(16, x, w, res) && aligned(V, out);
+  if constexpr (MODE != QM_MC_7168) {
+    if (!row_fits(hidden, vec_ok ? V : 1)) {
+      if (!wide_rows_ok(name, rows)) return MCOP_E_UNSUPPORTED;
+      using S = typename E::S;
+      auto* o = static_cast<uint8_t*>(out);
+      auto* xp = static_cast<const S*>(x);
+      auto* wp = static_cast<const S*>(w);
+      auto* rp = static_cast<S*>(res);
+      const dim3 grid((unsigned)rows), block(kWideLanes);
+#define MCOP_WIDE(VV, RR)                                                                     \
+  hipLaunchKernelGGL((k_rms_norm_quant_wide<E, VV, FP8, RR, MODE>), grid, block, 0, st, o,     \
+                     scales, xp, wp, scale_ub, rp, (int)hidden, eps)
+      if (vec_ok) {
+        if (res) MCOP_WIDE(V, true); else MCOP_WIDE(V, false);
+      } else {
+        if (res) MCOP_WIDE(1, true); else MCOP_WIDE(1, false);
+      }
+#undef MCOP_WIDE
+      return check_launch(name);
+    }
+  }
   const KernelOfNv kernels =
       vec_ok ? (res ? &kernel_of<E, V, FP8, true, MODE> : &kernel_of<E, V, FP8, false, MODE>)
              : (res ? &kernel_of<E, 1, FP8, true, MODE> : &kernel_of<E, 1, FP8, false, MODE>);

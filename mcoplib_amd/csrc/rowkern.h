@@ -396,6 +396,15 @@ using KernelOfNv = const void* (*)(int nv);
 bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, KernelOfNv kernels,
                      Geometry* g, int min_tpr = 16, bool wide_nv4 = true);
 
+// True when a row of `hidden` elements fits the register-resident kernels at vector width `vec`
+// (some vectors-per-lane candidate holds it within its lanes-per-row limit).
+bool row_fits(int64_t hidden, int vec, int min_tpr = 16);
+
+// Launch check of the multi-pass kernels for rows too wide for the register-resident ones
+// (one 1024-lane workgroup per row): false, with the message set, beyond 2^31 - 1 rows.
+bool wide_rows_ok(const char* op, int64_t rows);
+constexpr int kWideLanes = 1024;
+
 // True when every non-null pointer is aligned to `bytes`.
 bool aligned(int bytes, const void* p0, const void* p1 = nullptr, const void* p2 = nullptr,
              const void* p3 = nullptr, const void* p4 = nullptr, const void* p5 = nullptr);

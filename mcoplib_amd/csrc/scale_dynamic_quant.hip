@@ -81,6 +81,44 @@ k_scale_dynamic_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   }
 }
 
+// Rows too wide for the registers: one 1024-lane workgroup per row and two passes over it
+// (absmax; codes), the second re-reading the row and the smooth scales.
+template <int VEC>
+__global__ void __launch_bounds__(kWideLanes)
+k_scale_dynamic_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
+                           const uint16_t* __restrict__ x, const float* __restrict__ sm,
+                           int hidden) {
+  __shared__ float red_max[16];
+  const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x;
+  const int64_t base = (int64_t)blockIdx.x * hidden;
+  auto v_of = [&](int64_t o, float* v) {
+    const Pack<uint16_t, VEC> xv = ld<uint16_t, VEC>(x + base + o);
+    const Pack<float, VEC> sv = ld<float, VEC>(sm + o);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) v[e] = BF16::to_f(xv.v[e]) * sv.v[e];
+  };
+  float amax = 0.0f;
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    float v[VEC];
+    v_of((int64_t)j * VEC, v);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[e]));
+  }
+  amax = row_reduce(amax, red_max, tpr, MaxOp());
+  if (threadIdx.x == 0) scales[blockIdx.x] = amax * 0.00787401574803f;
+  const float inv = amax > 0.0f ? mcop_div_rn(127.0f, amax) : 0.0f;
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    const int64_t o = (int64_t)j * VEC;
+    float v[VEC];
+    v_of(o, v);
+    Pack<uint8_t, VEC> q;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(v[e] * inv);
+    st<uint8_t, VEC>(out + base + o, q);
+  }
+}
+
 // Two rows per lane when the vector path has at least 2048 rows and at most four vectors per
 // lane (more would spill); one otherwise (fewer rows: every row is already in flight).
 static int rows_per_lane(const Geometry& g, int64_t rows) {
@@ -159,12 +197,25 @@ extern "C" int mcop_scale_dynamic_quant(int8_t* out, float* scales, const void* 
   }
   constexpr int V = BF16::VEC;
   const bool vec_ok = hidden_size % V == 0 && aligned(16, input, smooth) && aligned(V, out);
+  auto st = static_cast<hipStream_t>(stream);
+  if (!row_fits(hidden_size, vec_ok ? V : 1)) {
+    if (!wide_rows_ok("scale_dynamic_quant", num_tokens)) return MCOP_E_UNSUPPORTED;
+    auto* o = reinterpret_cast<uint8_t*>(out);
+    auto* xp = static_cast<const uint16_t*>(input);
+    if (vec_ok) {
+      hipLaunchKernelGGL((k_scale_dynamic_quant_wide<V>), dim3((unsigned)num_tokens),
+                         dim3(kWideLanes), 0, st, o, scales, xp, smooth, (int)hidden_size);
+    } else {
+      hipLaunchKernelGGL((k_scale_dynamic_quant_wide<1>), dim3((unsigned)num_tokens),
+                         dim3(kWideLanes), 0, st, o, scales, xp, smooth, (int)hidden_size);
+    }
+    return check_launch("scale_dynamic_quant");
+  }
   Geometry g;
   if (!choose_geometry("scale_dynamic_quant", num_tokens, hidden_size, vec_ok ? V : 1,
                        vec_ok ? &kernel_of<V> : &kernel_of<1>, &g)) {
     return MCOP_E_UNSUPPORTED;
   }
-  auto st = static_cast<hipStream_t>(stream);
   if (g.vec == 1) {
     launch_nv<1>(g, out, scales, input, smooth, num_tokens, (int)hidden_size, st);
   } else {

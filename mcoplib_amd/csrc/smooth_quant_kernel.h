@@ -158,6 +158,106 @@ k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
                                         eps, flags, red_sum, red_max);
 }
 
+// Rows too wide for the registers: one 1024-lane workgroup per row and three passes over it --
+// sum of squares; absmax of v; after_res, after_norm and the codes -- each re-reading x (and
+// the residual, which this operator only reads), weight and smooth.
+template <class E, class EW, class ES, int VEC, bool FP8, bool RES>
+__global__ void __launch_bounds__(kWideLanes)
+k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
+                             const typename E::S* __restrict__ x,
+                             const typename EW::S* __restrict__ w,
+                             const typename ES::S* __restrict__ sm,
+                             typename E::S* __restrict__ ares, typename E::S* __restrict__ anorm,
+                             const typename E::S* __restrict__ res, int hidden, float eps,
+                             uint32_t flags) {
+  using S = typename E::S;
+  __shared__ double red_sum[16];
+  __shared__ float red_max[16];
+  const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x;
+  const int64_t base = (int64_t)blockIdx.x * hidden;
+  auto t_of = [&](int64_t o, float* t) {  // a = x (+ r), unrounded
+    const Pack<S, VEC> xv = ld<S, VEC>(x + base + o);
+    Pack<S, VEC> rv;
+    if constexpr (RES) rv = ld<S, VEC>(res + base + o);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      t[e] = E::to_f(xv.v[e]);
+      if constexpr (RES) t[e] += E::to_f(rv.v[e]);
+    }
+  };
+  double ss = 0.0;
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    float t[VEC];
+    t_of((int64_t)j * VEC, t);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) ss = __builtin_fma((double)t[e], (double)t[e], ss);
+  }
+  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+  const float inv_rho = mcop_div_rn(1.0f, rho);
+  const bool rho_ok = mcop_divisor_ok(rho);
+  const bool standard = (flags & MCOP_SQ_STANDARD_NORM) != 0;
+  // u = (b(a) / rho) * w (or (b(a) * rho) * w), v = u * smooth
+  auto uv_of = [&](int64_t o, const float* t, float* u, float* v) {
+    float a[VEC], n[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) a[e] = rnd<E>(t[e]);
+    if (standard) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) n[e] = a[e] * rho;
+    } else {
+      div_by_const<VEC>(n, a, rho, inv_rho, rho_ok);
+    }
+    WVec<EW, VEC> wv;
+    WVec<ES, VEC> sv;
+    wv.p = ld<typename EW::S, VEC>(w + o);
+    sv.p = ld<typename ES::S, VEC>(sm + o);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      u[e] = n[e] * wv.at(e);
+      v[e] = u[e] * sv.at(e);
+    }
+  };
+  float amax = 0.0f;
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    float t[VEC], u[VEC], v[VEC];
+    t_of((int64_t)j * VEC, t);
+    uv_of((int64_t)j * VEC, t, u, v);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[e]));
+  }
+  amax = row_reduce(amax, red_max, tpr, MaxOp());
+  const float s = mcop_div_rn(amax, FP8 ? 448.0f : 127.0f);
+  if (threadIdx.x == 0) scales[blockIdx.x] = s;
+  const float inv = amax > 0.0f ? mcop_div_rn(1.0f, s) : 0.0f;
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    const int64_t o = (int64_t)j * VEC;
+    float t[VEC], u[VEC], v[VEC];
+    t_of(o, t);
+    uv_of(o, t, u, v);
+    Pack<S, VEC> ar, an;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      ar.v[e] = E::from_f(t[e]);
+      an.v[e] = E::from_f(u[e]);
+    }
+    if (ares != nullptr) st<S, VEC>(ares + base + o, ar);
+    if (anorm != nullptr) st<S, VEC>(anorm + base + o, an);
+    Pack<uint8_t, VEC> q;
+    if constexpr (FP8) {
+      float c[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) c[e] = clamp_fp8(v[e] * inv);
+      q = cvt_fp8<VEC>(c);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-127>(v[e] * inv);
+    }
+    st<uint8_t, VEC>(out + base + o, q);
+  }
+}
+
 struct Args {
   void* out;
   float* scales;
@@ -226,6 +326,29 @@ static int dispatch(const Args& a, hipStream_t st) {
   const bool vec_ok = a.hidden % V == 0 && aligned(16, a.x, a.ares, a.anorm, a.res) &&
                       aligned(WB, a.w) && aligned(SB, a.sm) && aligned(V, a.out);
   const bool r = a.res != nullptr;
+  if (!row_fits(a.hidden, vec_ok ? V : 1)) {
+    const char* name = "rms_norm_dynamic_per_token_quant (smooth)";
+    if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
+    using S = typename E::S;
+    auto* o = static_cast<uint8_t*>(a.out);
+    auto* xp = static_cast<const S*>(a.x);
+    auto* wp = static_cast<const typename EW::S*>(a.w);
+    auto* sp = static_cast<const typename ES::S*>(a.sm);
+    auto* arp = static_cast<S*>(a.ares);
+    auto* anp = static_cast<S*>(a.anorm);
+    auto* rp = static_cast<const S*>(a.res);
+    const dim3 grid((unsigned)a.rows), block(kWideLanes);
+#define MCOP_WIDE(VV, RR)                                                                      \
+  hipLaunchKernelGGL((k_rms_norm_smooth_quant_wide<E, EW, ES, VV, FP8, RR>), grid, block, 0,   \
+                     st, o, a.scales, xp, wp, sp, arp, anp, rp, a.hidden, a.eps, a.flags)
+    if (vec_ok) {
+      if (r) MCOP_WIDE(V, true); else MCOP_WIDE(V, false);
+    } else {
+      if (r) MCOP_WIDE(1, true); else MCOP_WIDE(1, false);
+    }
+#undef MCOP_WIDE
+    return check_launch(name);
+  }
   const KernelOfNv kernels =
       vec_ok ? (r ? &kernel_of<E, EW, ES, V, FP8, true> : &kernel_of<E, EW, ES, V, FP8, false>)
              : (r ? &kernel_of<E, EW, ES, 1, FP8, true> : &kernel_of<E, EW, ES, 1, FP8, false>);
