@@ -41,6 +41,30 @@ __device__ __forceinline__ float group_max(float v, int lanes) {
   return v;
 }
 
+// Scale (*s) and codes of one vector of y in a group whose absmax is m.
+template <class E, int VEC, bool FP8>
+__device__ __forceinline__ Pack<uint8_t, VEC> group_codes(const float* y, float m, bool has_ub,
+                                                          float ub, float* s_out) {
+  const float A = has_ub ? __builtin_fminf(m, ub) : m;
+  const float s = FP8 ? __builtin_fmaxf(mcop_div_rn(A, 448.0f), 1.0f / 229376.0f)
+                      : __builtin_fmaxf(mcop_div_rn(A, 127.0f), FLT_EPSILON);
+  *s_out = s;
+  const float inv = mcop_div_rn(1.0f, s);
+  Pack<uint8_t, VEC> q;
+  if constexpr (FP8) {
+    const bool bounded = A == m && s <= 0x1p100f;
+    q = fp8_quotient_codes<VEC>(y, s, inv, mcop_divisor_ok(s), bounded);
+  } else if constexpr (std::is_same_v<E, F32>) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(y[e] * inv);
+  } else {
+    // |y * inv| <= 127 * (1 + 2^-22) < 127.5 (int8 takes no scale bound)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) q.v[e] = q_i8_in_range(y[e], inv);
+  }
+  return q;
+}
+
 template <class E, int VEC, int NV, bool FP8, bool RES>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
 k_rms_norm_group_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
@@ -126,27 +150,97 @@ k_rms_norm_group_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   for (int v = 0; v < NV; ++v) {
     const int j = index(v);
     if (!(p.live && j < nvec)) continue;
-    const float A = scale_ub != nullptr ? __builtin_fminf(m[v], ub) : m[v];
-    const float s = FP8 ? __builtin_fmaxf(mcop_div_rn(A, 448.0f), 1.0f / 229376.0f)
-                        : __builtin_fmaxf(mcop_div_rn(A, 127.0f), FLT_EPSILON);
-    const int g = (int)(((int64_t)j * VEC) / group);
+    float s;
+    const Pack<uint8_t, VEC> q = group_codes<E, VEC, FP8>(a[v], m[v], scale_ub != nullptr, ub, &s);
     if ((((int64_t)j * VEC) % group) == 0) {
+      const int g = (int)(((int64_t)j * VEC) / group);
       scales[p.row * scale_row_stride + (int64_t)g * scale_group_stride] = s;
     }
-    const float inv = mcop_div_rn(1.0f, s);
-    Pack<uint8_t, VEC> q;
-    if constexpr (FP8) {
-      const bool bounded = A == m[v] && s <= 0x1p100f;
-      q = fp8_quotient_codes<VEC>(a[v], s, inv, mcop_divisor_ok(s), bounded);
-    } else if constexpr (std::is_same_v<E, F32>) {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(a[v][e] * inv);
-    } else {
-      // |y * inv| <= 127 * (1 + 2^-22) < 127.5 (int8 takes no scale bound)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) q.v[e] = q_i8_in_range(a[v][e], inv);
-    }
     st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
+  }
+}
+
+// Rows too wide for the registers: one 1024-lane workgroup per row, two passes (sum of squares;
+// codes, scales and the residual), the second re-reading x, residual and weight; the residual
+// is written in the last pass only, by the lane that read it.  A lane takes U consecutive
+// elements per step (one 16-byte vector, or four scalars on the scalar path), so a group spans
+// group / U aligned lanes (<= 64) and 1024 lanes hold whole groups.
+template <class E, int U, bool VECLD, bool FP8, bool RES>
+__global__ void __launch_bounds__(kWideLanes)
+k_rms_norm_group_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
+                            const typename E::S* __restrict__ x,
+                            const typename E::S* __restrict__ w,
+                            const float* __restrict__ scale_ub, typename E::S* __restrict__ res,
+                            int hidden, float eps, int group, int64_t scale_row_stride,
+                            int64_t scale_group_stride) {
+  using S = typename E::S;
+  __shared__ double red_sum[16];
+  const int nunit = hidden / U;
+  const int tpr = (int)blockDim.x;
+  const int64_t base = (int64_t)blockIdx.x * hidden;
+  auto load = [&](const S* p, float* f) {
+    if constexpr (VECLD) {
+      const Pack<S, U> v = ld<S, U>(p);
+#pragma unroll
+      for (int e = 0; e < U; ++e) f[e] = E::to_f(v.v[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < U; ++e) f[e] = E::to_f(p[e]);
+    }
+  };
+  auto t_of = [&](int64_t o, float* t) {
+    load(x + base + o, t);
+    if constexpr (RES) {
+      float r[U];
+      load(res + base + o, r);
+#pragma unroll
+      for (int e = 0; e < U; ++e) t[e] += r[e];
+    }
+  };
+  double ss = 0.0;
+  for (int j = threadIdx.x; j < nunit; j += tpr) {
+    float t[U];
+    t_of((int64_t)j * U, t);
+#pragma unroll
+    for (int e = 0; e < U; ++e) ss = __builtin_fma((double)t[e], (double)t[e], ss);
+  }
+  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+  const float ub = scale_ub != nullptr ? *scale_ub : 0.0f;
+  for (int j = threadIdx.x; j < nunit; j += tpr) {
+    const int64_t o = (int64_t)j * U;
+    float t[U], wf[U], y[U];
+    t_of(o, t);
+    load(w + o, wf);
+    float m = 0.0f;
+#pragma unroll
+    for (int e = 0; e < U; ++e) {
+      y[e] = rnd<E>(rnd<E>(t[e] * rho) * wf[e]);
+      m = __builtin_fmaxf(m, __builtin_fabsf(y[e]));
+    }
+    m = group_max(m, group / U);
+    float s;
+    const Pack<uint8_t, U> q = group_codes<E, U, FP8>(y, m, scale_ub != nullptr, ub, &s);
+    if (o % group == 0) {
+      scales[(int64_t)blockIdx.x * scale_row_stride + (o / group) * scale_group_stride] = s;
+    }
+    if constexpr (RES) {
+      Pack<S, U> r;
+#pragma unroll
+      for (int e = 0; e < U; ++e) r.v[e] = E::from_f(t[e]);
+      if constexpr (VECLD) {
+        st<S, U>(res + base + o, r);
+      } else {
+#pragma unroll
+        for (int e = 0; e < U; ++e) res[base + o + e] = r.v[e];
+      }
+    }
+    if constexpr (VECLD) {
+      st<uint8_t, U>(out + base + o, q);
+    } else {
+#pragma unroll
+      for (int e = 0; e < U; ++e) out[base + o + e] = q.v[e];
+    }
   }
 }
 
@@ -212,6 +306,25 @@ static int dispatch(const GqArgs& a, hipStream_t st) {
   const char* name = "rms_norm_per_block_quant";
   constexpr int V = E::VEC;
   const bool vec_ok = a.hidden % V == 0 && aligned(16, a.x, a.w, a.res) && aligned(V, a.out);
+  if (!row_fits(a.hidden, vec_ok ? V : 1, 64)) {
+    if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
+    using S = typename E::S;
+    auto* o = static_cast<uint8_t*>(a.out);
+    auto* xp = static_cast<const S*>(a.x);
+    auto* wp = static_cast<const S*>(a.w);
+    auto* rp = static_cast<S*>(a.res);
+    const dim3 grid((unsigned)a.rows), block(kWideLanes);
+#define MCOP_WIDE(UU, VL, RR)                                                                 \
+  hipLaunchKernelGGL((k_rms_norm_group_quant_wide<E, UU, VL, FP8, RR>), grid, block, 0, st, o, \
+                     a.scales, xp, wp, a.scale_ub, rp, a.hidden, a.eps, a.group, a.srow, a.sgrp)
+    if (vec_ok) {
+      if (a.res) MCOP_WIDE(V, true, true); else MCOP_WIDE(V, true, false);
+    } else {
+      if (a.res) MCOP_WIDE(4, false, true); else MCOP_WIDE(4, false, false);
+    }
+#undef MCOP_WIDE
+    return check_launch(name);
+  }
   const KernelOfNv kernels =
       vec_ok ? (a.res ? &kernel_of<E, V, FP8, true> : &kernel_of<E, V, FP8, false>)
              : (a.res ? &kernel_of<E, 1, FP8, true> : &kernel_of<E, 1, FP8, false>);

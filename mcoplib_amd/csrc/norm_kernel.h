@@ -74,6 +74,30 @@ struct NormW {
   __device__ __forceinline__ float at(int e) const { return EW::to_f(p.v[e]); }
 };
 
+// The normalized output of one vector from a (x [+ r], or b(x + r) for the element-wise chain
+// with a residual).
+template <class E, class EW, int VEC>
+__device__ __forceinline__ Pack<typename E::S, VEC> norm_out(const float* a,
+                                                             const NormW<EW, VEC>& w, float rho,
+                                                             float inv_rho, int mode,
+                                                             int rms_div) {
+  Pack<typename E::S, VEC> o;
+  if (mode == NORM_VLLM) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(rnd<E>(a[e] * rho) * w.at(e));
+  } else if (mode == NORM_MC || !rms_div) {
+    const float d = (mode == NORM_MC && rms_div) ? inv_rho : rho;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f((a[e] * d) * w.at(e));
+  } else {
+    float n[VEC];
+    div_by_const<VEC>(n, a, rho, inv_rho, mcop_divisor_ok(rho));
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(n[e] * w.at(e));
+  }
+  return o;
+}
+
 template <class E, class EW, int VEC, int NV, bool RES>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
 k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
@@ -138,21 +162,62 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
     if (!(p.live && j < nvec)) continue;
-    Pack<S, VEC> o;
-    if (mode == NORM_VLLM) {
+    st_nt<S, VEC>(out + out_base + (int64_t)j * VEC,
+                  norm_out<E, EW, VEC>(a[v], wv[v], rho, inv_rho, mode, rms_div));
+  }
+}
+
+// Rows too wide for the registers: one 1024-lane workgroup per row, two passes (sum of squares;
+// after_res and the output), the second re-reading x, residual and weight.
+template <class E, class EW, int VEC, bool RES>
+__global__ void __launch_bounds__(kWideLanes)
+k_rms_norm_wide(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
+                const typename E::S* __restrict__ x, const typename EW::S* __restrict__ w,
+                const typename E::S* __restrict__ res, RowMap map, int hidden, float eps,
+                int mode, int rms_div) {
+  using S = typename E::S;
+  __shared__ double red_sum[16];
+  const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x;
+  const RowOffsets lo = row_offsets(map, blockIdx.x);
+  const int64_t rbase = (int64_t)blockIdx.x * hidden;
+  auto t_of = [&](int64_t o, float* t) {
+    const Pack<S, VEC> xv = ld<S, VEC>(x + lo.in + o);
+    Pack<S, VEC> rv;
+    if constexpr (RES) rv = ld<S, VEC>(res + rbase + o);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(rnd<E>(a[v][e] * rho) * wv[v].at(e));
-    } else if (mode == NORM_MC || !rms_div) {
-      const float d = (mode == NORM_MC && rms_div) ? inv_rho : rho;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f((a[v][e] * d) * wv[v].at(e));
-    } else {
-      float n[VEC];
-      div_by_const<VEC>(n, a[v], rho, inv_rho, mcop_divisor_ok(rho));
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(n[e] * wv[v].at(e));
+    for (int e = 0; e < VEC; ++e) {
+      t[e] = E::to_f(xv.v[e]);
+      if constexpr (RES) t[e] += E::to_f(rv.v[e]);
     }
-    st_nt<S, VEC>(out + out_base + (int64_t)j * VEC, o);
+  };
+  double ss = 0.0;
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    float t[VEC];
+    t_of((int64_t)j * VEC, t);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) ss = __builtin_fma((double)t[e], (double)t[e], ss);
+  }
+  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+  const float inv_rho = mcop_div_rn(1.0f, rho);
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    const int64_t o = (int64_t)j * VEC;
+    float t[VEC];
+    t_of(o, t);
+    if constexpr (RES) {
+      Pack<S, VEC> r;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        r.v[e] = E::from_f(t[e]);
+        // the element-wise kernels re-read the rounded after_res
+        if (mode == NORM_MC_GENERIC) t[e] = E::to_f(r.v[e]);
+      }
+      st<S, VEC>(ares + rbase + o, r);
+    }
+    NormW<EW, VEC> wv;
+    wv.p = ld<typename EW::S, VEC>(w + lo.w + o);
+    st<S, VEC>(out + lo.out + o, norm_out<E, EW, VEC>(t, wv, rho, inv_rho, mode, rms_div));
   }
 }
 
@@ -229,6 +294,26 @@ static int norm_dispatch(const char* name, const NormArgs& a, hipStream_t st) {
   constexpr int V = E::VEC;
   const bool vec_ok = norm_vec_ok<E, EW>(a);
   const bool r = a.res != nullptr;
+  if (!row_fits(a.hidden, vec_ok ? V : 1)) {
+    if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
+    using S = typename E::S;
+    auto* o = static_cast<S*>(a.out);
+    auto* arp = static_cast<S*>(a.ares);
+    auto* xp = static_cast<const S*>(a.x);
+    auto* wp = static_cast<const typename EW::S*>(a.w);
+    auto* rp = static_cast<const S*>(a.res);
+    const dim3 grid((unsigned)a.rows), block(kWideLanes);
+#define MCOP_WIDE(VV, RR)                                                                  \
+  hipLaunchKernelGGL((k_rms_norm_wide<E, EW, VV, RR>), grid, block, 0, st, o, arp, xp, wp, rp, \
+                     a.map, a.hidden, a.eps, a.mode, a.rms_div)
+    if (vec_ok) {
+      if (r) MCOP_WIDE(V, true); else MCOP_WIDE(V, false);
+    } else {
+      if (r) MCOP_WIDE(1, true); else MCOP_WIDE(1, false);
+    }
+#undef MCOP_WIDE
+    return check_launch(name);
+  }
   const KernelOfNv kernels =
       vec_ok ? (r ? &norm_kernel_of<E, EW, V, true> : &norm_kernel_of<E, EW, V, false>)
              : (r ? &norm_kernel_of<E, EW, 1, true> : &norm_kernel_of<E, EW, 1, false>);

@@ -130,6 +130,76 @@ k_add_rms_norm_quant_padded(uint8_t* __restrict__ padded, uint16_t* __restrict__
   }
 }
 
+// Rows too wide for the registers (the generic chain: 7168-wide rows always fit): one 1024-lane
+// workgroup per row, two passes (sum of squares and absmax, which does not need rho; then the
+// residual, rms, codes, padded codes and scale), the second re-reading x, residual and weight;
+// the residual is written in the last pass only, by the lane that read it.
+template <int VEC>
+__global__ void __launch_bounds__(kWideLanes)
+k_add_rms_norm_quant_padded_wide(uint8_t* __restrict__ padded, uint16_t* __restrict__ rms,
+                                 uint8_t* __restrict__ q_out, float* __restrict__ scales,
+                                 const uint16_t* __restrict__ x, uint16_t* __restrict__ res,
+                                 const uint16_t* __restrict__ w, int hidden, int64_t pad_bytes,
+                                 float eps) {
+  using E = BF16;
+  __shared__ double red_sum[16];
+  __shared__ float red_max[16];
+  const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x;
+  const int64_t base = (int64_t)blockIdx.x * hidden;
+  const int64_t pbase = (int64_t)blockIdx.x * pad_bytes;
+  auto ld3 = [&](int64_t o, Pack<uint16_t, VEC>& xv, Pack<uint16_t, VEC>& rv,
+                 Pack<uint16_t, VEC>& wv) {
+    xv = ld<uint16_t, VEC>(x + base + o);
+    rv = ld<uint16_t, VEC>(res + base + o);
+    wv = ld<uint16_t, VEC>(w + o);
+  };
+  double ss = 0.0;
+  float amax = 0.0f;
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    Pack<uint16_t, VEC> xv, rv, wv;
+    ld3((int64_t)j * VEC, xv, rv, wv);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float t = E::to_f(xv.v[e]) + E::to_f(rv.v[e]);
+      ss = __builtin_fma((double)t, (double)t, ss);
+      amax = __builtin_fmaxf(amax, __builtin_fabsf(rnd<E>(rnd<E>(t) * E::to_f(wv.v[e]))));
+    }
+  }
+  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  amax = row_reduce(amax, red_max, tpr, MaxOp());
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+  const float s = __builtin_fmaxf(mcop_div_rn(amax * rho, 127.0f), FLT_EPSILON);
+  const float inv = mcop_div_rn(1.0f, s);
+  if (threadIdx.x == 0) {
+    scales[blockIdx.x] = s;
+    uint8_t* sp = padded + pbase + hidden;
+    if ((reinterpret_cast<uintptr_t>(sp) & 3) == 0) {
+      *reinterpret_cast<float*>(sp) = s;
+    } else {
+      const uint32_t b = __builtin_bit_cast(uint32_t, s);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sp[k] = (uint8_t)(b >> (8 * k));
+    }
+  }
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    const int64_t o = (int64_t)j * VEC;
+    Pack<uint16_t, VEC> xv, rv, wv, zo, ro;
+    Pack<uint8_t, VEC> q;
+    ld3(o, xv, rv, wv);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      zo.v[e] = E::from_f(E::to_f(xv.v[e]) + E::to_f(rv.v[e]));
+      ro.v[e] = E::from_f(rnd<E>(E::to_f(zo.v[e]) * rho) * E::to_f(wv.v[e]));
+      q.v[e] = q_i8<-127>(E::to_f(ro.v[e]) * inv);
+    }
+    st<uint16_t, VEC>(res + base + o, zo);
+    st<uint16_t, VEC>(rms + base + o, ro);
+    st<uint8_t, VEC>(q_out + base + o, q);
+    st<uint8_t, VEC>(padded + pbase + o, q);
+  }
+}
+
 template <int VEC, bool OPT>
 static const void* kernel_of(int nv) {
   if constexpr (VEC == 1) {
@@ -186,6 +256,20 @@ static int dispatch(const PadArgs& a, hipStream_t st) {
   const char* name = "fused_add_rms_norm_dynamic_per_token_quant_padding_output";
   const bool vec_ok = a.hidden % 8 == 0 && a.pad_bytes % 8 == 0 &&
                       aligned(16, a.x, a.res, a.w, a.rms) && aligned(8, a.q, a.padded);
+  if constexpr (!OPT) {
+    if (!row_fits(a.hidden, vec_ok ? 8 : 1)) {
+      if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
+      const dim3 grid((unsigned)a.rows), block(kWideLanes);
+      if (vec_ok) {
+        hipLaunchKernelGGL((k_add_rms_norm_quant_padded_wide<8>), grid, block, 0, st, a.padded,
+                           a.rms, a.q, a.scales, a.x, a.res, a.w, a.hidden, a.pad_bytes, a.eps);
+      } else {
+        hipLaunchKernelGGL((k_add_rms_norm_quant_padded_wide<1>), grid, block, 0, st, a.padded,
+                           a.rms, a.q, a.scales, a.x, a.res, a.w, a.hidden, a.pad_bytes, a.eps);
+      }
+      return check_launch(name);
+    }
+  }
   Geometry g;
   if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? 8 : 1,
                        vec_ok ? &kernel_of<8, OPT> : &kernel_of<1, OPT>, &g)) {

@@ -10,7 +10,8 @@
 //     (a constant row, s == 0, has no finite zero point: zp = -128 and q = -128 here)
 //   fp8 e4m3fn       op/vllm/quantization/fp8/common.cu:142-180
 //     A = max|v| (min with *scale_ub); s = max(A / 448, 1/(448*512)); q = e4m3fn(clamp(v / s))
-// The row is loaded once into VGPRs; one max reduction (two for the zero point form).
+// The row is loaded once into VGPRs; one max reduction (two for the zero point form).  Rows too
+// wide for the registers take k_per_token_quant_wide (two passes over the row).
 #include <hip/hip_runtime.h>
 
 #include "../../include/mcop_norm.h"
@@ -19,6 +20,92 @@
 namespace mcop {
 
 enum PtqMode { PTQ_INT8 = 0, PTQ_INT8_AZP = 1, PTQ_FP8 = 2 };
+
+// Per-row quantization parameters from the row's max (|v| max, or v max with the zero point)
+// and, for the zero point, the max of -v.
+struct PtqRow {
+  float s;      // the stored scale
+  float inv;    // the multiplier of the codes
+  int zp;       // zero point (PTQ_INT8_AZP)
+  bool narrow;  // |zp| <= 2^29: the zero point sum fits int32 (PTQ_INT8_AZP)
+  bool s_ok;    // s inside the fast-quotient domain (PTQ_FP8)
+  bool bounded; // no scale bound cut the row's absmax (PTQ_FP8)
+};
+
+template <int MODE>
+__device__ __forceinline__ PtqRow ptq_row(float mx, float nmn, const float* scale_ub) {
+  PtqRow r{};
+  if constexpr (MODE == PTQ_INT8_AZP) {
+    const float mn = -nmn;
+    r.s = mcop_div_rn(mx - mn, 255.0f);
+    const bool degenerate = !(r.s > 0.0f);
+    // zp = rne(-128 - mn / s) converted with saturation (it lies in [-128, 127] for s > 0)
+    r.zp = degenerate ? -128 : cvt_rne_i32(-128.0f - mcop_div_rn(mn, r.s));
+    r.inv = degenerate ? 0.0f : mcop_div_rn(1.0f, r.s);
+    r.narrow = r.zp >= -(1 << 29) && r.zp <= (1 << 29);
+  } else if constexpr (MODE == PTQ_INT8) {
+    r.s = mcop_div_rn(mx, 127.0f);
+    r.inv = mx > 0.0f ? mcop_div_rn(127.0f, mx) : 0.0f;
+  } else {
+    float A = mx;
+    if (scale_ub != nullptr) A = __builtin_fminf(A, *scale_ub);
+    r.s = __builtin_fmaxf(mcop_div_rn(A, 448.0f), 1.0f / 229376.0f);
+    r.inv = mcop_div_rn(1.0f, r.s);
+    r.s_ok = mcop_divisor_ok(r.s);
+    r.bounded = A == mx && r.s <= 0x1p100f;
+  }
+  return r;
+}
+
+// Codes of one vector of v.
+template <class E, int VEC, int MODE>
+__device__ __forceinline__ Pack<uint8_t, VEC> ptq_codes(const float* a, const PtqRow& r) {
+  Pack<uint8_t, VEC> q;
+  if constexpr (MODE == PTQ_INT8_AZP) {
+    // float_to_int32_rn of the reference clamps with fmin/fmax before the saturating
+    // conversion, so a NaN product becomes 2^31 -> INT32_MAX and codes 127.  Every finite v lies
+    // in [mn, mx], so |v * inv| <= |mn / s| + 255 (to a relative 2^-21), and |zp| >= |mn / s| -
+    // 129.  With |zp| <= 2^29 (uniform over the row) the products stay below 2^30 in magnitude:
+    // clamping NaN to 2^30 instead still codes 127, and the int32 sum with zp cannot overflow.
+    // Otherwise the sum is formed in 64 bits.  The sum saturates to int8.
+    if (r.narrow) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const int t = cvt_rne_i32(__builtin_fminf(a[e] * r.inv, 0x1p30f)) + r.zp;
+        q.v[e] = (uint8_t)(int8_t)(t < -128 ? -128 : (t > 127 ? 127 : t));
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const int64_t t = (int64_t)cvt_rne_i32(__builtin_fminf(a[e] * r.inv, 0x1p31f)) + r.zp;
+        q.v[e] = (uint8_t)(int8_t)(t < -128 ? -128 : (t > 127 ? 127 : t));
+      }
+    }
+  } else if constexpr (MODE == PTQ_INT8) {
+    if constexpr (std::is_same_v<E, F32>) {
+      // fp32 inputs can carry NaN payloads in the low byte: round, convert and saturate
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-127>(a[e] * r.inv);
+    } else {
+      // |v * inv| <= 127 * (1 + 2^-23) < 127.5, so the code never saturates
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) q.v[e] = q_i8_in_range(a[e], r.inv);
+    }
+  } else {
+    q = fp8_quotient_codes<VEC>(a, r.s, r.inv, r.s_ok, r.bounded);
+  }
+  return q;
+}
+
+template <int MODE>
+__device__ __forceinline__ void ptq_fold(float t, float& mx, float& nmn) {
+  if constexpr (MODE == PTQ_INT8_AZP) {
+    mx = __builtin_fmaxf(mx, t);
+    nmn = __builtin_fmaxf(nmn, -t);
+  } else {
+    mx = __builtin_fmaxf(mx, __builtin_fabsf(t));
+  }
+}
 
 template <class E, int VEC, int NV, int MODE>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
@@ -47,95 +134,61 @@ k_per_token_quant(uint8_t* __restrict__ out, float* __restrict__ scales, int32_t
   for (int v = 0; v < NV; ++v) {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const float t = E::to_f(xv[v].v[e]);
-      a[v][e] = t;
-      if constexpr (MODE == PTQ_INT8_AZP) {
-        mx = __builtin_fmaxf(mx, t);
-        nmn = __builtin_fmaxf(nmn, -t);
-      } else {
-        mx = __builtin_fmaxf(mx, __builtin_fabsf(t));
-      }
+      a[v][e] = E::to_f(xv[v].v[e]);
+      ptq_fold<MODE>(a[v][e], mx, nmn);
     }
   }
   mx = row_reduce(mx, red_a, tpr, MaxOp());
+  if constexpr (MODE == PTQ_INT8_AZP) nmn = row_reduce(nmn, red_b, tpr, MaxOp());
+  const PtqRow r = ptq_row<MODE>(mx, nmn, scale_ub);
+  if (p.live && p.lt == 0) {
+    scales[p.row] = r.s;
+    if constexpr (MODE == PTQ_INT8_AZP) azp[p.row] = r.zp;
+  }
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int j = vec_index(v, tpr, p.lt);
+    if (p.live && j < nvec) {
+      st_nt<uint8_t, VEC>(out + obase + (int64_t)j * VEC, ptq_codes<E, VEC, MODE>(a[v], r));
+    }
+  }
+}
 
-  if constexpr (MODE == PTQ_INT8_AZP) {
-    nmn = row_reduce(nmn, red_b, tpr, MaxOp());
-    const float mn = -nmn;
-    const float s = mcop_div_rn(mx - mn, 255.0f);
-    const bool degenerate = !(s > 0.0f);
-    // zp = rne(-128 - mn / s) converted with saturation (it lies in [-128, 127] for s > 0)
-    const int zp = degenerate ? -128 : cvt_rne_i32(-128.0f - mcop_div_rn(mn, s));
-    const float inv = degenerate ? 0.0f : mcop_div_rn(1.0f, s);
-    if (p.live && p.lt == 0) {
-      scales[p.row] = s;
-      azp[p.row] = zp;
-    }
-    // float_to_int32_rn of the reference clamps with fmin/fmax before the saturating
-    // conversion, so a NaN product becomes 2^31 -> INT32_MAX and codes 127.  Every finite v lies
-    // in [mn, mx], so |v * inv| <= |mn / s| + 255 (to a relative 2^-21), and |zp| >= |mn / s| -
-    // 129.  With |zp| <= 2^29 (uniform over the row) the products stay below 2^30 in magnitude:
-    // clamping NaN to 2^30 instead still codes 127, and the int32 sum with zp cannot overflow.
-    // Otherwise the sum is formed in 64 bits.  The sum saturates to int8.
-    const bool narrow = zp >= -(1 << 29) && zp <= (1 << 29);
+// Rows too wide for the registers: one 1024-lane workgroup per row, two passes (max / min;
+// codes), the second re-reading the row.
+template <class E, int VEC, int MODE>
+__global__ void __launch_bounds__(kWideLanes)
+k_per_token_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
+                       int32_t* __restrict__ azp, const typename E::S* __restrict__ x,
+                       const float* __restrict__ scale_ub, int hidden, int64_t in_stride,
+                       int64_t out_stride) {
+  using S = typename E::S;
+  __shared__ float red_a[16];
+  __shared__ float red_b[16];
+  const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x;
+  const S* xr = x + (int64_t)blockIdx.x * in_stride;
+  uint8_t* orow = out + (int64_t)blockIdx.x * out_stride;
+  float mx = MODE == PTQ_INT8_AZP ? -__builtin_inff() : 0.0f;
+  float nmn = -__builtin_inff();
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    const Pack<S, VEC> xv = ld<S, VEC>(xr + (int64_t)j * VEC);
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int j = vec_index(v, tpr, p.lt);
-      if (p.live && j < nvec) {
-        Pack<uint8_t, VEC> q;
-        if (narrow) {
+    for (int e = 0; e < VEC; ++e) ptq_fold<MODE>(E::to_f(xv.v[e]), mx, nmn);
+  }
+  mx = row_reduce(mx, red_a, tpr, MaxOp());
+  if constexpr (MODE == PTQ_INT8_AZP) nmn = row_reduce(nmn, red_b, tpr, MaxOp());
+  const PtqRow r = ptq_row<MODE>(mx, nmn, scale_ub);
+  if (threadIdx.x == 0) {
+    scales[blockIdx.x] = r.s;
+    if constexpr (MODE == PTQ_INT8_AZP) azp[blockIdx.x] = r.zp;
+  }
+  for (int j = threadIdx.x; j < nvec; j += tpr) {
+    const Pack<S, VEC> xv = ld<S, VEC>(xr + (int64_t)j * VEC);
+    float a[VEC];
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) {
-            const int t = cvt_rne_i32(__builtin_fminf(a[v][e] * inv, 0x1p30f)) + zp;
-            q.v[e] = (uint8_t)(int8_t)(t < -128 ? -128 : (t > 127 ? 127 : t));
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) {
-            const int64_t t =
-                (int64_t)cvt_rne_i32(__builtin_fminf(a[v][e] * inv, 0x1p31f)) + zp;
-            q.v[e] = (uint8_t)(int8_t)(t < -128 ? -128 : (t > 127 ? 127 : t));
-          }
-        }
-        st_nt<uint8_t, VEC>(out + obase + (int64_t)j * VEC, q);
-      }
-    }
-  } else if constexpr (MODE == PTQ_INT8) {
-    if (p.live && p.lt == 0) scales[p.row] = mcop_div_rn(mx, 127.0f);
-    const float inv = mx > 0.0f ? mcop_div_rn(127.0f, mx) : 0.0f;
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int j = vec_index(v, tpr, p.lt);
-      if (p.live && j < nvec) {
-        Pack<uint8_t, VEC> q;
-        if constexpr (std::is_same_v<E, F32>) {
-          // fp32 inputs can carry NaN payloads in the low byte: round, convert and saturate
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-127>(a[v][e] * inv);
-        } else {
-          // |v * inv| <= 127 * (1 + 2^-23) < 127.5, so the code never saturates
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) q.v[e] = q_i8_in_range(a[v][e], inv);
-        }
-        st_nt<uint8_t, VEC>(out + obase + (int64_t)j * VEC, q);
-      }
-    }
-  } else {
-    float A = mx;
-    if (scale_ub != nullptr) A = __builtin_fminf(A, *scale_ub);
-    const float s = __builtin_fmaxf(mcop_div_rn(A, 448.0f), 1.0f / 229376.0f);
-    if (p.live && p.lt == 0) scales[p.row] = s;
-    const float inv = mcop_div_rn(1.0f, s);
-    const bool s_ok = mcop_divisor_ok(s);
-    const bool bounded = A == mx && s <= 0x1p100f;  // no scale bound cut the row's absmax
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int j = vec_index(v, tpr, p.lt);
-      if (p.live && j < nvec) {
-        st_nt<uint8_t, VEC>(out + obase + (int64_t)j * VEC,
-                            fp8_quotient_codes<VEC>(a[v], s, inv, s_ok, bounded));
-      }
-    }
+    for (int e = 0; e < VEC; ++e) a[e] = E::to_f(xv.v[e]);
+    st<uint8_t, VEC>(orow + (int64_t)j * VEC, ptq_codes<E, VEC, MODE>(a, r));
   }
 }
 
@@ -195,6 +248,21 @@ static int dispatch(const char* name, const PtqArgs& a, hipStream_t st) {
   constexpr int V = E::VEC;
   const bool vec_ok = a.hidden % V == 0 && a.in_stride % V == 0 && a.out_stride % V == 0 &&
                       aligned(16, a.x) && aligned(V, a.out);
+  if (!row_fits(a.hidden, vec_ok ? V : 1)) {
+    if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
+    using S = typename E::S;
+    auto* o = static_cast<uint8_t*>(a.out);
+    auto* xp = static_cast<const S*>(a.x);
+    const dim3 grid((unsigned)a.rows), block(kWideLanes);
+    if (vec_ok) {
+      hipLaunchKernelGGL((k_per_token_quant_wide<E, V, MODE>), grid, block, 0, st, o, a.scales,
+                         a.azp, xp, a.scale_ub, a.hidden, a.in_stride, a.out_stride);
+    } else {
+      hipLaunchKernelGGL((k_per_token_quant_wide<E, 1, MODE>), grid, block, 0, st, o, a.scales,
+                         a.azp, xp, a.scale_ub, a.hidden, a.in_stride, a.out_stride);
+    }
+    return check_launch(name);
+  }
   Geometry g;
   if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? V : 1,
                        vec_ok ? &kernel_of<E, V, MODE> : &kernel_of<E, 1, MODE>, &g)) {

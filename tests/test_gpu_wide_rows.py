@@ -1,7 +1,7 @@
 """Rows wider than the register-resident kernels hold (65536 bf16/fp16 or 32768 fp32 elements
 with 16-byte vectors; 16384 on the scalar path) take the multi-pass kernels (one 1024-lane
-workgroup per row, re-reading the row each pass) for H1, H2, H3, H4 and H5: bit for bit against
-the oracle, as the register-resident ones are."""
+workgroup per row, re-reading the row each pass) in every operator: bit for bit against the
+oracle, as the register-resident ones are."""
 
 import pytest
 import torch
@@ -133,3 +133,134 @@ def test_wide_rows_many_rows():
     assert_scales(s, s_ref, "scales")
     assert_codes(q, q_ref, "codes")
     assert_exact(rd, r_ref, "residual")
+
+
+# --------------------------------------------- the operators beyond the north-star path
+
+
+@pytest.mark.parametrize("dtype,H", [(torch.bfloat16, 65544), (torch.bfloat16, 65537),
+                                     (torch.float32, 32772)])
+def test_wide_standalone_quantizers(dtype, H):
+    say(f"wide quantizers {dtype} H={H}")
+    x = _x(3, H, 20, dtype)
+    x[1, 3] = -80.0
+    for azp in (False, True):
+        q_ref, s_ref, z_ref = oracle.dynamic_scaled_int8_quant(x, use_azp=azp)
+        q = torch.empty(x.shape, dtype=torch.int8, device=DEV)
+        s = torch.empty(3, 1, device=DEV)
+        z = torch.empty(3, 1, dtype=torch.int32, device=DEV) if azp else None
+        torch.ops._C.dynamic_scaled_int8_quant(q, x.to(DEV), s, z)
+        torch.cuda.synchronize()
+        assert_scales(s, s_ref, f"int8 azp={azp} scales")
+        assert_codes(q, q_ref, f"int8 azp={azp} codes")
+        if azp:
+            assert torch.equal(z.cpu().flatten(), z_ref.flatten())
+    # fp8 with strided rows on both sides and a scale bound
+    big = torch.zeros(3, H + 24, dtype=dtype)
+    big[:, :H] = x
+    xd = big.to(DEV)[:, :H]
+    for ub in (None, 0.05):
+        q_ref, s_ref = oracle.dynamic_per_token_scaled_fp8_quant(x, ub)
+        qb = torch.empty(3, H + 40, dtype=torch.float8_e4m3fn, device=DEV)
+        s = torch.empty(3, 1, device=DEV)
+        ubd = None if ub is None else torch.tensor([ub], device=DEV)
+        torch.ops._C.dynamic_per_token_scaled_fp8_quant(qb[:, :H], xd, s, ubd)
+        torch.cuda.synchronize()
+        assert_scales(s, s_ref, f"fp8 ub={ub} scales")
+        assert_codes(qb[:, :H].contiguous(), q_ref, f"fp8 ub={ub} codes")
+
+
+@pytest.mark.parametrize("H", [65544, 65540])
+def test_wide_padded(H):
+    say(f"wide padded H={H}")
+    pad = (H + 4 + 63) // 64 * 32
+    x, r, w = _x(3, H, 21, torch.bfloat16), _x(3, H, 22, torch.bfloat16), _w(H, 23,
+                                                                             torch.bfloat16)
+    p_ref, r_ref, rms_ref, q_ref, s_ref = oracle.add_rms_norm_quant_padded(x, r, w, pad, 1e-6)
+    p = torch.zeros(3, 2 * pad, dtype=torch.int8, device=DEV)
+    rms = torch.empty(x.shape, dtype=torch.bfloat16, device=DEV)
+    q = torch.empty(x.shape, dtype=torch.int8, device=DEV)
+    s = torch.empty(3, 1, device=DEV)
+    rd = r.to(DEV)
+    op.fused_add_rms_norm_dynamic_per_token_quant_padding_output(p, rms, q, s, x.to(DEV), rd,
+                                                                  w.to(DEV), pad, 1e-6)
+    torch.cuda.synchronize()
+    assert_exact(rd, r_ref, "residual")
+    assert_exact(rms, rms_ref, "output_rms")
+    assert_codes(q, q_ref, "codes")
+    assert_scales(s, s_ref, "scales")
+    assert torch.equal(p.cpu().view(torch.uint8), p_ref), "padded rows"
+
+
+@pytest.mark.parametrize("qdt", [torch.int8, torch.float8_e4m3fn])
+@pytest.mark.parametrize("G", [64, 128])
+@pytest.mark.parametrize("misaligned", [False, True])
+def test_wide_per_block(qdt, G, misaligned):
+    say(f"wide per-block {qdt} G={G} misaligned={misaligned}")
+    H = 65536 + 128
+    x, r, w = _x(3, H, 24, torch.bfloat16), _x(3, H, 25, torch.bfloat16), _w(H, 26,
+                                                                             torch.bfloat16)
+    for transposed, ub in ((False, None), (True, 0.05 if qdt == torch.float8_e4m3fn else None)):
+        q_ref, s_ref, r_ref = oracle.rms_norm_per_block_quant(x, w, 1e-6, qdt, G, ub, r,
+                                                              transposed)
+        if misaligned:  # one element into a buffer: the scalar path
+            xb = torch.empty(3 * H + 1, dtype=torch.bfloat16, device=DEV)
+            xb[1:] = x.flatten().to(DEV)
+            xd = xb[1:].view(3, H)
+        else:
+            xd = x.to(DEV)
+        q = torch.empty(x.shape, dtype=qdt, device=DEV)
+        s = torch.empty(H // G, 3, device=DEV) if transposed else torch.empty(3, H // G,
+                                                                               device=DEV)
+        rd = r.to(DEV)
+        ubd = None if ub is None else torch.tensor([ub], device=DEV)
+        torch.ops._C.rms_norm_per_block_quant(q, xd, w.to(DEV), s, 1e-6, ubd, rd, G, transposed)
+        torch.cuda.synchronize()
+        tag = f"transposed={transposed} ub={ub}"
+        assert_exact(rd, r_ref, tag + " residual")
+        assert_scales(s, s_ref, tag + " scales")
+        assert_codes(q, q_ref, tag + " codes")
+
+
+@pytest.mark.parametrize("dtype,wdtype,H", [(torch.bfloat16, torch.bfloat16, 65544),
+                                            (torch.float16, torch.float32, 65608),
+                                            (torch.float32, torch.float32, 32776),
+                                            (torch.bfloat16, torch.bfloat16, 20001)])
+def test_wide_norms(dtype, wdtype, H):
+    say(f"wide norms {dtype} w={wdtype} H={H}")
+    x, r, w = _x(3, H, 27, dtype), _x(3, H, 28, dtype), _w(H, 29, wdtype)
+    for res in (None, r):
+        for rms_div in (True, False):
+            out_ref, ares_ref = oracle.rms_norm(x, w, 1e-6, residual=res, rms_div=rms_div)
+            out = torch.empty(x.shape, dtype=dtype, device=DEV)
+            ares = torch.empty(x.shape, dtype=dtype, device=DEV) if res is not None else None
+            op.rms_norm(out, x.to(DEV), w.to(DEV), 1e-6, ares,
+                        None if res is None else res.to(DEV), rms_div)
+            torch.cuda.synchronize()
+            tag = f"res={res is not None} rms_div={rms_div}"
+            assert_exact(out, out_ref, tag + " out")
+            if res is not None:
+                assert_exact(ares, ares_ref, tag + " after_res")
+    if dtype != torch.float16:
+        # vLLM rms_norm on a 3-D view with strided rows
+        big = torch.randn(2, 3, H + 16, generator=gen(30)).to(dtype)
+        xv = big[:, :, :H]
+        wv = _w(H, 31, dtype)
+        ref = oracle.vllm_rms_norm(xv.contiguous().view(6, H), wv, 1e-6)
+        o = torch.empty(2, 3, H, dtype=dtype, device=DEV)
+        torch.ops._C.rms_norm(o, big.to(DEV)[:, :, :H], wv.to(DEV), 1e-6)
+        torch.cuda.synchronize()
+        assert_exact(o.view(6, H), ref, "vLLM rms_norm 3-D strided")
+
+
+def test_wide_head_rms_norm():
+    say("wide head_rms_norm D=65544")
+    T, NH, D = 2, 3, 65544
+    hs = torch.randn(T, NH, D, generator=gen(32)).to(torch.bfloat16)
+    w = _w(NH * D, 33, torch.bfloat16).view(NH, D)
+    base = torch.zeros_like(hs)
+    ref = oracle.head_rms_norm(base, hs, w, 1e-6, 1, 2)
+    out = base.to(DEV)
+    op.head_rms_norm(out, hs.to(DEV), w.to(DEV), 1e-6, 1, 2)
+    torch.cuda.synchronize()
+    assert_exact(out, ref, "head_rms_norm")
