@@ -38,7 +38,7 @@ typedef enum {
 enum {
   MCOP_OK = 0,
   MCOP_E_INVALID = -1,  /* bad argument: null pointer, size, dtype combination */
-  MCOP_E_UNSUPPORTED = -2, /* valid request this build does not implement (e.g. hidden_size too large) */
+  MCOP_E_UNSUPPORTED = -2, /* valid request beyond a launch limit (more than 2^31 - 1 workgroups) */
   MCOP_E_LAUNCH = -3    /* the HIP runtime rejected the kernel launch */
 };
 
