@@ -44,7 +44,7 @@ def parse():
                     choices=["cfg2", "cfg3", "cfg4", "cfg5-large", "cfg5-decode1",
                              "cfg5-decode4", "cfg5-decode16", "cfg5-decode64", "ptq-int8",
                              "ptq-int8-azp", "ptq-fp8", "padded", "block-fp8", "norm-res",
-                             "vllm-norm", "head-norm", "sdq"])
+                             "vllm-norm", "head-norm", "sdq", "wide-int8"])
     ap.add_argument("--sets", type=int, default=0,
                     help="rotated input sets (default: enough for > 1 GiB, at least 3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -188,6 +188,8 @@ WORKLOADS = {
     "head-norm": Workload("head-norm", 65536 * 8, 128, 1e-6, "head_norm"),
     # the un-normed SmoothQuant sibling (scale_dynamic_quant) at SmoothQuant's shape
     "sdq": Workload("sdq", 16384, 7168, 0.0, "sdq"),
+    # rows wider than the registers hold: the headline operator's multi-pass kernel
+    "wide-int8": Workload("wide-int8", 2048, 131072, 1e-6, "add_norm_int8"),
 }
 KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "fused_add": "k_fused_add_rms_norm",
                "smooth_fp8": "k_rms_norm_smooth_quant", "ptq_int8": "k_per_token_quant",
@@ -195,13 +197,19 @@ KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "fused_add": "k_fused_add_rm
                "padded": "k_add_rms_norm_quant_padded", "block_fp8": "k_rms_norm_group_quant",
                "norm_res": "k_rms_norm", "vllm_norm": "k_rms_norm", "head_norm": "k_rms_norm",
                "sdq": "k_scale_dynamic_quant"}
+# workloads whose kernel is not their kind's register-resident one
+KERNEL_NAME_OF_WORKLOAD = {"wide-int8": "k_rms_norm_quant_wide"}
+
+
+def kernel_name(wl) -> str:
+    return KERNEL_NAME_OF_WORKLOAD.get(wl.name, KERNEL_NAME[wl.kind])
 
 
 # ------------------------------------------------------------------------------ pieces
 def traffic_from_profiles(wl: Workload):
     """HBM bytes per dispatch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by
     a copy kernel's reading), from the committed summary, or None."""
-    p = ROOT / "profiles" / f"{KERNEL_NAME[wl.kind]}_{wl.name}.txt"
+    p = ROOT / "profiles" / f"{kernel_name(wl)}_{wl.name}.txt"
     if not p.exists():
         return None
     m = re.search(r"^hbm_bytes_per_dispatch:\s*([0-9.eE+]+)", p.read_text(), re.M)
@@ -412,7 +420,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
-                     "kernel": KERNEL_NAME[wl.kind],
+                     "kernel": kernel_name(wl),
                      "kernel_avg_us": round(kernel_ms * 1e3, 3),
                      "single_launch_us_p10_p50_p90": [
                          round(per_launch_ms[int(q * (K - 1))] * 1e3, 3) for q in (0.1, 0.5, 0.9)],
