@@ -185,8 +185,10 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 
 // Rows too wide for the registers (QM_VLLM and QM_MC; QM_MC_7168 rows always fit): one
 // 1024-lane workgroup per row and three passes over it -- sum of squares; absmax of y; codes and
-// the residual -- each re-reading x and residual (the residual is written in the last pass
-// only, by the lane that read it, as the reference's multi-pass kernels do).
+// the residual.  The row's head (the first NC vectors of every lane: 8 x 1024 16-byte vectors
+// without a residual, 5 x 1024 with one -- as many as fit 128 VGPRs without spilling) stays in
+// registers across the passes; the rest is re-read each pass.  The residual is written in the last pass only, by the lane that read it, as the
+// reference's multi-pass kernels do.
 template <class E, int VEC, bool FP8, bool RES, int MODE>
 __global__ void __launch_bounds__(kWideLanes)
 k_rms_norm_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
@@ -195,11 +197,29 @@ k_rms_norm_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
                       int hidden, float eps) {
   static_assert(MODE != QM_MC_7168, "7168-wide rows fit the register-resident kernel");
   using S = typename E::S;
+  constexpr int NC = VEC > 1 ? (RES ? 5 : 8) : 16;
   __shared__ double red_sum[16];
   __shared__ float red_max[16];
   const int nvec = hidden / VEC;
   const int tpr = (int)blockDim.x;
   const int64_t base = (int64_t)blockIdx.x * hidden;
+  // the head, loaded once (lanes past the row end hold nothing and skip it)
+  Pack<S, VEC> xc[NC], rc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j = c * tpr + (int)threadIdx.x;
+    if (j < nvec) {
+      xc[c] = ld<S, VEC>(x + base + (int64_t)j * VEC);
+      if constexpr (RES) rc[c] = ld<S, VEC>(res + base + (int64_t)j * VEC);
+    }
+  }
+  auto a_head = [&](int c, float* a) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      a[e] = E::to_f(xc[c].v[e]);
+      if constexpr (RES) a[e] += E::to_f(rc[c].v[e]);
+    }
+  };
   auto a_of = [&](int64_t o, float* a) {
     const Pack<S, VEC> xv = ld<S, VEC>(x + base + o);
     Pack<S, VEC> rv;
@@ -210,8 +230,18 @@ k_rms_norm_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
       if constexpr (RES) a[e] += E::to_f(rv.v[e]);
     }
   };
+  const int tail0 = NC * tpr + (int)threadIdx.x;  // the lane's first re-read vector
   double ss = 0.0;
-  for (int j = threadIdx.x; j < nvec; j += tpr) {
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if (c * tpr + (int)threadIdx.x < nvec) {
+      float a[VEC];
+      a_head(c, a);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) ss = __builtin_fma((double)a[e], (double)a[e], ss);
+    }
+  }
+  for (int j = tail0; j < nvec; j += tpr) {
     float a[VEC];
     a_of((int64_t)j * VEC, a);
 #pragma unroll
@@ -225,7 +255,18 @@ k_rms_norm_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
     for (int e = 0; e < VEC; ++e) y[e] = rnd<E>(rnd<E>(a[e] * rho) * E::to_f(wv.v[e]));
   };
   float amax = 0.0f;
-  for (int j = threadIdx.x; j < nvec; j += tpr) {
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j = c * tpr + (int)threadIdx.x;
+    if (j < nvec) {
+      float a[VEC], y[VEC];
+      a_head(c, a);
+      y_of((int64_t)j * VEC, a, y);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) amax = __builtin_fmaxf(amax, __builtin_fabsf(y[e]));
+    }
+  }
+  for (int j = tail0; j < nvec; j += tpr) {
     float a[VEC], y[VEC];
     a_of((int64_t)j * VEC, a);
     y_of((int64_t)j * VEC, a, y);
@@ -239,20 +280,32 @@ k_rms_norm_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
   const float inv = mcop_div_rn(1.0f, s);
   const bool s_ok = mcop_divisor_ok(s);
   const bool bounded = A == amax && s <= 0x1p100f;
-  for (int j = threadIdx.x; j < nvec; j += tpr) {
-    const int64_t o = (int64_t)j * VEC;
-    float a[VEC], y[VEC];
-    a_of(o, a);
+  auto emit = [&](int64_t o, const float* a) {
     if constexpr (RES) {
       Pack<S, VEC> r;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) r.v[e] = E::from_f(a[e]);
       st<S, VEC>(res + base + o, r);
     }
+    float y[VEC];
     y_of(o, a, y);
     st<uint8_t, VEC>(out + base + o,
                      row_codes<E, VEC, FP8, MODE>(y, rho, s, inv, s_ok, bounded,
                                                   scale_ub != nullptr));
+  };
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j = c * tpr + (int)threadIdx.x;
+    if (j < nvec) {
+      float a[VEC];
+      a_head(c, a);
+      emit((int64_t)j * VEC, a);
+    }
+  }
+  for (int j = tail0; j < nvec; j += tpr) {
+    float a[VEC];
+    a_of((int64_t)j * VEC, a);
+    emit((int64_t)j * VEC, a);
   }
 }
 
