@@ -75,7 +75,7 @@ struct NormW {
 };
 
 // The normalized output of one vector from a (x [+ r], or b(x + r) for the element-wise chain
-// with a residual).
+// with a residual), as the register-resident kernel computes it inline.
 template <class E, class EW, int VEC>
 __device__ __forceinline__ Pack<typename E::S, VEC> norm_out(const float* a,
                                                              const NormW<EW, VEC>& w, float rho,
@@ -162,8 +162,23 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
     if (!(p.live && j < nvec)) continue;
-    st_nt<S, VEC>(out + out_base + (int64_t)j * VEC,
-                  norm_out<E, EW, VEC>(a[v], wv[v], rho, inv_rho, mode, rms_div));
+    // kept inline (norm_out computes the same): through the helper the compiler issued this
+    // kernel's streamed load before the shared weight load
+    Pack<S, VEC> o;
+    if (mode == NORM_VLLM) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(rnd<E>(a[v][e] * rho) * wv[v].at(e));
+    } else if (mode == NORM_MC || !rms_div) {
+      const float d = (mode == NORM_MC && rms_div) ? inv_rho : rho;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f((a[v][e] * d) * wv[v].at(e));
+    } else {
+      float n[VEC];
+      div_by_const<VEC>(n, a[v], rho, inv_rho, mcop_divisor_ok(rho));
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(n[e] * wv[v].at(e));
+    }
+    st_nt<S, VEC>(out + out_base + (int64_t)j * VEC, o);
   }
 }
 
