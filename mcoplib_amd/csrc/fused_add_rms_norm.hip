@@ -8,7 +8,8 @@
 // One pass over HBM: x, residual and weight are loaded once into VGPRs, residual is written
 // from registers before the reduction, x after it (8*H bytes per bf16 row, plus the weight).
 // Rows too wide for the registers take k_fused_add_rms_norm_wide: one 1024-lane workgroup per
-// row and two passes over the row (sum of squares; then residual and output), the second
+// row, the row's first 12 vectors a lane (8 for fp16) held in registers (one read of rows up to
+// 98304 bf16 elements), and beyond them two passes (sum of squares; then residual and output), the second
 // re-reading x and residual, which each lane then overwrites at the same addresses.
 #include <hip/hip_runtime.h>
 
@@ -85,35 +86,103 @@ k_fused_add_rms_norm_wide(typename E::S* __restrict__ x, int64_t x_stride,
                           typename E::S* __restrict__ res, const typename E::S* __restrict__ w,
                           int hidden, float eps) {
   using S = typename E::S;
+  // The row head (the lane's first NC vectors) stays in registers as the rounded sum z, so
+  // rows up to NC * 1024 vectors are read once.  Head loads are unconditional (a lane past the
+  // row end re-reads the row's last vector and does not count it) and issued G vectors at a
+  // time; the residual of the head is written in the first pass, that of the re-read tail in
+  // the second, after its last read.
+  // NC is the largest head that compiles without spills at 1024 lanes (128 VGPRs a lane)
+  constexpr int NC = std::is_same<E, F16>::value ? 8 : 12, G = 4;
   __shared__ double red_sum[16];
   const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x, tid = (int)threadIdx.x;
   S* xr = x + (int64_t)blockIdx.x * x_stride;
   S* rr = res + (int64_t)blockIdx.x * hidden;
-  double ss = 0.0;
-  for (int j = threadIdx.x; j < nvec; j += blockDim.x) {
-    const Pack<S, VEC> xv = ld<S, VEC>(xr + (int64_t)j * VEC);
-    const Pack<S, VEC> rv = ld<S, VEC>(rr + (int64_t)j * VEC);
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const double d = (double)rnd<E>(E::to_f(xv.v[e]) + E::to_f(rv.v[e]));
-      ss = __builtin_fma(d, d, ss);
-    }
-  }
-  ss = row_reduce(ss, red_sum, (int)blockDim.x, SumOp());
-  const float rho = mcop_inv_rms(ss, hidden, eps);
-  for (int j = threadIdx.x; j < nvec; j += blockDim.x) {
-    const int64_t o = (int64_t)j * VEC;
+  // element offsets within the row fit 32 bits (hidden <= INT32_MAX)
+  auto z_of = [&](int o) {
     const Pack<S, VEC> xv = ld<S, VEC>(xr + o);
     const Pack<S, VEC> rv = ld<S, VEC>(rr + o);
-    const Pack<S, VEC> wv = ld<S, VEC>(w + o);
-    Pack<S, VEC> zo, yo;
+    Pack<S, VEC> z;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) z.v[e] = E::from_f(E::to_f(xv.v[e]) + E::to_f(rv.v[e]));
+    return z;
+  };
+  auto sum_sq = [&](const Pack<S, VEC>& z) {
+    double vs = 0.0;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      zo.v[e] = E::from_f(E::to_f(xv.v[e]) + E::to_f(rv.v[e]));
-      yo.v[e] = E::from_f(rnd<E>(E::to_f(zo.v[e]) * rho) * E::to_f(wv.v[e]));
+      const double d = (double)E::to_f(z.v[e]);
+      vs = __builtin_fma(d, d, vs);
     }
-    st<S, VEC>(rr + o, zo);
-    st<S, VEC>(xr + o, yo);
+    return vs;
+  };
+  // offset of head vector c of lane t, clamped into the row (lanes past its end re-read the
+  // last vector and neither count nor store it)
+  auto head_off = [&](int c, int t) { return min(c * tpr + t, nvec - 1) * VEC; };
+
+  Pack<S, VEC> zc[NC];
+  double ss = 0.0;
+#pragma unroll
+  for (int g = 0; g < NC; g += G) {
+    Pack<S, VEC> xv[G], rv[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      xv[k] = ld<S, VEC>(xr + head_off(g + k, tid));
+      rv[k] = ld<S, VEC>(rr + head_off(g + k, tid));
+    }
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        zc[g + k].v[e] = E::from_f(E::to_f(xv[k].v[e]) + E::to_f(rv[k].v[e]));
+      }
+      const double vs = sum_sq(zc[g + k]);
+      ss += (g + k) * tpr + tid < nvec ? vs : 0.0;
+      if constexpr (sizeof(Pack<S, VEC>) == 16) {  // keep z packed (4 VGPRs), not as floats
+        u32x4 u = __builtin_bit_cast(u32x4, zc[g + k]);
+        asm volatile("" : "+v"(u));
+        zc[g + k] = __builtin_bit_cast(Pack<S, VEC>, u);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      if ((g + k) * tpr + tid < nvec) st<S, VEC>(rr + head_off(g + k, tid), zc[g + k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // at most G vectors' loads in flight
+  }
+  const int tail0 = NC * tpr + tid;
+  for (int j = tail0; j < nvec; j += tpr) ss += sum_sq(z_of(j * VEC));
+  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+  // the lane index again, opaque to the compiler: the second pass recomputes its addresses
+  // instead of holding the first pass's in registers across the reduction
+  int tid2 = tid;
+  asm volatile("" : "+v"(tid2));
+  auto y_of = [&](const Pack<S, VEC>& z, const Pack<S, VEC>& wv) {
+    Pack<S, VEC> y;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      y.v[e] = E::from_f(rnd<E>(E::to_f(z.v[e]) * rho) * E::to_f(wv.v[e]));
+    }
+    return y;
+  };
+#pragma unroll
+  for (int g = 0; g < NC; g += G) {
+    Pack<S, VEC> wv[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k) wv[k] = ld<S, VEC>(w + head_off(g + k, tid2));
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const Pack<S, VEC> y = y_of(zc[g + k], wv[k]);
+      if ((g + k) * tpr + tid2 < nvec) st<S, VEC>(xr + head_off(g + k, tid2), y);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int j = tail0; j < nvec; j += tpr) {
+    const int o = j * VEC;
+    const Pack<S, VEC> z = z_of(o);
+    st<S, VEC>(rr + o, z);
+    st<S, VEC>(xr + o, y_of(z, ld<S, VEC>(w + o)));
   }
 }
 
