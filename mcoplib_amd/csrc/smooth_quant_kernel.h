@@ -159,8 +159,9 @@ k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 }
 
 // Rows too wide for the registers: one 1024-lane workgroup per row and three passes over it --
-// sum of squares; absmax of v; after_res, after_norm and the codes -- each re-reading x (and
-// the residual, which this operator only reads), weight and smooth.
+// sum of squares; absmax of v; after_res, after_norm and the codes.  The row head stays in
+// registers; each pass re-reads the rest of x (and of the residual, which this operator only
+// reads), and the weight and smooth vectors (shared by all rows).
 template <class E, class EW, class ES, int VEC, bool FP8, bool RES>
 __global__ void __launch_bounds__(kWideLanes)
 k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
@@ -171,12 +172,32 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
                              const typename E::S* __restrict__ res, int hidden, float eps,
                              uint32_t flags) {
   using S = typename E::S;
+  // The row head (the lane's first NC vectors of x, and of the residual) is loaded once and
+  // kept in registers across the three passes; the passes re-read only the rest of the row.
+  // NC is the largest head that compiles without spills at 1024 lanes (128 VGPRs a lane).
+  constexpr int NC = VEC > 1 ? (RES ? 4 : sizeof(typename EW::S) == 4 ? 7 : 8) : 16;
   __shared__ double red_sum[16];
   __shared__ float red_max[16];
   const int nvec = hidden / VEC;
   const int tpr = (int)blockDim.x;
   const int64_t base = (int64_t)blockIdx.x * hidden;
-  auto t_of = [&](int64_t o, float* t) {  // a = x (+ r), unrounded
+  Pack<S, VEC> xc[NC], rc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j = c * tpr + (int)threadIdx.x;
+    if (j < nvec) {
+      xc[c] = ld<S, VEC>(x + base + (int64_t)j * VEC);
+      if constexpr (RES) rc[c] = ld<S, VEC>(res + base + (int64_t)j * VEC);
+    }
+  }
+  auto t_head = [&](int c, float* t) {  // a = x (+ r), unrounded
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      t[e] = E::to_f(xc[c].v[e]);
+      if constexpr (RES) t[e] += E::to_f(rc[c].v[e]);
+    }
+  };
+  auto t_of = [&](int64_t o, float* t) {
     const Pack<S, VEC> xv = ld<S, VEC>(x + base + o);
     Pack<S, VEC> rv;
     if constexpr (RES) rv = ld<S, VEC>(res + base + o);
@@ -186,8 +207,18 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
       if constexpr (RES) t[e] += E::to_f(rv.v[e]);
     }
   };
+  const int tail0 = NC * tpr + (int)threadIdx.x;  // the lane's first re-read vector
   double ss = 0.0;
-  for (int j = threadIdx.x; j < nvec; j += tpr) {
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if (c * tpr + (int)threadIdx.x < nvec) {
+      float t[VEC];
+      t_head(c, t);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) ss = __builtin_fma((double)t[e], (double)t[e], ss);
+    }
+  }
+  for (int j = tail0; j < nvec; j += tpr) {
     float t[VEC];
     t_of((int64_t)j * VEC, t);
 #pragma unroll
@@ -220,7 +251,18 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
     }
   };
   float amax = 0.0f;
-  for (int j = threadIdx.x; j < nvec; j += tpr) {
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j = c * tpr + (int)threadIdx.x;
+    if (j < nvec) {
+      float t[VEC], u[VEC], v[VEC];
+      t_head(c, t);
+      uv_of((int64_t)j * VEC, t, u, v);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[e]));
+    }
+  }
+  for (int j = tail0; j < nvec; j += tpr) {
     float t[VEC], u[VEC], v[VEC];
     t_of((int64_t)j * VEC, t);
     uv_of((int64_t)j * VEC, t, u, v);
@@ -231,10 +273,8 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
   const float s = mcop_div_rn(amax, FP8 ? 448.0f : 127.0f);
   if (threadIdx.x == 0) scales[blockIdx.x] = s;
   const float inv = amax > 0.0f ? mcop_div_rn(1.0f, s) : 0.0f;
-  for (int j = threadIdx.x; j < nvec; j += tpr) {
-    const int64_t o = (int64_t)j * VEC;
-    float t[VEC], u[VEC], v[VEC];
-    t_of(o, t);
+  auto emit = [&](int64_t o, const float* t) {
+    float u[VEC], v[VEC];
     uv_of(o, t, u, v);
     Pack<S, VEC> ar, an;
 #pragma unroll
@@ -255,6 +295,20 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
       for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-127>(v[e] * inv);
     }
     st<uint8_t, VEC>(out + base + o, q);
+  };
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j = c * tpr + (int)threadIdx.x;
+    if (j < nvec) {
+      float t[VEC];
+      t_head(c, t);
+      emit((int64_t)j * VEC, t);
+    }
+  }
+  for (int j = tail0; j < nvec; j += tpr) {
+    float t[VEC];
+    t_of((int64_t)j * VEC, t);
+    emit((int64_t)j * VEC, t);
   }
 }
 
