@@ -187,7 +187,8 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 // 1024-lane workgroup per row and three passes over it -- sum of squares; absmax of y; codes and
 // the residual.  The row's head (the first NC vectors of every lane: 8 x 1024 16-byte vectors
 // without a residual, 5 x 1024 with one -- as many as fit 128 VGPRs without spilling) stays in
-// registers across the passes; the rest is re-read each pass.  The residual is written in the last pass only, by the lane that read it, as the
+// registers across the passes, the next NL vectors (128 KB) in LDS; the rest is re-read each
+// pass.  The residual is written in the last pass only, by the lane that read it, as the
 // reference's multi-pass kernels do.
 template <class E, int VEC, bool FP8, bool RES, int MODE>
 __global__ void __launch_bounds__(kWideLanes)
@@ -213,11 +214,37 @@ k_rms_norm_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
       if constexpr (RES) rc[c] = ld<S, VEC>(res + base + (int64_t)j * VEC);
     }
   }
-  auto a_head = [&](int c, float* a) {
+  // The next NL vectors of every lane are held in LDS: lane-private slots (vector c of lane t
+  // at [c][t]: consecutive lanes, consecutive 16-byte slots), so no barrier is needed.  The
+  // workgroup already fills a CU's registers, so the 128 KB cost no occupancy.
+  constexpr int NL = VEC > 1 ? (RES ? 4 : 8) : 0;
+  constexpr int NLS = NL > 0 ? NL * (RES ? 2 : 1) : 1;
+  __shared__ Pack<S, VEC> lds[NLS][kWideLanes];
+  const int tid = (int)threadIdx.x;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      a[e] = E::to_f(xc[c].v[e]);
-      if constexpr (RES) a[e] += E::to_f(rc[c].v[e]);
+  for (int c = 0; c < NL; ++c) {
+    const int j = (NC + c) * tpr + tid;
+    if (j < nvec) {
+      lds[c][tid] = ld<S, VEC>(x + base + (int64_t)j * VEC);
+      if constexpr (RES) lds[NL + c][tid] = ld<S, VEC>(res + base + (int64_t)j * VEC);
+    }
+  }
+  auto a_head = [&](int c, float* a) {  // c < NC + NL
+    if (c < NC) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        a[e] = E::to_f(xc[c].v[e]);
+        if constexpr (RES) a[e] += E::to_f(rc[c].v[e]);
+      }
+    } else {
+      const Pack<S, VEC> xv = lds[c - NC][tid];
+      Pack<S, VEC> rv;
+      if constexpr (RES) rv = lds[NL + c - NC][tid];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        a[e] = E::to_f(xv.v[e]);
+        if constexpr (RES) a[e] += E::to_f(rv.v[e]);
+      }
     }
   };
   auto a_of = [&](int64_t o, float* a) {
@@ -230,10 +257,10 @@ k_rms_norm_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
       if constexpr (RES) a[e] += E::to_f(rv.v[e]);
     }
   };
-  const int tail0 = NC * tpr + (int)threadIdx.x;  // the lane's first re-read vector
+  const int tail0 = (NC + NL) * tpr + (int)threadIdx.x;  // the lane's first re-read vector
   double ss = 0.0;
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
+  for (int c = 0; c < NC + NL; ++c) {
     if (c * tpr + (int)threadIdx.x < nvec) {
       float a[VEC];
       a_head(c, a);
@@ -256,7 +283,7 @@ k_rms_norm_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
   };
   float amax = 0.0f;
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
+  for (int c = 0; c < NC + NL; ++c) {
     const int j = c * tpr + (int)threadIdx.x;
     if (j < nvec) {
       float a[VEC], y[VEC];
@@ -294,7 +321,7 @@ k_rms_norm_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
                                                   scale_ub != nullptr));
   };
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
+  for (int c = 0; c < NC + NL; ++c) {
     const int j = c * tpr + (int)threadIdx.x;
     if (j < nvec) {
       float a[VEC];
