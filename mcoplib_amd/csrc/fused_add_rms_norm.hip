@@ -8,8 +8,8 @@
 // One pass over HBM: x, residual and weight are loaded once into VGPRs, residual is written
 // from registers before the reduction, x after it (8*H bytes per bf16 row, plus the weight).
 // Rows too wide for the registers take k_fused_add_rms_norm_wide: one 1024-lane workgroup per
-// row, the row's first 12 vectors a lane (8 for fp16) held in registers (one read of rows up to
-// 98304 bf16 elements), and beyond them two passes (sum of squares; then residual and output), the second
+// row, the row's first 8 vectors a lane held in registers and (bf16, fp32) the next 8 in LDS
+// (one read of rows up to 131072 bf16 elements), and beyond them two passes (sum of squares; then residual and output), the second
 // re-reading x and residual, which each lane then overwrites at the same addresses.
 #include <hip/hip_runtime.h>
 
@@ -86,13 +86,14 @@ k_fused_add_rms_norm_wide(typename E::S* __restrict__ x, int64_t x_stride,
                           typename E::S* __restrict__ res, const typename E::S* __restrict__ w,
                           int hidden, float eps) {
   using S = typename E::S;
-  // The row head (the lane's first NC vectors) stays in registers as the rounded sum z, so
-  // rows up to NC * 1024 vectors are read once.  Head loads are unconditional (a lane past the
+  // The row head (the lane's first NC vectors) stays in registers as the rounded sum z, and
+  // the next NL in LDS, so rows up to (NC + NL) * 1024 vectors are read once.  Head loads are unconditional (a lane past the
   // row end re-reads the row's last vector and does not count it) and issued G vectors at a
   // time; the residual of the head is written in the first pass, that of the re-read tail in
   // the second, after its last read.
-  // NC is the largest head that compiles without spills at 1024 lanes (128 VGPRs a lane)
-  constexpr int NC = std::is_same<E, F16>::value ? 8 : 12, G = 4;
+  // NC (with NL below) is the largest head that compiles without spills at 1024 lanes (128
+  // VGPRs a lane)
+  constexpr int NC = 8, G = 4;
   __shared__ double red_sum[16];
   const int nvec = hidden / VEC;
   const int tpr = (int)blockDim.x, tid = (int)threadIdx.x;
@@ -150,7 +151,35 @@ k_fused_add_rms_norm_wide(typename E::S* __restrict__ x, int64_t x_stride,
     }
     __builtin_amdgcn_sched_barrier(0);  // at most G vectors' loads in flight
   }
-  const int tail0 = NC * tpr + tid;
+  // The next NL vectors of every lane are held in LDS: lane-private slots (vector c of lane t
+  // at [c][t]), so no barrier is needed; the workgroup already fills a CU's registers, so the
+  // 128 KB cost no occupancy.  With them a 131072-wide bf16 row is read once.  (Not for fp16,
+  // whose conversions leave no registers for the LDS traffic.)
+  constexpr int NL = VEC > 1 && !std::is_same<E, F16>::value ? 8 : 0;
+  __shared__ Pack<S, VEC> lds[NL > 0 ? NL : 1][kWideLanes];
+  int tid1 = tid;  // opaque copies of the lane index: each loop computes its own addresses
+  asm volatile("" : "+v"(tid1));
+#pragma unroll
+  for (int g = NC; g < NC + NL; g += G) {
+    Pack<S, VEC> xv[G], rv[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      xv[k] = ld<S, VEC>(xr + head_off(g + k, tid1));
+      rv[k] = ld<S, VEC>(rr + head_off(g + k, tid1));
+    }
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      Pack<S, VEC> z;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) z.v[e] = E::from_f(E::to_f(xv[k].v[e]) + E::to_f(rv[k].v[e]));
+      const double vs = sum_sq(z);
+      ss += (g + k) * tpr + tid1 < nvec ? vs : 0.0;
+      lds[g + k - NC][tid] = z;
+      if ((g + k) * tpr + tid1 < nvec) st<S, VEC>(rr + head_off(g + k, tid1), z);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const int tail0 = (NC + NL) * tpr + tid;
   for (int j = tail0; j < nvec; j += tpr) ss += sum_sq(z_of(j * VEC));
   ss = row_reduce(ss, red_sum, tpr, SumOp());
   const float rho = mcop_inv_rms(ss, hidden, eps);
@@ -175,6 +204,20 @@ k_fused_add_rms_norm_wide(typename E::S* __restrict__ x, int64_t x_stride,
     for (int k = 0; k < G; ++k) {
       const Pack<S, VEC> y = y_of(zc[g + k], wv[k]);
       if ((g + k) * tpr + tid2 < nvec) st<S, VEC>(xr + head_off(g + k, tid2), y);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  int tid3 = tid;
+  asm volatile("" : "+v"(tid3));
+#pragma unroll
+  for (int g = NC; g < NC + NL; g += G) {
+    Pack<S, VEC> wv[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k) wv[k] = ld<S, VEC>(w + head_off(g + k, tid3));
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const Pack<S, VEC> y = y_of(lds[g + k - NC][tid], wv[k]);
+      if ((g + k) * tpr + tid3 < nvec) st<S, VEC>(xr + head_off(g + k, tid3), y);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
