@@ -160,7 +160,7 @@ k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 
 // Rows too wide for the registers: one 1024-lane workgroup per row and three passes over it --
 // sum of squares; absmax of v; after_res, after_norm and the codes.  The row head stays in
-// registers; each pass re-reads the rest of x (and of the residual, which this operator only
+// registers and LDS; each pass re-reads the rest of x (and of the residual, which this operator only
 // reads), and the weight and smooth vectors (shared by all rows).
 template <class E, class EW, class ES, int VEC, bool FP8, bool RES>
 __global__ void __launch_bounds__(kWideLanes)
@@ -173,9 +173,10 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
                              uint32_t flags) {
   using S = typename E::S;
   // The row head (the lane's first NC vectors of x, and of the residual) is loaded once and
-  // kept in registers across the three passes; the passes re-read only the rest of the row.
+  // kept in registers across the three passes, the next NL in LDS; the passes re-read only the
+  // rest of the row.
   // NC is the largest head that compiles without spills at 1024 lanes (128 VGPRs a lane).
-  constexpr int NC = VEC > 1 ? (RES ? 4 : sizeof(typename EW::S) == 4 ? 7 : 8) : 16;
+  constexpr int NC = VEC > 1 ? (RES ? 4 : sizeof(typename EW::S) == 4 ? 5 : 6) : 16;
   __shared__ double red_sum[16];
   __shared__ float red_max[16];
   const int nvec = hidden / VEC;
@@ -190,11 +191,34 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
       if constexpr (RES) rc[c] = ld<S, VEC>(res + base + (int64_t)j * VEC);
     }
   }
-  auto t_head = [&](int c, float* t) {  // a = x (+ r), unrounded
+  // The next NL vectors of every lane are held in LDS: lane-private slots (vector c of lane t
+  // at [c][t]: consecutive lanes, consecutive 16-byte slots), so no barrier is needed.  The
+  // workgroup already fills a CU's registers, so the 128 KB cost no occupancy.
+  constexpr int NL = VEC > 1 ? (RES ? 4 : 8) : 0;
+  constexpr int NLS = NL > 0 ? NL * (RES ? 2 : 1) : 1;
+  __shared__ Pack<S, VEC> lds[NLS][kWideLanes];
+  const int tid = (int)threadIdx.x;
+#pragma unroll
+  for (int c = 0; c < NL; ++c) {
+    const int j = (NC + c) * tpr + tid;
+    if (j < nvec) {
+      lds[c][tid] = ld<S, VEC>(x + base + (int64_t)j * VEC);
+      if constexpr (RES) lds[NL + c][tid] = ld<S, VEC>(res + base + (int64_t)j * VEC);
+    }
+  }
+  auto t_head = [&](int c, float* t) {  // a = x (+ r), unrounded; c < NC + NL
+    Pack<S, VEC> xv, rv;
+    if (c < NC) {
+      xv = xc[c];
+      if constexpr (RES) rv = rc[c];
+    } else {
+      xv = lds[c - NC][tid];
+      if constexpr (RES) rv = lds[NL + c - NC][tid];
+    }
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      t[e] = E::to_f(xc[c].v[e]);
-      if constexpr (RES) t[e] += E::to_f(rc[c].v[e]);
+      t[e] = E::to_f(xv.v[e]);
+      if constexpr (RES) t[e] += E::to_f(rv.v[e]);
     }
   };
   auto t_of = [&](int64_t o, float* t) {
@@ -207,10 +231,10 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
       if constexpr (RES) t[e] += E::to_f(rv.v[e]);
     }
   };
-  const int tail0 = NC * tpr + (int)threadIdx.x;  // the lane's first re-read vector
+  const int tail0 = (NC + NL) * tpr + (int)threadIdx.x;  // the lane's first re-read vector
   double ss = 0.0;
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
+  for (int c = 0; c < NC + NL; ++c) {
     if (c * tpr + (int)threadIdx.x < nvec) {
       float t[VEC];
       t_head(c, t);
@@ -252,7 +276,7 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
   };
   float amax = 0.0f;
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
+  for (int c = 0; c < NC + NL; ++c) {
     const int j = c * tpr + (int)threadIdx.x;
     if (j < nvec) {
       float t[VEC], u[VEC], v[VEC];
@@ -297,7 +321,7 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
     st<uint8_t, VEC>(out + base + o, q);
   };
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
+  for (int c = 0; c < NC + NL; ++c) {
     const int j = c * tpr + (int)threadIdx.x;
     if (j < nvec) {
       float t[VEC];
