@@ -82,40 +82,72 @@ k_scale_dynamic_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 }
 
 // Rows too wide for the registers: one 1024-lane workgroup per row and two passes over it
-// (absmax; codes), the second re-reading the row and the smooth scales.
+// (absmax; codes).  The row's head stays on chip between the passes -- the first NC vectors of
+// every lane in registers, the next NL in lane-private LDS slots (vector c of lane t at [c][t],
+// so no barrier is needed; the workgroup already fills a CU's registers, so the 128 KB cost no
+// occupancy) -- and the second pass re-reads the rest of the row and the smooth scales.
 template <int VEC>
 __global__ void __launch_bounds__(kWideLanes)
 k_scale_dynamic_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
                            const uint16_t* __restrict__ x, const float* __restrict__ sm,
                            int hidden) {
+  constexpr int NC = VEC > 1 ? 8 : 16, NL = VEC > 1 ? 8 : 0;
   __shared__ float red_max[16];
+  __shared__ Pack<uint16_t, VEC> lds[NL > 0 ? NL : 1][kWideLanes];
   const int nvec = hidden / VEC;
-  const int tpr = (int)blockDim.x;
+  const int tpr = (int)blockDim.x, tid = (int)threadIdx.x;
   const int64_t base = (int64_t)blockIdx.x * hidden;
-  auto v_of = [&](int64_t o, float* v) {
-    const Pack<uint16_t, VEC> xv = ld<uint16_t, VEC>(x + base + o);
+  auto v_from = [&](const Pack<uint16_t, VEC>& xv, int64_t o, float* v) {
     const Pack<float, VEC> sv = ld<float, VEC>(sm + o);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) v[e] = BF16::to_f(xv.v[e]) * sv.v[e];
   };
+  Pack<uint16_t, VEC> xc[NC];
+#pragma unroll
+  for (int c = 0; c < NC + NL; ++c) {
+    const int j = c * tpr + tid;
+    if (j < nvec) {
+      const Pack<uint16_t, VEC> xv = ld<uint16_t, VEC>(x + base + (int64_t)j * VEC);
+      if (c < NC) xc[c] = xv; else lds[c - NC][tid] = xv;
+    }
+  }
+  auto head = [&](int c) -> Pack<uint16_t, VEC> { return c < NC ? xc[c] : lds[c - NC][tid]; };
   float amax = 0.0f;
-  for (int j = threadIdx.x; j < nvec; j += tpr) {
+#pragma unroll
+  for (int c = 0; c < NC + NL; ++c) {
+    const int j = c * tpr + tid;
+    if (j < nvec) {
+      float v[VEC];
+      v_from(head(c), (int64_t)j * VEC, v);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[e]));
+    }
+  }
+  const int tail0 = (NC + NL) * tpr + tid;
+  for (int j = tail0; j < nvec; j += tpr) {
     float v[VEC];
-    v_of((int64_t)j * VEC, v);
+    v_from(ld<uint16_t, VEC>(x + base + (int64_t)j * VEC), (int64_t)j * VEC, v);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[e]));
   }
   amax = row_reduce(amax, red_max, tpr, MaxOp());
   if (threadIdx.x == 0) scales[blockIdx.x] = amax * 0.00787401574803f;
   const float inv = amax > 0.0f ? mcop_div_rn(127.0f, amax) : 0.0f;
-  for (int j = threadIdx.x; j < nvec; j += tpr) {
-    const int64_t o = (int64_t)j * VEC;
+  auto emit = [&](const Pack<uint16_t, VEC>& xv, int64_t o) {
     float v[VEC];
-    v_of(o, v);
+    v_from(xv, o, v);
     Pack<uint8_t, VEC> q;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(v[e] * inv);
     st<uint8_t, VEC>(out + base + o, q);
+  };
+#pragma unroll
+  for (int c = 0; c < NC + NL; ++c) {
+    const int j = c * tpr + tid;
+    if (j < nvec) emit(head(c), (int64_t)j * VEC);
+  }
+  for (int j = tail0; j < nvec; j += tpr) {
+    emit(ld<uint16_t, VEC>(x + base + (int64_t)j * VEC), (int64_t)j * VEC);
   }
 }
 

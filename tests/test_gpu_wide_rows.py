@@ -31,7 +31,7 @@ def _w(H, seed, dtype):
     return (1 + 0.1 * torch.randn(H, generator=gen(seed))).to(dtype)
 
 
-@pytest.mark.parametrize("dtype,H", SHAPES)
+@pytest.mark.parametrize("dtype,H", SHAPES + [(torch.bfloat16, 163848)])  # past the LDS-held part
 def test_wide_h1_fused_add_rms_norm(dtype, H):
     say(f"wide H1 {dtype} H={H}")
     x, r, w = _x(3, H, 1, dtype), _x(3, H, 2, dtype), _w(H, 3, dtype)
@@ -107,7 +107,7 @@ def test_wide_h4_smooth_quant(dtype, H, qdt):
         assert_codes(q, q_ref, tag + " codes")
 
 
-@pytest.mark.parametrize("H", [65544, 131072, 20001])
+@pytest.mark.parametrize("H", [65544, 131072, 20001, 163848])
 def test_wide_h5_scale_dynamic_quant(H):
     say(f"wide H5 H={H}")
     h = _x(3, H, 14, torch.bfloat16)
