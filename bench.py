@@ -45,7 +45,7 @@ def parse():
                              "cfg5-decode4", "cfg5-decode16", "cfg5-decode64", "ptq-int8",
                              "ptq-int8-azp", "ptq-fp8", "padded", "block-fp8", "norm-res",
                              "vllm-norm", "head-norm", "sdq", "wide-int8", "wide-fused",
-                             "wide-fp8", "wide-sdq"])
+                             "wide-fp8", "wide-sdq", "wide-norm", "wide-ptq"])
     ap.add_argument("--sets", type=int, default=0,
                     help="rotated input sets (default: enough for > 1 GiB, at least 3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -194,6 +194,8 @@ WORKLOADS = {
     "wide-fused": Workload("wide-fused", 2048, 131072, 1e-6, "fused_add"),
     "wide-fp8": Workload("wide-fp8", 2048, 131072, 1e-6, "smooth_fp8"),
     "wide-sdq": Workload("wide-sdq", 2048, 131072, 0.0, "sdq"),
+    "wide-norm": Workload("wide-norm", 2048, 131072, 1e-6, "norm_res"),
+    "wide-ptq": Workload("wide-ptq", 2048, 131072, 0.0, "ptq_int8"),
 }
 KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "fused_add": "k_fused_add_rms_norm",
                "smooth_fp8": "k_rms_norm_smooth_quant", "ptq_int8": "k_per_token_quant",
@@ -205,7 +207,8 @@ KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "fused_add": "k_fused_add_rm
 KERNEL_NAME_OF_WORKLOAD = {"wide-int8": "k_rms_norm_quant_wide",
                            "wide-fused": "k_fused_add_rms_norm_wide",
                            "wide-fp8": "k_rms_norm_smooth_quant_wide",
-                           "wide-sdq": "k_scale_dynamic_quant_wide"}
+                           "wide-sdq": "k_scale_dynamic_quant_wide",
+                           "wide-norm": "k_rms_norm_wide", "wide-ptq": "k_per_token_quant_wide"}
 
 
 def kernel_name(wl) -> str:

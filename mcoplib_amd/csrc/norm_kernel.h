@@ -183,7 +183,11 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
 }
 
 // Rows too wide for the registers: one 1024-lane workgroup per row, two passes (sum of squares;
-// after_res and the output), the second re-reading x, residual and weight.
+// after_res and the output).  The row's head stays on chip between the passes -- the first NC
+// vectors of x (and residual) of every lane in registers, the next NL in lane-private LDS slots
+// (vector c of lane t at [c][t], so no barrier is needed; the workgroup already fills a CU's
+// registers, so the 128 KB cost no occupancy) -- and the second pass re-reads the rest of the
+// row, and the weight.
 template <class E, class EW, int VEC, bool RES>
 __global__ void __launch_bounds__(kWideLanes)
 k_rms_norm_wide(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
@@ -191,23 +195,68 @@ k_rms_norm_wide(typename E::S* __restrict__ out, typename E::S* __restrict__ are
                 const typename E::S* __restrict__ res, RowMap map, int hidden, float eps,
                 int mode, int rms_div) {
   using S = typename E::S;
+  // NC: the largest register head that compiles without spills at 1024 lanes (fp16 conversions
+  // take more registers)
+  constexpr int NC = VEC > 1 ? (RES ? 4 : std::is_same<E, F16>::value ? 4 : 8) : 16;
+  constexpr int NL = VEC > 1 ? (RES ? 4 : 8) : 0;
+  constexpr int NLS = NL > 0 ? NL * (RES ? 2 : 1) : 1;
   __shared__ double red_sum[16];
+  __shared__ Pack<S, VEC> lds[NLS][kWideLanes];
   const int nvec = hidden / VEC;
-  const int tpr = (int)blockDim.x;
+  const int tpr = (int)blockDim.x, tid = (int)threadIdx.x;
   const RowOffsets lo = row_offsets(map, blockIdx.x);
   const int64_t rbase = (int64_t)blockIdx.x * hidden;
-  auto t_of = [&](int64_t o, float* t) {
-    const Pack<S, VEC> xv = ld<S, VEC>(x + lo.in + o);
-    Pack<S, VEC> rv;
-    if constexpr (RES) rv = ld<S, VEC>(res + rbase + o);
+  auto t_from = [&](const Pack<S, VEC>& xv, const Pack<S, VEC>& rv, float* t) {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       t[e] = E::to_f(xv.v[e]);
       if constexpr (RES) t[e] += E::to_f(rv.v[e]);
     }
   };
+  auto t_of = [&](int64_t o, float* t) {
+    const Pack<S, VEC> xv = ld<S, VEC>(x + lo.in + o);
+    Pack<S, VEC> rv;
+    if constexpr (RES) rv = ld<S, VEC>(res + rbase + o);
+    t_from(xv, rv, t);
+  };
+  Pack<S, VEC> xc[NC], rc[NC];
+#pragma unroll
+  for (int c = 0; c < NC + NL; ++c) {
+    const int j = c * tpr + tid;
+    if (j < nvec) {
+      const Pack<S, VEC> xv = ld<S, VEC>(x + lo.in + (int64_t)j * VEC);
+      Pack<S, VEC> rv;
+      if constexpr (RES) rv = ld<S, VEC>(res + rbase + (int64_t)j * VEC);
+      if (c < NC) {
+        xc[c] = xv;
+        if constexpr (RES) rc[c] = rv;
+      } else {
+        lds[c - NC][tid] = xv;
+        if constexpr (RES) lds[NL + c - NC][tid] = rv;
+      }
+    }
+  }
+  auto t_head = [&](int c, float* t) {
+    if (c < NC) {
+      t_from(xc[c], rc[c], t);
+    } else {
+      Pack<S, VEC> rv;
+      if constexpr (RES) rv = lds[NL + c - NC][tid];
+      t_from(lds[c - NC][tid], rv, t);
+    }
+  };
   double ss = 0.0;
-  for (int j = threadIdx.x; j < nvec; j += tpr) {
+#pragma unroll
+  for (int c = 0; c < NC + NL; ++c) {
+    if (c * tpr + tid < nvec) {
+      float t[VEC];
+      t_head(c, t);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) ss = __builtin_fma((double)t[e], (double)t[e], ss);
+    }
+  }
+  const int tail0 = (NC + NL) * tpr + tid;
+  for (int j = tail0; j < nvec; j += tpr) {
     float t[VEC];
     t_of((int64_t)j * VEC, t);
 #pragma unroll
@@ -216,10 +265,7 @@ k_rms_norm_wide(typename E::S* __restrict__ out, typename E::S* __restrict__ are
   ss = row_reduce(ss, red_sum, tpr, SumOp());
   const float rho = mcop_inv_rms(ss, hidden, eps);
   const float inv_rho = mcop_div_rn(1.0f, rho);
-  for (int j = threadIdx.x; j < nvec; j += tpr) {
-    const int64_t o = (int64_t)j * VEC;
-    float t[VEC];
-    t_of(o, t);
+  auto emit = [&](int64_t o, float* t) {
     if constexpr (RES) {
       Pack<S, VEC> r;
 #pragma unroll
@@ -233,6 +279,20 @@ k_rms_norm_wide(typename E::S* __restrict__ out, typename E::S* __restrict__ are
     NormW<EW, VEC> wv;
     wv.p = ld<typename EW::S, VEC>(w + lo.w + o);
     st<S, VEC>(out + lo.out + o, norm_out<E, EW, VEC>(t, wv, rho, inv_rho, mode, rms_div));
+  };
+#pragma unroll
+  for (int c = 0; c < NC + NL; ++c) {
+    const int j = c * tpr + tid;
+    if (j < nvec) {
+      float t[VEC];
+      t_head(c, t);
+      emit((int64_t)j * VEC, t);
+    }
+  }
+  for (int j = tail0; j < nvec; j += tpr) {
+    float t[VEC];
+    t_of((int64_t)j * VEC, t);
+    emit((int64_t)j * VEC, t);
   }
 }
 

@@ -11,7 +11,7 @@
 //   fp8 e4m3fn       op/vllm/quantization/fp8/common.cu:142-180
 //     A = max|v| (min with *scale_ub); s = max(A / 448, 1/(448*512)); q = e4m3fn(clamp(v / s))
 // The row is loaded once into VGPRs; one max reduction (two for the zero point form).  Rows too
-// wide for the registers take k_per_token_quant_wide (two passes over the row).
+// wide for the registers take k_per_token_quant_wide (two passes, the row's head held on chip).
 #include <hip/hip_runtime.h>
 
 #include "../../include/mcop_norm.h"
@@ -155,7 +155,10 @@ k_per_token_quant(uint8_t* __restrict__ out, float* __restrict__ scales, int32_t
 }
 
 // Rows too wide for the registers: one 1024-lane workgroup per row, two passes (max / min;
-// codes), the second re-reading the row.
+// codes).  The row's head stays on chip between the passes -- the first NC vectors of every
+// lane in registers, the next NL in lane-private LDS slots (vector c of lane t at [c][t], so no
+// barrier is needed; the workgroup already fills a CU's registers, so the 128 KB cost no
+// occupancy) -- and the second pass re-reads only the rest.
 template <class E, int VEC, int MODE>
 __global__ void __launch_bounds__(kWideLanes)
 k_per_token_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
@@ -163,15 +166,36 @@ k_per_token_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
                        const float* __restrict__ scale_ub, int hidden, int64_t in_stride,
                        int64_t out_stride) {
   using S = typename E::S;
+  constexpr int NC = VEC > 1 ? 8 : 16, NL = VEC > 1 ? 8 : 0;
   __shared__ float red_a[16];
   __shared__ float red_b[16];
+  __shared__ Pack<S, VEC> lds[NL > 0 ? NL : 1][kWideLanes];
   const int nvec = hidden / VEC;
-  const int tpr = (int)blockDim.x;
+  const int tpr = (int)blockDim.x, tid = (int)threadIdx.x;
   const S* xr = x + (int64_t)blockIdx.x * in_stride;
   uint8_t* orow = out + (int64_t)blockIdx.x * out_stride;
+  Pack<S, VEC> xc[NC];
+#pragma unroll
+  for (int c = 0; c < NC + NL; ++c) {
+    const int j = c * tpr + tid;
+    if (j < nvec) {
+      const Pack<S, VEC> xv = ld<S, VEC>(xr + (int64_t)j * VEC);
+      if (c < NC) xc[c] = xv; else lds[c - NC][tid] = xv;
+    }
+  }
+  auto head = [&](int c) -> Pack<S, VEC> { return c < NC ? xc[c] : lds[c - NC][tid]; };
   float mx = MODE == PTQ_INT8_AZP ? -__builtin_inff() : 0.0f;
   float nmn = -__builtin_inff();
-  for (int j = threadIdx.x; j < nvec; j += tpr) {
+#pragma unroll
+  for (int c = 0; c < NC + NL; ++c) {
+    if (c * tpr + tid < nvec) {
+      const Pack<S, VEC> xv = head(c);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) ptq_fold<MODE>(E::to_f(xv.v[e]), mx, nmn);
+    }
+  }
+  const int tail0 = (NC + NL) * tpr + tid;
+  for (int j = tail0; j < nvec; j += tpr) {
     const Pack<S, VEC> xv = ld<S, VEC>(xr + (int64_t)j * VEC);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) ptq_fold<MODE>(E::to_f(xv.v[e]), mx, nmn);
@@ -183,12 +207,19 @@ k_per_token_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
     scales[blockIdx.x] = r.s;
     if constexpr (MODE == PTQ_INT8_AZP) azp[blockIdx.x] = r.zp;
   }
-  for (int j = threadIdx.x; j < nvec; j += tpr) {
-    const Pack<S, VEC> xv = ld<S, VEC>(xr + (int64_t)j * VEC);
+  auto emit = [&](const Pack<S, VEC>& xv, int64_t o) {
     float a[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) a[e] = E::to_f(xv.v[e]);
-    st<uint8_t, VEC>(orow + (int64_t)j * VEC, ptq_codes<E, VEC, MODE>(a, r));
+    st<uint8_t, VEC>(orow + o, ptq_codes<E, VEC, MODE>(a, r));
+  };
+#pragma unroll
+  for (int c = 0; c < NC + NL; ++c) {
+    const int j = c * tpr + tid;
+    if (j < nvec) emit(head(c), (int64_t)j * VEC);
+  }
+  for (int j = tail0; j < nvec; j += tpr) {
+    emit(ld<S, VEC>(xr + (int64_t)j * VEC), (int64_t)j * VEC);
   }
 }
 

@@ -139,7 +139,7 @@ def test_wide_rows_many_rows():
 
 
 @pytest.mark.parametrize("dtype,H", [(torch.bfloat16, 65544), (torch.bfloat16, 65537),
-                                     (torch.float32, 32772)])
+                                     (torch.float32, 32772), (torch.bfloat16, 163848)])
 def test_wide_standalone_quantizers(dtype, H):
     say(f"wide quantizers {dtype} H={H}")
     x = _x(3, H, 20, dtype)
@@ -225,7 +225,8 @@ def test_wide_per_block(qdt, G, misaligned):
 @pytest.mark.parametrize("dtype,wdtype,H", [(torch.bfloat16, torch.bfloat16, 65544),
                                             (torch.float16, torch.float32, 65608),
                                             (torch.float32, torch.float32, 32776),
-                                            (torch.bfloat16, torch.bfloat16, 20001)])
+                                            (torch.bfloat16, torch.bfloat16, 20001),
+                                            (torch.bfloat16, torch.float32, 163848)])
 def test_wide_norms(dtype, wdtype, H):
     say(f"wide norms {dtype} w={wdtype} H={H}")
     x, r, w = _x(3, H, 27, dtype), _x(3, H, 28, dtype), _w(H, 29, wdtype)
