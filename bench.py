@@ -45,7 +45,8 @@ def parse():
                              "cfg5-decode4", "cfg5-decode16", "cfg5-decode64", "ptq-int8",
                              "ptq-int8-azp", "ptq-fp8", "padded", "block-fp8", "norm-res",
                              "vllm-norm", "head-norm", "sdq", "wide-int8", "wide-fused",
-                             "wide-fp8", "wide-sdq", "wide-norm", "wide-ptq"])
+                             "wide-fp8", "wide-sdq", "wide-norm", "wide-ptq", "wide-padded",
+                             "wide-block"])
     ap.add_argument("--sets", type=int, default=0,
                     help="rotated input sets (default: enough for > 1 GiB, at least 3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -63,6 +64,11 @@ class Workload:
 
     def __init__(self, name, T, H, eps, kind):
         self.name, self.T, self.H, self.eps, self.kind = name, T, H, eps, kind
+
+    @property
+    def pad(self) -> int:
+        """Padded row size in bf16 elements (padded workloads): PAD_SIZE, or enough for H + 4."""
+        return PAD_SIZE if 2 * PAD_SIZE >= self.H + 4 else (self.H + 4 + 63) // 64 * 32
 
     @property
     def bytes(self) -> int:
@@ -115,7 +121,7 @@ class Workload:
             d["q"] = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=dev)
             d["s"] = torch.empty(T, H // BLOCK_GROUP, dtype=torch.float32, device=dev)
         if self.kind == "padded":
-            d["p"] = torch.empty(T, 2 * PAD_SIZE, dtype=torch.int8, device=dev)
+            d["p"] = torch.empty(T, 2 * self.pad, dtype=torch.int8, device=dev)
             d["rms"] = torch.empty_like(x)
             d["q"] = torch.empty(T, H, dtype=torch.int8, device=dev)
             d["s"] = torch.empty(T, 1, dtype=torch.float32, device=dev)
@@ -155,7 +161,7 @@ class Workload:
                 d["q"], d["x"], d["w"], d["s"], self.eps, None, d["r"], BLOCK_GROUP, False)
         if self.kind == "padded":
             return lambda: op.fused_add_rms_norm_dynamic_per_token_quant_padding_output(
-                d["p"], d["rms"], d["q"], d["s"], d["x"], d["r"], d["w"], PAD_SIZE, self.eps)
+                d["p"], d["rms"], d["q"], d["s"], d["x"], d["r"], d["w"], self.pad, self.eps)
         if self.kind == "sdq":  # returns new tensors, as the reference's op does
             return lambda: op.scale_dynamic_quant(d["x"], d["sm"], torch.int8)
         if self.kind == "ptq_fp8":
@@ -196,6 +202,8 @@ WORKLOADS = {
     "wide-sdq": Workload("wide-sdq", 2048, 131072, 0.0, "sdq"),
     "wide-norm": Workload("wide-norm", 2048, 131072, 1e-6, "norm_res"),
     "wide-ptq": Workload("wide-ptq", 2048, 131072, 0.0, "ptq_int8"),
+    "wide-padded": Workload("wide-padded", 2048, 131072, 1e-6, "padded"),
+    "wide-block": Workload("wide-block", 2048, 131072, 1e-6, "block_fp8"),
 }
 KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "fused_add": "k_fused_add_rms_norm",
                "smooth_fp8": "k_rms_norm_smooth_quant", "ptq_int8": "k_per_token_quant",
@@ -208,7 +216,9 @@ KERNEL_NAME_OF_WORKLOAD = {"wide-int8": "k_rms_norm_quant_wide",
                            "wide-fused": "k_fused_add_rms_norm_wide",
                            "wide-fp8": "k_rms_norm_smooth_quant_wide",
                            "wide-sdq": "k_scale_dynamic_quant_wide",
-                           "wide-norm": "k_rms_norm_wide", "wide-ptq": "k_per_token_quant_wide"}
+                           "wide-norm": "k_rms_norm_wide", "wide-ptq": "k_per_token_quant_wide",
+                           "wide-padded": "k_add_rms_norm_quant_padded_wide",
+                           "wide-block": "k_rms_norm_group_quant_wide"}
 
 
 def kernel_name(wl) -> str:
@@ -257,7 +267,7 @@ def cpu_baseline(wl: Workload, seconds: float) -> dict:
             oracle.rms_norm_per_block_quant(x, w, wl.eps, torch.float8_e4m3fn, BLOCK_GROUP,
                                             residual=r)
         elif wl.kind == "padded":
-            oracle.add_rms_norm_quant_padded(x, r, w, PAD_SIZE, wl.eps)
+            oracle.add_rms_norm_quant_padded(x, r, w, wl.pad, wl.eps)
         elif wl.kind == "sdq":
             oracle.scale_dynamic_quant(x, sm)
         elif wl.kind == "ptq_fp8":

@@ -178,10 +178,14 @@ k_rms_norm_group_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 }
 
 // Rows too wide for the registers: one 1024-lane workgroup per row, two passes (sum of squares;
-// codes, scales and the residual), the second re-reading x, residual and weight; the residual
-// is written in the last pass only, by the lane that read it.  A lane takes U consecutive
-// elements per step (one 16-byte vector, or four scalars on the scalar path), so a group spans
-// group / U aligned lanes (<= 64) and 1024 lanes hold whole groups.
+// codes, scales and the residual).  The row's head stays on chip between the passes -- the
+// first NC units of x (and residual) of every lane in registers, the next NL in lane-private LDS
+// slots (unit c of lane t at [c][t], so no barrier is needed; the workgroup already fills a
+// CU's registers, so the 128 KB cost no occupancy) -- and the second pass re-reads the rest,
+// and the weight; the residual is written in the last pass only, by the lane that read it.  A
+// lane takes U consecutive elements per step (one 16-byte vector, or four scalars on the scalar
+// path), so a group spans group / U aligned lanes (<= 64), 1024 lanes hold whole groups, and a
+// unit's bound check is the same for all lanes of its group.
 template <class E, int U, bool VECLD, bool FP8, bool RES>
 __global__ void __launch_bounds__(kWideLanes)
 k_rms_norm_group_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
@@ -191,31 +195,73 @@ k_rms_norm_group_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scale
                             int hidden, float eps, int group, int64_t scale_row_stride,
                             int64_t scale_group_stride) {
   using S = typename E::S;
+  constexpr int NC = VECLD ? (RES ? 4 : 8) : 8, NL = VECLD ? (RES ? 4 : 8) : 0;
+  constexpr int NLS = NL > 0 ? NL * (RES ? 2 : 1) : 1;
   __shared__ double red_sum[16];
+  __shared__ Pack<S, U> lds[NLS][kWideLanes];
   const int nunit = hidden / U;
-  const int tpr = (int)blockDim.x;
+  const int tpr = (int)blockDim.x, tid = (int)threadIdx.x;
   const int64_t base = (int64_t)blockIdx.x * hidden;
-  auto load = [&](const S* p, float* f) {
+  auto raw = [&](const S* p) {
+    Pack<S, U> v;
     if constexpr (VECLD) {
-      const Pack<S, U> v = ld<S, U>(p);
-#pragma unroll
-      for (int e = 0; e < U; ++e) f[e] = E::to_f(v.v[e]);
+      v = ld<S, U>(p);
     } else {
 #pragma unroll
-      for (int e = 0; e < U; ++e) f[e] = E::to_f(p[e]);
+      for (int e = 0; e < U; ++e) v.v[e] = p[e];
+    }
+    return v;
+  };
+  auto t_from = [&](const Pack<S, U>& xv, const Pack<S, U>& rv, float* t) {
+#pragma unroll
+    for (int e = 0; e < U; ++e) {
+      t[e] = E::to_f(xv.v[e]);
+      if constexpr (RES) t[e] += E::to_f(rv.v[e]);
     }
   };
   auto t_of = [&](int64_t o, float* t) {
-    load(x + base + o, t);
-    if constexpr (RES) {
-      float r[U];
-      load(res + base + o, r);
+    Pack<S, U> rv;
+    if constexpr (RES) rv = raw(res + base + o);
+    t_from(raw(x + base + o), rv, t);
+  };
+  Pack<S, U> xc[NC], rc[NC];
 #pragma unroll
-      for (int e = 0; e < U; ++e) t[e] += r[e];
+  for (int c = 0; c < NC + NL; ++c) {
+    const int j = c * tpr + tid;
+    if (j < nunit) {
+      const Pack<S, U> xv = raw(x + base + (int64_t)j * U);
+      Pack<S, U> rv;
+      if constexpr (RES) rv = raw(res + base + (int64_t)j * U);
+      if (c < NC) {
+        xc[c] = xv;
+        if constexpr (RES) rc[c] = rv;
+      } else {
+        lds[c - NC][tid] = xv;
+        if constexpr (RES) lds[NL + c - NC][tid] = rv;
+      }
+    }
+  }
+  auto t_head = [&](int c, float* t) {
+    if (c < NC) {
+      t_from(xc[c], rc[c], t);
+    } else {
+      Pack<S, U> rv;
+      if constexpr (RES) rv = lds[NL + c - NC][tid];
+      t_from(lds[c - NC][tid], rv, t);
     }
   };
   double ss = 0.0;
-  for (int j = threadIdx.x; j < nunit; j += tpr) {
+#pragma unroll
+  for (int c = 0; c < NC + NL; ++c) {
+    if (c * tpr + tid < nunit) {
+      float t[U];
+      t_head(c, t);
+#pragma unroll
+      for (int e = 0; e < U; ++e) ss = __builtin_fma((double)t[e], (double)t[e], ss);
+    }
+  }
+  const int tail0 = (NC + NL) * tpr + tid;
+  for (int j = tail0; j < nunit; j += tpr) {
     float t[U];
     t_of((int64_t)j * U, t);
 #pragma unroll
@@ -224,11 +270,11 @@ k_rms_norm_group_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scale
   ss = row_reduce(ss, red_sum, tpr, SumOp());
   const float rho = mcop_inv_rms(ss, hidden, eps);
   const float ub = scale_ub != nullptr ? *scale_ub : 0.0f;
-  for (int j = threadIdx.x; j < nunit; j += tpr) {
-    const int64_t o = (int64_t)j * U;
-    float t[U], wf[U], y[U];
-    t_of(o, t);
-    load(w + o, wf);
+  auto emit = [&](int64_t o, const float* t) {
+    float wf[U], y[U];
+    const Pack<S, U> wv = raw(w + o);
+#pragma unroll
+    for (int e = 0; e < U; ++e) wf[e] = E::to_f(wv.v[e]);
     float m = 0.0f;
 #pragma unroll
     for (int e = 0; e < U; ++e) {
@@ -258,6 +304,20 @@ k_rms_norm_group_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scale
 #pragma unroll
       for (int e = 0; e < U; ++e) out[base + o + e] = q.v[e];
     }
+  };
+#pragma unroll
+  for (int c = 0; c < NC + NL; ++c) {
+    const int j = c * tpr + tid;
+    if (j < nunit) {
+      float t[U];
+      t_head(c, t);
+      emit((int64_t)j * U, t);
+    }
+  }
+  for (int j = tail0; j < nunit; j += tpr) {
+    float t[U];
+    t_of((int64_t)j * U, t);
+    emit((int64_t)j * U, t);
   }
 }
 

@@ -132,8 +132,12 @@ k_add_rms_norm_quant_padded(uint8_t* __restrict__ padded, uint16_t* __restrict__
 
 // Rows too wide for the registers (the generic chain: 7168-wide rows always fit): one 1024-lane
 // workgroup per row, two passes (sum of squares and absmax, which does not need rho; then the
-// residual, rms, codes, padded codes and scale), the second re-reading x, residual and weight;
-// the residual is written in the last pass only, by the lane that read it.
+// residual, rms, codes, padded codes and scale).  The row's head stays on chip as the rounded
+// sums z = b(x + r) -- the first NC vectors of every lane in registers, the next NL in
+// lane-private LDS slots (vector c of lane t at [c][t], so no barrier is needed; the workgroup
+// already fills a CU's registers, so the 128 KB cost no occupancy) -- and its residual is
+// written in the first pass.  The second pass re-reads the rest of x and residual, and the
+// weight; the residual of that rest is written in the last pass only, by the lane that read it.
 template <int VEC>
 __global__ void __launch_bounds__(kWideLanes)
 k_add_rms_norm_quant_padded_wide(uint8_t* __restrict__ padded, uint16_t* __restrict__ rms,
@@ -142,30 +146,43 @@ k_add_rms_norm_quant_padded_wide(uint8_t* __restrict__ padded, uint16_t* __restr
                                  const uint16_t* __restrict__ w, int hidden, int64_t pad_bytes,
                                  float eps) {
   using E = BF16;
+  constexpr int NC = VEC > 1 ? 8 : 16, NL = VEC > 1 ? 8 : 0;
   __shared__ double red_sum[16];
   __shared__ float red_max[16];
+  __shared__ Pack<uint16_t, VEC> lds[NL > 0 ? NL : 1][kWideLanes];
   const int nvec = hidden / VEC;
-  const int tpr = (int)blockDim.x;
+  const int tpr = (int)blockDim.x, tid = (int)threadIdx.x;
   const int64_t base = (int64_t)blockIdx.x * hidden;
   const int64_t pbase = (int64_t)blockIdx.x * pad_bytes;
-  auto ld3 = [&](int64_t o, Pack<uint16_t, VEC>& xv, Pack<uint16_t, VEC>& rv,
-                 Pack<uint16_t, VEC>& wv) {
-    xv = ld<uint16_t, VEC>(x + base + o);
-    rv = ld<uint16_t, VEC>(res + base + o);
-    wv = ld<uint16_t, VEC>(w + o);
-  };
   double ss = 0.0;
   float amax = 0.0f;
-  for (int j = threadIdx.x; j < nvec; j += tpr) {
-    Pack<uint16_t, VEC> xv, rv, wv;
-    ld3((int64_t)j * VEC, xv, rv, wv);
+  // sum of squares (on the unrounded sums) and absmax of one vector; returns z = b(x + r)
+  auto fold = [&](int64_t o) {
+    const Pack<uint16_t, VEC> xv = ld<uint16_t, VEC>(x + base + o);
+    const Pack<uint16_t, VEC> rv = ld<uint16_t, VEC>(res + base + o);
+    const Pack<uint16_t, VEC> wv = ld<uint16_t, VEC>(w + o);
+    Pack<uint16_t, VEC> z;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const float t = E::to_f(xv.v[e]) + E::to_f(rv.v[e]);
       ss = __builtin_fma((double)t, (double)t, ss);
-      amax = __builtin_fmaxf(amax, __builtin_fabsf(rnd<E>(rnd<E>(t) * E::to_f(wv.v[e]))));
+      z.v[e] = E::from_f(t);
+      amax = __builtin_fmaxf(amax, __builtin_fabsf(rnd<E>(E::to_f(z.v[e]) * E::to_f(wv.v[e]))));
+    }
+    return z;
+  };
+  Pack<uint16_t, VEC> zc[NC];
+#pragma unroll
+  for (int c = 0; c < NC + NL; ++c) {
+    const int j = c * tpr + tid;
+    if (j < nvec) {
+      const Pack<uint16_t, VEC> z = fold((int64_t)j * VEC);
+      if (c < NC) zc[c] = z; else lds[c - NC][tid] = z;
+      st<uint16_t, VEC>(res + base + (int64_t)j * VEC, z);
     }
   }
+  const int tail0 = (NC + NL) * tpr + tid;
+  for (int j = tail0; j < nvec; j += tpr) (void)fold((int64_t)j * VEC);
   ss = row_reduce(ss, red_sum, tpr, SumOp());
   amax = row_reduce(amax, red_max, tpr, MaxOp());
   const float rho = mcop_inv_rms(ss, hidden, eps);
@@ -182,21 +199,33 @@ k_add_rms_norm_quant_padded_wide(uint8_t* __restrict__ padded, uint16_t* __restr
       for (int k = 0; k < 4; ++k) sp[k] = (uint8_t)(b >> (8 * k));
     }
   }
-  for (int j = threadIdx.x; j < nvec; j += tpr) {
-    const int64_t o = (int64_t)j * VEC;
-    Pack<uint16_t, VEC> xv, rv, wv, zo, ro;
+  auto emit = [&](const Pack<uint16_t, VEC>& z, int64_t o) {
+    const Pack<uint16_t, VEC> wv = ld<uint16_t, VEC>(w + o);
+    Pack<uint16_t, VEC> ro;
     Pack<uint8_t, VEC> q;
-    ld3(o, xv, rv, wv);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      zo.v[e] = E::from_f(E::to_f(xv.v[e]) + E::to_f(rv.v[e]));
-      ro.v[e] = E::from_f(rnd<E>(E::to_f(zo.v[e]) * rho) * E::to_f(wv.v[e]));
+      ro.v[e] = E::from_f(rnd<E>(E::to_f(z.v[e]) * rho) * E::to_f(wv.v[e]));
       q.v[e] = q_i8<-127>(E::to_f(ro.v[e]) * inv);
     }
-    st<uint16_t, VEC>(res + base + o, zo);
     st<uint16_t, VEC>(rms + base + o, ro);
     st<uint8_t, VEC>(q_out + base + o, q);
     st<uint8_t, VEC>(padded + pbase + o, q);
+  };
+#pragma unroll
+  for (int c = 0; c < NC + NL; ++c) {
+    const int j = c * tpr + tid;
+    if (j < nvec) emit(c < NC ? zc[c] : lds[c - NC][tid], (int64_t)j * VEC);
+  }
+  for (int j = tail0; j < nvec; j += tpr) {
+    const int64_t o = (int64_t)j * VEC;
+    const Pack<uint16_t, VEC> xv = ld<uint16_t, VEC>(x + base + o);
+    const Pack<uint16_t, VEC> rv = ld<uint16_t, VEC>(res + base + o);
+    Pack<uint16_t, VEC> z;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) z.v[e] = E::from_f(E::to_f(xv.v[e]) + E::to_f(rv.v[e]));
+    st<uint16_t, VEC>(res + base + o, z);
+    emit(z, o);
   }
 }
 

@@ -170,7 +170,7 @@ def test_wide_standalone_quantizers(dtype, H):
         assert_codes(qb[:, :H].contiguous(), q_ref, f"fp8 ub={ub} codes")
 
 
-@pytest.mark.parametrize("H", [65544, 65540])
+@pytest.mark.parametrize("H", [65544, 65540, 163848])
 def test_wide_padded(H):
     say(f"wide padded H={H}")
     pad = (H + 4 + 63) // 64 * 32
@@ -195,11 +195,12 @@ def test_wide_padded(H):
 @pytest.mark.parametrize("qdt", [torch.int8, torch.float8_e4m3fn])
 @pytest.mark.parametrize("G", [64, 128])
 @pytest.mark.parametrize("misaligned", [False, True])
-def test_wide_per_block(qdt, G, misaligned):
-    say(f"wide per-block {qdt} G={G} misaligned={misaligned}")
-    H = 65536 + 128
-    x, r, w = _x(3, H, 24, torch.bfloat16), _x(3, H, 25, torch.bfloat16), _w(H, 26,
-                                                                             torch.bfloat16)
+@pytest.mark.parametrize("with_res", [True, False])
+def test_wide_per_block(qdt, G, misaligned, with_res):
+    say(f"wide per-block {qdt} G={G} misaligned={misaligned} res={with_res}")
+    H = 65536 + 128 if with_res else 131072 + 128  # past the on-chip head either way
+    x, w = _x(3, H, 24, torch.bfloat16), _w(H, 26, torch.bfloat16)
+    r = _x(3, H, 25, torch.bfloat16) if with_res else None
     for transposed, ub in ((False, None), (True, 0.05 if qdt == torch.float8_e4m3fn else None)):
         q_ref, s_ref, r_ref = oracle.rms_norm_per_block_quant(x, w, 1e-6, qdt, G, ub, r,
                                                               transposed)
@@ -212,12 +213,13 @@ def test_wide_per_block(qdt, G, misaligned):
         q = torch.empty(x.shape, dtype=qdt, device=DEV)
         s = torch.empty(H // G, 3, device=DEV) if transposed else torch.empty(3, H // G,
                                                                                device=DEV)
-        rd = r.to(DEV)
+        rd = r.to(DEV) if with_res else None
         ubd = None if ub is None else torch.tensor([ub], device=DEV)
         torch.ops._C.rms_norm_per_block_quant(q, xd, w.to(DEV), s, 1e-6, ubd, rd, G, transposed)
         torch.cuda.synchronize()
         tag = f"transposed={transposed} ub={ub}"
-        assert_exact(rd, r_ref, tag + " residual")
+        if with_res:
+            assert_exact(rd, r_ref, tag + " residual")
         assert_scales(s, s_ref, tag + " scales")
         assert_codes(q, q_ref, tag + " codes")
 
