@@ -11,7 +11,8 @@ is already resident in HBM; three input sets are rotated so consecutive steps do
 Prints ONE JSON line:  value = algorithmic GB/s of the whole job (bytes = every input read once
 + every output written once, 7*T*H + 2*H + 4*T for config 3), plus `roofline` (the kernel's
 average launch duration from HIP events recorded around every launch inside the timed region)
-and `cpu_baseline` (the C oracle on a bounded row sample on this host's cores).
+and `cpu_baseline` (the C oracle on a bounded row sample on this host's cores), with
+`cpu_torch` beside it (the same operation in vectorized torch on the CPU).
 
   python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--workload cfg3]
 """
@@ -302,6 +303,56 @@ def cpu_baseline(wl: Workload, seconds: float) -> dict:
             "tokens_per_s": round(rows / med, 1)}
 
 
+def torch_cpu_add_norm_int8(x, r, w, eps: float):
+    """Add + RMSNorm + per-token int8 restated in vectorized torch (the form of the reference's
+    own torch-native test oracles), following the reference's rounding points
+    (op/vllm/quantization/fused_kernels/layernorm_utils.cuh:245-276, 436-447, 503-531 and
+    fused_layernorm_dynamic_per_token_quant.cu:37): residual b(x + r), rho on the unrounded sum,
+    y = b(b(a * rho) * w), s = max(A / 127, FLT_EPSILON), q = sat(rne(y * (1/s))).
+    Returns (q, s, residual)."""
+    import torch
+
+    bf, H = torch.bfloat16, x.shape[-1]
+    a = x.float() + r.float()
+    res = a.to(bf)
+    ss = (a.double() * a.double()).sum(-1, keepdim=True)
+    rho = 1.0 / torch.sqrt((ss / H).float() + eps)
+    y = ((a * rho).to(bf).float() * w.float()).to(bf).float()
+    s = torch.clamp(y.abs().amax(-1, keepdim=True) / 127.0, min=torch.finfo(torch.float32).eps)
+    q = torch.round(y * (1.0 / s)).clamp(-128, 127).to(torch.int8)
+    return q, s, res
+
+
+def cpu_torch(wl: Workload, seconds: float):
+    """torch_cpu_add_norm_int8 timed on this host (torch's intra-op threads) on a bounded row
+    sample, beside the C oracle.  Only the headline operation (kind add_norm_int8) has this leg;
+    None otherwise."""
+    if wl.kind != "add_norm_int8":
+        return None
+    import torch
+
+    rows = min(wl.T, 512)
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(rows, wl.H, generator=g).to(torch.bfloat16)
+    r = torch.randn(rows, wl.H, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(wl.H, generator=g)).to(torch.bfloat16)
+    torch_cpu_add_norm_int8(x, r, w, wl.eps)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        torch_cpu_add_norm_int8(x, r, w, wl.eps)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    sample_bytes = Workload(wl.name, rows, wl.H, wl.eps, wl.kind).bytes
+    threads = torch.get_num_threads()
+    return {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "sample": f"{rows} of {wl.T} rows x {wl.H}, median of {len(times)} runs over "
+                      f"~{seconds:.0f} s, vectorized torch on the CPU with {threads} intra-op "
+                      "threads (bench.py torch_cpu_add_norm_int8)",
+            "tokens_per_s": round(rows / med, 1)}
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -455,6 +506,7 @@ def main() -> int:
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+        out["cpu_torch"] = cpu_torch(wl, min(args.cpu_seconds, 10.0))
     print(json.dumps(out), flush=True)
     return 0
 
