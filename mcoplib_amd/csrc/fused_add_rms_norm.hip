@@ -9,8 +9,9 @@
 // from registers before the reduction, x after it (8*H bytes per bf16 row, plus the weight).
 // Rows too wide for the registers take k_fused_add_rms_norm_wide: one 1024-lane workgroup per
 // row, the row's first 8 vectors a lane held in registers and (bf16, fp32) the next 8 in LDS
-// (one read of rows up to 131072 bf16 elements), and beyond them two passes (sum of squares; then residual and output), the second
-// re-reading x and residual, which each lane then overwrites at the same addresses.
+// (one read of rows up to 131072 bf16 elements); beyond them two passes (sum of squares; then
+// residual and output), the second re-reading x and residual, which each lane then overwrites
+// at the same addresses.
 #include <hip/hip_runtime.h>
 
 #include "../../include/mcop_norm.h"
@@ -87,12 +88,11 @@ k_fused_add_rms_norm_wide(typename E::S* __restrict__ x, int64_t x_stride,
                           int hidden, float eps) {
   using S = typename E::S;
   // The row head (the lane's first NC vectors) stays in registers as the rounded sum z, and
-  // the next NL in LDS, so rows up to (NC + NL) * 1024 vectors are read once.  Head loads are unconditional (a lane past the
-  // row end re-reads the row's last vector and does not count it) and issued G vectors at a
-  // time; the residual of the head is written in the first pass, that of the re-read tail in
-  // the second, after its last read.
-  // NC (with NL below) is the largest head that compiles without spills at 1024 lanes (128
-  // VGPRs a lane)
+  // the next NL in LDS, so rows up to (NC + NL) * 1024 vectors are read once.  Head loads are
+  // unconditional (a lane past the row end re-reads the row's last vector and does not count
+  // it) and issued G vectors at a time; the residual of the head is written in the first pass,
+  // that of the re-read tail in the second, after its last read.  NC (with NL below) is the
+  // largest head that compiles without spills at 1024 lanes (128 VGPRs a lane).
   constexpr int NC = 8, G = 4;
   __shared__ double red_sum[16];
   const int nvec = hidden / VEC;
