@@ -12,9 +12,9 @@ from gpu_util import DEV, randn, weight, say
 pytestmark = pytest.mark.gpu
 
 
-def test_graph_replays_match_eager():
-    T, H = 64, 5120
-    say("graph capture: decode-shaped add + rmsnorm + int8, then fused_add_rms_norm")
+@pytest.mark.parametrize("T,H", [(64, 5120), (4, 131072)])  # register and multi-pass kernels
+def test_graph_replays_match_eager(T, H):
+    say(f"graph capture: add + rmsnorm + int8, then fused_add_rms_norm, T={T} H={H}")
     x = torch.empty(T, H, dtype=torch.bfloat16, device=DEV)
     r = torch.empty_like(x)
     w = weight(H, 1, torch.bfloat16).to(DEV)
