@@ -17,7 +17,8 @@ from gpu_util import DEV, assert_codes, assert_exact, assert_scales, gen, say
 
 pytestmark = pytest.mark.gpu
 
-OPS = ["h1", "h2", "h3", "h4", "h5", "ptq_int8", "ptq_azp", "ptq_fp8", "norm", "vllm_norm"]
+OPS = ["h1", "h2", "h3", "h4", "h5", "ptq_int8", "ptq_azp", "ptq_fp8", "norm", "vllm_norm",
+       "padded", "per_block"]
 DTYPES = [torch.bfloat16, torch.float16, torch.float32]
 
 
@@ -162,6 +163,44 @@ def test_random_shape(seed):
         assert_exact(out, out_ref, "out")
         if r is not None:
             assert_exact(ares, ares_ref, "after_res")
+    elif name == "padded":
+        x, r, w = (_x(T, H, seed, torch.bfloat16), _x(T, H, seed + 1, torch.bfloat16),
+                   _w(H, seed + 2, torch.bfloat16))
+        pad = (H + 4 + 63) // 64 * 32 + rng.choice([0, 0, 32])
+        p_ref, r_ref, rms_ref, q_ref, s_ref = oracle.add_rms_norm_quant_padded(x, r, w, pad, eps)
+        p = torch.zeros(T, 2 * pad, dtype=torch.int8, device=DEV)
+        rms = torch.empty(T, H, dtype=torch.bfloat16, device=DEV)
+        q = torch.empty(T, H, dtype=torch.int8, device=DEV)
+        s = torch.empty(T, 1, device=DEV)
+        rd = r.to(DEV)
+        op.fused_add_rms_norm_dynamic_per_token_quant_padding_output(p, rms, q, s, x.to(DEV), rd,
+                                                                      w.to(DEV), pad, eps)
+        torch.cuda.synchronize()
+        assert_exact(rd, r_ref, "residual")
+        assert_exact(rms, rms_ref, "output_rms")
+        assert_codes(q, q_ref, "codes")
+        assert_scales(s, s_ref, "scales")
+        assert torch.equal(p.cpu().view(torch.uint8), p_ref), "padded rows"
+    elif name == "per_block":
+        G = rng.choice([64, 128])
+        H = G * max(1, H // G)
+        qdt = rng.choice([torch.int8, torch.float8_e4m3fn])
+        transposed = rng.random() < 0.3
+        x, w = _x(T, H, seed, dtype), _w(H, seed + 2, dtype)
+        r = _x(T, H, seed + 1, dtype) if rng.random() < 0.5 else None
+        q_ref, s_ref, r_ref = oracle.rms_norm_per_block_quant(x, w, eps, qdt, G, None, r,
+                                                              transposed)
+        q = torch.empty(T, H, dtype=qdt, device=DEV)
+        s = (torch.empty(H // G, T, device=DEV) if transposed
+             else torch.empty(T, H // G, device=DEV))
+        rd = None if r is None else r.to(DEV)
+        torch.ops._C.rms_norm_per_block_quant(q, x.to(DEV), w.to(DEV), s, eps, None, rd, G,
+                                              transposed)
+        torch.cuda.synchronize()
+        assert_scales(s, s_ref, "scales")
+        assert_codes(q, q_ref, "codes")
+        if r is not None:
+            assert_exact(rd, r_ref, "residual")
     else:  # vllm_norm
         x, w = _x(T, H, seed, dtype), _w(H, seed + 2, dtype)
         ref = oracle.vllm_rms_norm(x, w, eps)
