@@ -60,11 +60,16 @@ def test_random_shape(seed):
     if name == "h1":
         x, r, w = _x(T, H, seed, dtype), _x(T, H, seed + 1, dtype), _w(H, seed + 2, dtype)
         x_ref, r_ref = oracle.fused_add_rms_norm(x, r, w, eps)
-        xd, rd = x.to(DEV), r.to(DEV)
+        pad = rng.choice([0, 0, 8, 3])  # x rows may be strided (input.stride(-2) > H)
+        big = torch.zeros(T, H + pad, dtype=dtype)
+        big[:, :H] = x
+        bigd, rd = big.to(DEV), r.to(DEV)
+        xd = bigd[:, :H]
         torch.ops._C.fused_add_rms_norm(xd, rd, w.to(DEV), eps)
         torch.cuda.synchronize()
         assert_exact(rd, r_ref, "residual")
-        assert_exact(xd, x_ref, "output")
+        assert_exact(xd.contiguous(), x_ref, "output")
+        assert not pad or bool((bigd[:, H:] == 0).all()), "row padding written"
     elif name == "h2":
         qdt = rng.choice([torch.int8, torch.float8_e4m3fn])
         with_res = rng.random() < 0.5
@@ -143,13 +148,17 @@ def test_random_shape(seed):
         x = _x(T, H, seed, dtype)
         ub = 0.05 if rng.random() < 0.3 else None
         q_ref, s_ref = oracle.dynamic_per_token_scaled_fp8_quant(x, ub)
-        q = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=DEV)
+        pin, pout = rng.choice([0, 0, 16, 5]), rng.choice([0, 0, 32, 7])  # strided rows
+        big = torch.zeros(T, H + pin, dtype=dtype)
+        big[:, :H] = x
+        qb = torch.zeros(T, H + pout, dtype=torch.float8_e4m3fn, device=DEV)
         s = torch.empty(T, 1, device=DEV)
         ubd = None if ub is None else torch.tensor([ub], device=DEV)
-        torch.ops._C.dynamic_per_token_scaled_fp8_quant(q, x.to(DEV), s, ubd)
+        torch.ops._C.dynamic_per_token_scaled_fp8_quant(qb[:, :H], big.to(DEV)[:, :H], s, ubd)
         torch.cuda.synchronize()
         assert_scales(s, s_ref, "scales")
-        assert_codes(q, q_ref, "codes")
+        assert_codes(qb[:, :H].contiguous(), q_ref, "codes")
+        assert not pout or bool((qb[:, H:].view(torch.uint8) == 0).all()), "row padding written"
     elif name == "norm":
         x, w = _x(T, H, seed, dtype), _w(H, seed + 2, rng.choice([dtype, torch.float32]))
         r = _x(T, H, seed + 1, dtype) if rng.random() < 0.5 else None
@@ -201,10 +210,15 @@ def test_random_shape(seed):
         assert_codes(q, q_ref, "codes")
         if r is not None:
             assert_exact(rd, r_ref, "residual")
-    else:  # vllm_norm
+    else:  # vllm_norm, on a 2-D or a 3-D input with strided rows
         x, w = _x(T, H, seed, dtype), _w(H, seed + 2, dtype)
         ref = oracle.vllm_rms_norm(x, w, eps)
         out = torch.empty(T, H, dtype=dtype, device=DEV)
-        torch.ops._C.rms_norm(out, x.to(DEV), w.to(DEV), eps)
+        if T % 2 == 0 and rng.random() < 0.5:
+            big = torch.zeros(2, T // 2, H + 16, dtype=dtype)
+            big[:, :, :H] = x.view(2, T // 2, H)
+            torch.ops._C.rms_norm(out.view(2, T // 2, H), big.to(DEV)[:, :, :H], w.to(DEV), eps)
+        else:
+            torch.ops._C.rms_norm(out, x.to(DEV), w.to(DEV), eps)
         torch.cuda.synchronize()
         assert_exact(out, ref, "out")
