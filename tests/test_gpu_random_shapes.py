@@ -88,8 +88,8 @@ def test_random_shape(seed):
         if r is not None:
             assert_exact(rd, r_ref, "residual")
     elif name == "h3":
-        x, w = _x(T, H, seed, torch.bfloat16), _w(H, seed + 2, torch.bfloat16)
-        r = _x(T, H, seed + 1, torch.bfloat16) if rng.random() < 0.7 else None
+        x, w = _x(T, H, seed, dtype), _w(H, seed + 2, dtype)
+        r = _x(T, H, seed + 1, dtype) if rng.random() < 0.7 else None
         q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant_custom(x, w, eps,
                                                                             residual=r)
         q = torch.empty(T, H, dtype=torch.int8, device=DEV)
