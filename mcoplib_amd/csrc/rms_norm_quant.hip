@@ -82,8 +82,13 @@ __device__ __forceinline__ Pack<uint8_t, VEC> row_codes(const float* y, float rh
   return q;
 }
 
+// With eight vectors a lane the int8 kernel asks for four waves per SIMD (at most 128 VGPRs,
+// which it meets without spilling): left free it took 140 VGPRs and three waves, one 512-lane
+// workgroup per CU, and rows of 20480-32768 bf16 elements ran 14-20% slower.  The fp8 forms
+// would spill under that bound and keep the default.
 template <class E, int VEC, int NV, bool FP8, bool RES, int MODE>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
+__attribute__((amdgpu_waves_per_eu(NV == 8 && !FP8 ? 4 : 1)))
 k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
                  const typename E::S* __restrict__ x, const typename E::S* __restrict__ w,
                  const float* __restrict__ scale_ub, typename E::S* __restrict__ res,
