@@ -11,7 +11,8 @@
  *     hold tensors on another device make it current first.
  *   - Return value: MCOP_OK (0) or a negative MCOP_E_* code. The message of the last failure on
  *     the calling thread is returned by mcop_last_error(). Nothing is allocated, no state is
- *     kept between calls (apart from the tuning override below), and calls are re-entrant.
+ *     kept between calls (apart from the calling thread's debug launch-shape override below),
+ *     and calls are re-entrant.
  *   - Floating-point inputs may be bf16, fp16 or fp32 (mcop_dtype). Quantized outputs are int8
  *     or OCP fp8-e4m3fn. Per-token scales are fp32, one per row.
  *   - Results do not depend on the launch configuration: the row sum of squares is accumulated
@@ -88,7 +89,7 @@ int mcop_rms_norm_dynamic_per_token_quant(void* out, mcop_dtype out_dtype, float
  *   u = (a~ / rho) * w   (or (a~ * rho) * w with MCOP_SQ_STANDARD_NORM); after_norm <- round(u)
  *   v = u * smooth;  A = max|v|
  *   int8: s = A/127, q = sat[-127,127](rne(v * (1/s)));  fp8: s = A/448,
- *   q = e4m3fn(clamp(v * (1/s), -448, 448));  A == 0 gives s = 0 and q = 0.
+ *   q = e4m3fn(clamp(v / s, -448, 448));  A == 0 gives s = 0 and q = 0.
  * `weight_dtype` and `smooth_dtype` are each `in_dtype` or MCOP_F32. after_res, after_norm and
  * residual may be NULL.
  * Replaces rms_norm_dynamic_per_token_quant(), op/fused_rms_norm_dq.cu:646-667
@@ -236,15 +237,15 @@ const char* mcop_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int mcop_abi_version(void);
-#define MCOP_ABI_VERSION 1
+#define MCOP_ABI_VERSION 2
 
-/* Launch-shape override for the row kernels (no reference counterpart; used by the tuning sweep
- * and by the tests that check results do not depend on the launch shape).
- * vectors_per_lane in {0,1,2,4,8,16}, lanes_per_row in {0, 16, 32} or a multiple of 64 up to
- * 1024;
- * 0 restores the automatic choice. A request the row does not fit falls back to automatic.
- * Process-wide; not meant to be changed while other threads launch. */
-int mcop_set_launch_override(int vectors_per_lane, int lanes_per_row);
+/* Debug hook, not part of the operator interface (no reference counterpart): forces the launch
+ * shape of the row kernels for later calls made BY THE CALLING THREAD only, for the tests that
+ * check results do not depend on the launch shape and for tuning sweeps. Other threads keep the
+ * automatic choice. vectors_per_lane in {0,1,2,4,8,16}, lanes_per_row in {0, 16, 32} or a
+ * multiple of 64 up to 1024; (0, 0) restores the automatic choice. A request the row does not
+ * fit falls back to automatic. Results do not change, only speed. */
+int mcop_debug_set_launch_override(int vectors_per_lane, int lanes_per_row);
 
 #ifdef __cplusplus
 }

@@ -14,7 +14,9 @@ from __future__ import annotations
 
 import argparse
 import concurrent.futures as cf
+import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -44,17 +46,81 @@ COMPILE_FLAGS = [
 ]
 
 
+# Kernels that ask for four waves per SIMD (amdgpu_waves_per_eu(4), i.e. at most 128 VGPRs): each
+# must meet that bound without spilling registers to scratch.  Patterns match demangled names.
+FOUR_WAVE_KERNELS = (
+    r"^void mcop::k_rms_norm_quant<mcop::BF16, 8, 8, false, (true|false), [0-9]>\(",
+    r"^void mcop::k_fused_add_rms_norm<mcop::BF16, 8, 8>\(",
+)
+RESOURCES = "resource_usage.json"
+
+
 def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def _compile(src: Path, build_dir: Path = BUILD, defines: tuple = ()) -> Path:
+def _remarks(text: str, tu: str) -> list[dict]:
+    """Per-kernel records of hipcc's -Rpass-analysis=kernel-resource-usage remarks."""
+    out, cur = [], None
+    for line in text.splitlines():
+        m = re.search(r"remark: (?:\s*)Function Name: (\S+)", line)
+        if m:
+            cur = {"tu": tu, "mangled": m.group(1)}
+            out.append(cur)
+            continue
+        m = re.search(r"remark:\s+([A-Za-z ]+?)(?: \[[^\]]*\])?: (\S+) \[-Rpass", line)
+        if m and cur is not None:
+            key = {"VGPRs": "vgprs", "AGPRs": "agprs", "ScratchSize": "scratch",
+                   "Occupancy": "occupancy", "LDS Size": "lds", "TotalSGPRs": "sgprs"}.get(
+                       m.group(1).strip())
+            if key:
+                cur[key] = int(m.group(2)) if m.group(2).isdigit() else m.group(2)
+    return out
+
+
+def _compile(src: Path, build_dir: Path = BUILD, defines: tuple = ()) -> tuple[Path, list]:
     obj = build_dir / (src.stem + ".o")
-    cmd = [HIPCC, *COMPILE_FLAGS, *[f"-D{d}" for d in defines], "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMPILE_FLAGS, "-Rpass-analysis=kernel-resource-usage",
+           *[f"-D{d}" for d in defines], "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")
-    return obj
+    return obj, _remarks(proc.stderr, src.name)
+
+
+def _demangle(records: list[dict]) -> None:
+    names = [r["mangled"] for r in records]
+    try:
+        proc = subprocess.run(["c++filt"], input="\n".join(names), capture_output=True,
+                              text=True, check=True)
+        dem = proc.stdout.split("\n")
+    except (OSError, subprocess.CalledProcessError):
+        dem = names
+    for r, d in zip(records, dem):
+        r["kernel"] = d
+
+
+def check_resources(records: list[dict]) -> list[str]:
+    """Problems with the compiled kernels' resources (empty = fine):
+    - a multi-pass kernel (k_*_wide) that spills (they are launched without a resource check);
+    - a kernel built with the four-waves request that spills or misses four waves per SIMD;
+    - no kernel matching one of those requests (a renamed kernel would escape the check).
+    Register-resident kernels may spill at 8 or 16 vectors per lane: the launch code skips
+    spilling kernels and sends such rows to the operator's multi-pass kernel."""
+    bad = []
+    for r in records:
+        k = r.get("kernel", r["mangled"])
+        if "_wide<" in k and r.get("scratch", 0) != 0:
+            bad.append(f"multi-pass kernel spills {r['scratch']} B/lane: {k}")
+    for pat in FOUR_WAVE_KERNELS:
+        hits = [r for r in records if re.search(pat, r.get("kernel", ""))]
+        if not hits:
+            bad.append(f"no kernel matches the four-waves pattern {pat}")
+        for r in hits:
+            if r.get("scratch", 0) != 0 or r.get("occupancy", 0) < 4:
+                bad.append(f"four-waves kernel spills {r.get('scratch')} B/lane or runs "
+                           f"{r.get('occupancy')} waves/SIMD: {r['kernel']}")
+    return bad
 
 
 def build(jobs: int | None = None, verbose: bool = True, out: Path = LIB,
@@ -68,7 +134,14 @@ def build(jobs: int | None = None, verbose: bool = True, out: Path = LIB,
     srcs = sources()
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, build_dir, defines), srcs))
+        done = list(ex.map(lambda s: _compile(s, build_dir, defines), srcs))
+    objs = [o for o, _ in done]
+    records = [r for _, rs in done for r in rs]
+    _demangle(records)
+    (build_dir / RESOURCES).write_text(json.dumps(records, indent=0))
+    problems = check_resources(records)
+    if problems:
+        raise RuntimeError("kernel resource check failed:\n  " + "\n  ".join(problems))
     tmp = out.with_suffix(".so.tmp")
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", f"-Wl,-soname,{LIB.name}", "-o",
            str(tmp), *map(str, objs)]

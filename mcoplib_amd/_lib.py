@@ -16,7 +16,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libmcop_norm.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # mcop_dtype codes (include/mcop_norm.h)
 BF16, F16, F32, I8, FP8_E4M3FN = 0, 1, 2, 3, 4
@@ -45,10 +45,10 @@ def _load() -> ctypes.CDLL:
     lib.mcop_vllm_rms_norm.argtypes = [P, P, P, I64, I64, I, I64, I64, I64, I64, I64, I, F, P]
     lib.mcop_rms_norm_dynamic_per_token_quant_custom.argtypes = [P, P, P, P, P, P, I64, I64, I,
                                                                   F, P]
-    lib.mcop_set_launch_override.argtypes = [I, I]
+    lib.mcop_debug_set_launch_override.argtypes = [I, I]
     for fn in ("mcop_fused_add_rms_norm", "mcop_rms_norm_dynamic_per_token_quant",
                "mcop_rms_norm_smooth_quant", "mcop_scale_dynamic_quant",
-               "mcop_fp8_e4m3fn_from_f32", "mcop_set_launch_override", "mcop_abi_version",
+               "mcop_fp8_e4m3fn_from_f32", "mcop_debug_set_launch_override", "mcop_abi_version",
                "mcop_dynamic_scaled_int8_quant", "mcop_dynamic_per_token_scaled_fp8_quant",
                "mcop_fused_add_rms_norm_dynamic_per_token_quant_padding_output",
                "mcop_rms_norm_per_block_quant", "mcop_rms_norm", "mcop_head_rms_norm",
@@ -87,5 +87,6 @@ def stream_of(t: torch.Tensor) -> int:
 
 
 def set_launch_override(vectors_per_lane: int = 0, lanes_per_row: int = 0) -> None:
-    """Force the row kernels' launch shape (0, 0 = automatic). Results do not change."""
-    check(lib.mcop_set_launch_override(int(vectors_per_lane), int(lanes_per_row)))
+    """Force the row kernels' launch shape for later calls from this thread (0, 0 = automatic;
+    a debug hook for tests and tuning). Results do not change."""
+    check(lib.mcop_debug_set_launch_override(int(vectors_per_lane), int(lanes_per_row)))

@@ -1,8 +1,7 @@
 // abi.hip -- host-side pieces shared by every entry point of libmcop_norm.so: error state,
-// launch geometry, the launch-shape override.
+// launch geometry, the (debug) launch-shape override.
 #include <hip/hip_runtime.h>
 
-#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -17,8 +16,9 @@ namespace mcop {
 
 namespace {
 thread_local char g_err[512] = "";
-std::atomic<int> g_over_nv{0};
-std::atomic<int> g_over_tpr{0};
+// launch-shape override of the calling thread (mcop_debug_set_launch_override)
+thread_local int g_over_nv = 0;
+thread_local int g_over_tpr = 0;
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t round64(int64_t a) { return ceil_div(a, 64) * 64; }
@@ -60,10 +60,36 @@ bool trace_enabled() {
   return on;
 }
 
-// Resident workgroups per CU of one kernel at one workgroup size (hipOccupancy..., cached; the
-// answer depends only on the kernel's registers / LDS and the architecture).
-// Kernels that spill registers to scratch (private segment > 0) count as 0: per-lane scratch
+// Attributes of one kernel (hipFuncGetAttributes, cached; the answer depends only on the code
+// object).  `spills`: the kernel keeps registers in private (scratch) memory, whose per-lane
 // traffic would compete with the streamed rows.
+struct KernelInfo {
+  bool ok;
+  bool spills;
+};
+KernelInfo kernel_info(const void* kernel) {
+  static std::mutex mu;
+  static std::unordered_map<const void*, KernelInfo> cache;
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(kernel);
+    if (it != cache.end()) return it->second;
+  }
+  KernelInfo k{false, false};
+  hipFuncAttributes attr;
+  if (hipFuncGetAttributes(&attr, kernel) != hipSuccess) {
+    (void)hipGetLastError();
+    return k;  // not cached: no device yet, or a transient failure
+  }
+  k.ok = true;
+  k.spills = attr.localSizeBytes > 0;
+  std::lock_guard<std::mutex> lk(mu);
+  cache[kernel] = k;
+  return k;
+}
+
+// Resident workgroups per CU of one kernel at one workgroup size (hipOccupancy..., cached).
+// Kernels that spill count as 0.
 int blocks_per_cu(const void* kernel, int block) {
   static std::mutex mu;
   static std::unordered_map<uint64_t, int> cache;
@@ -74,8 +100,8 @@ int blocks_per_cu(const void* kernel, int block) {
     if (it != cache.end()) return it->second;
   }
   int n = 0;
-  hipFuncAttributes attr;
-  if (hipFuncGetAttributes(&attr, kernel) != hipSuccess || attr.localSizeBytes > 0 ||
+  const KernelInfo k = kernel_info(kernel);
+  if (!k.ok || k.spills ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, block, 0) != hipSuccess) {
     (void)hipGetLastError();
     n = 0;
@@ -110,14 +136,15 @@ static bool valid_tpr(int64_t t, int min_tpr) {
   return (t >= min_tpr && (t == 16 || t == 32)) || (t > 0 && t % 64 == 0);
 }
 
-bool row_fits(int64_t hidden, int vec, int min_tpr) {
+bool row_fits(int64_t hidden, int vec, KernelOfNv kernels, int min_tpr) {
   static const int kVecNv[] = {1, 2, 4, 8, 16};
   static const int kScalarNv[] = {4, 16};
   const int64_t nvec = hidden / vec;
   const int* cands = vec > 1 ? kVecNv : kScalarNv;
   const int ncand = vec > 1 ? 5 : 2;
   for (int c = 0; c < ncand; ++c) {
-    if (row_lanes(ceil_div(nvec, cands[c]), min_tpr) <= max_tpr(vec, cands[c])) return true;
+    if (row_lanes(ceil_div(nvec, cands[c]), min_tpr) > max_tpr(vec, cands[c])) continue;
+    if (!kernel_info(kernels(cands[c])).spills) return true;
   }
   return false;
 }
@@ -141,8 +168,8 @@ bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, Kern
   const int64_t nvec = hidden / vec;
   int nv = 0;
   int64_t tpr = 0;
-  const int onv = g_over_nv.load(std::memory_order_relaxed);
-  const int otpr = g_over_tpr.load(std::memory_order_relaxed);
+  const int onv = g_over_nv;
+  const int otpr = g_over_tpr;
   const bool nv_allowed = vec > 1 ? (onv == 1 || onv == 2 || onv == 4 || onv == 8 || onv == 16)
                                   : (onv == 4 || onv == 16);
   if (nv_allowed) {
@@ -165,6 +192,7 @@ bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, Kern
       const int64_t t = row_lanes(ceil_div(nvec, cand), min_tpr);
       if (t > max_tpr(vec, cand)) continue;
       if (vec > 1 && cand == 1 && nvec > 64) continue;
+      if (kernel_info(kernels(cand)).spills) continue;
       if (fallback_nv == 0) {
         fallback_nv = cand;
         fallback_tpr = t;
@@ -231,14 +259,14 @@ const char* mcop_last_error(void) { return mcop::g_err; }
 
 int mcop_abi_version(void) { return MCOP_ABI_VERSION; }
 
-int mcop_set_launch_override(int vectors_per_lane, int lanes_per_row) {
+int mcop_debug_set_launch_override(int vectors_per_lane, int lanes_per_row) {
   if (vectors_per_lane < 0 || lanes_per_row < 0 || lanes_per_row > 1024 ||
       (lanes_per_row % 64 != 0 && lanes_per_row != 16 && lanes_per_row != 32)) {
-    return mcop::set_error(MCOP_E_INVALID, "mcop_set_launch_override: bad shape (%d, %d)",
+    return mcop::set_error(MCOP_E_INVALID, "mcop_debug_set_launch_override: bad shape (%d, %d)",
                            vectors_per_lane, lanes_per_row);
   }
-  mcop::g_over_nv.store(vectors_per_lane, std::memory_order_relaxed);
-  mcop::g_over_tpr.store(lanes_per_row, std::memory_order_relaxed);
+  mcop::g_over_nv = vectors_per_lane;
+  mcop::g_over_tpr = lanes_per_row;
   return MCOP_OK;
 }
 

@@ -279,7 +279,8 @@ static int dispatch(void* x, int64_t xs, void* res, const void* w, int64_t rows,
                     float eps, hipStream_t st) {
   constexpr int V = E::VEC;
   const bool vec_ok = hidden % V == 0 && xs % V == 0 && aligned(16, x, res, w);
-  if (!row_fits(hidden, vec_ok ? V : 1)) {
+  const KernelOfNv kernels = vec_ok ? &kernel_of<E, V> : &kernel_of<E, 1>;
+  if (!row_fits(hidden, vec_ok ? V : 1, kernels)) {
     if (!wide_rows_ok("fused_add_rms_norm", rows)) return MCOP_E_UNSUPPORTED;
     using S = typename E::S;
     auto* xp = static_cast<S*>(x);
@@ -295,8 +296,7 @@ static int dispatch(void* x, int64_t xs, void* res, const void* w, int64_t rows,
     return check_launch("fused_add_rms_norm");
   }
   Geometry g;
-  if (!choose_geometry("fused_add_rms_norm", rows, hidden, vec_ok ? V : 1, vec_ok ? &kernel_of<E, V> : &kernel_of<E, 1>,
-                       &g)) {
+  if (!choose_geometry("fused_add_rms_norm", rows, hidden, vec_ok ? V : 1, kernels, &g)) {
     return MCOP_E_UNSUPPORTED;
   }
   if (g.vec == 1) {

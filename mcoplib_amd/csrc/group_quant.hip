@@ -383,7 +383,10 @@ static int dispatch(const GqArgs& a, hipStream_t st) {
   const char* name = "rms_norm_per_block_quant";
   constexpr int V = E::VEC;
   const bool vec_ok = a.hidden % V == 0 && aligned(16, a.x, a.w, a.res) && aligned(V, a.out);
-  if (!row_fits(a.hidden, vec_ok ? V : 1, 64)) {
+  const KernelOfNv kernels =
+      vec_ok ? (a.res ? &kernel_of<E, V, FP8, true> : &kernel_of<E, V, FP8, false>)
+             : (a.res ? &kernel_of<E, 1, FP8, true> : &kernel_of<E, 1, FP8, false>);
+  if (!row_fits(a.hidden, vec_ok ? V : 1, kernels, 64)) {
     if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
     using S = typename E::S;
     auto* o = static_cast<uint8_t*>(a.out);
@@ -402,9 +405,6 @@ static int dispatch(const GqArgs& a, hipStream_t st) {
 #undef MCOP_WIDE
     return check_launch(name);
   }
-  const KernelOfNv kernels =
-      vec_ok ? (a.res ? &kernel_of<E, V, FP8, true> : &kernel_of<E, V, FP8, false>)
-             : (a.res ? &kernel_of<E, 1, FP8, true> : &kernel_of<E, 1, FP8, false>);
   Geometry g;
   // whole waves per row: a group's lanes must lie inside one row slice of the lane mapping
   if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? V : 1, kernels, &g, 64)) {

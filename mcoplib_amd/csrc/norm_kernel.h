@@ -369,7 +369,10 @@ static int norm_dispatch(const char* name, const NormArgs& a, hipStream_t st) {
   constexpr int V = E::VEC;
   const bool vec_ok = norm_vec_ok<E, EW>(a);
   const bool r = a.res != nullptr;
-  if (!row_fits(a.hidden, vec_ok ? V : 1)) {
+  const KernelOfNv kernels =
+      vec_ok ? (r ? &norm_kernel_of<E, EW, V, true> : &norm_kernel_of<E, EW, V, false>)
+             : (r ? &norm_kernel_of<E, EW, 1, true> : &norm_kernel_of<E, EW, 1, false>);
+  if (!row_fits(a.hidden, vec_ok ? V : 1, kernels)) {
     if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
     using S = typename E::S;
     auto* o = static_cast<S*>(a.out);
@@ -389,9 +392,6 @@ static int norm_dispatch(const char* name, const NormArgs& a, hipStream_t st) {
 #undef MCOP_WIDE
     return check_launch(name);
   }
-  const KernelOfNv kernels =
-      vec_ok ? (r ? &norm_kernel_of<E, EW, V, true> : &norm_kernel_of<E, EW, V, false>)
-             : (r ? &norm_kernel_of<E, EW, 1, true> : &norm_kernel_of<E, EW, 1, false>);
   Geometry g;
   if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? V : 1, kernels, &g)) {
     return MCOP_E_UNSUPPORTED;

@@ -286,7 +286,7 @@ static int dispatch(const PadArgs& a, hipStream_t st) {
   const bool vec_ok = a.hidden % 8 == 0 && a.pad_bytes % 8 == 0 &&
                       aligned(16, a.x, a.res, a.w, a.rms) && aligned(8, a.q, a.padded);
   if constexpr (!OPT) {
-    if (!row_fits(a.hidden, vec_ok ? 8 : 1)) {
+    if (!row_fits(a.hidden, vec_ok ? 8 : 1, vec_ok ? &kernel_of<8, OPT> : &kernel_of<1, OPT>)) {
       if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
       const dim3 grid((unsigned)a.rows), block(kWideLanes);
       if (vec_ok) {

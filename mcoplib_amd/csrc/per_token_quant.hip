@@ -279,7 +279,8 @@ static int dispatch(const char* name, const PtqArgs& a, hipStream_t st) {
   constexpr int V = E::VEC;
   const bool vec_ok = a.hidden % V == 0 && a.in_stride % V == 0 && a.out_stride % V == 0 &&
                       aligned(16, a.x) && aligned(V, a.out);
-  if (!row_fits(a.hidden, vec_ok ? V : 1)) {
+  const KernelOfNv kernels = vec_ok ? &kernel_of<E, V, MODE> : &kernel_of<E, 1, MODE>;
+  if (!row_fits(a.hidden, vec_ok ? V : 1, kernels)) {
     if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
     using S = typename E::S;
     auto* o = static_cast<uint8_t*>(a.out);
@@ -295,8 +296,7 @@ static int dispatch(const char* name, const PtqArgs& a, hipStream_t st) {
     return check_launch(name);
   }
   Geometry g;
-  if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? V : 1,
-                       vec_ok ? &kernel_of<E, V, MODE> : &kernel_of<E, 1, MODE>, &g)) {
+  if (!choose_geometry(name, a.rows, a.hidden, vec_ok ? V : 1, kernels, &g)) {
     return MCOP_E_UNSUPPORTED;
   }
   if (g.vec == 1) launch_nv<E, 1, MODE>(g, a, st);

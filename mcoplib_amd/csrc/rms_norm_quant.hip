@@ -82,13 +82,14 @@ __device__ __forceinline__ Pack<uint8_t, VEC> row_codes(const float* y, float rh
   return q;
 }
 
-// With eight vectors a lane the int8 kernel asks for four waves per SIMD (at most 128 VGPRs,
-// which it meets without spilling): left free it took 140 VGPRs and three waves, one 512-lane
-// workgroup per CU, and rows of 20480-32768 bf16 elements ran 14-20% slower.  The fp8 forms
-// would spill under that bound and keep the default.
+// With eight vectors a lane the bf16 int8 kernel asks for four waves per SIMD (at most 128
+// VGPRs, which it meets without spilling): left free it took 140 VGPRs and three waves, one
+// 512-lane workgroup per CU, and rows of 20480-32768 bf16 elements ran 14-20% slower.  The fp8
+// forms, and fp16 (whose conversions need more registers), would spill under that bound and keep
+// the default.
 template <class E, int VEC, int NV, bool FP8, bool RES, int MODE>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
-__attribute__((amdgpu_waves_per_eu(NV == 8 && !FP8 ? 4 : 1)))
+__attribute__((amdgpu_waves_per_eu(NV == 8 && !FP8 && std::is_same<E, BF16>::value ? 4 : 1)))
 k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
                  const typename E::S* __restrict__ x, const typename E::S* __restrict__ w,
                  const float* __restrict__ scale_ub, typename E::S* __restrict__ res,
@@ -203,7 +204,7 @@ k_rms_norm_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
                       int hidden, float eps) {
   static_assert(MODE != QM_MC_7168, "7168-wide rows fit the register-resident kernel");
   using S = typename E::S;
-  constexpr int NC = VEC > 1 ? (RES ? 5 : 8) : 16;
+  constexpr int NC = VEC > 1 ? (RES ? 5 : (FP8 && std::is_same<E, F16>::value ? 7 : 8)) : 16;
   __shared__ double red_sum[16];
   __shared__ float red_max[16];
   const int nvec = hidden / VEC;
@@ -390,8 +391,11 @@ static int dispatch(const char* name, void* out, float* scales, const void* x, c
                     hipStream_t st) {
   constexpr int V = E::VEC;
   const bool vec_ok = hidden % V == 0 && aligned(16, x, w, res) && aligned(V, out);
+  const KernelOfNv kernels =
+      vec_ok ? (res ? &kernel_of<E, V, FP8, true, MODE> : &kernel_of<E, V, FP8, false, MODE>)
+             : (res ? &kernel_of<E, 1, FP8, true, MODE> : &kernel_of<E, 1, FP8, false, MODE>);
   if constexpr (MODE != QM_MC_7168) {
-    if (!row_fits(hidden, vec_ok ? V : 1)) {
+    if (!row_fits(hidden, vec_ok ? V : 1, kernels)) {
       if (!wide_rows_ok(name, rows)) return MCOP_E_UNSUPPORTED;
       using S = typename E::S;
       auto* o = static_cast<uint8_t*>(out);
@@ -411,9 +415,6 @@ static int dispatch(const char* name, void* out, float* scales, const void* x, c
       return check_launch(name);
     }
   }
-  const KernelOfNv kernels =
-      vec_ok ? (res ? &kernel_of<E, V, FP8, true, MODE> : &kernel_of<E, V, FP8, false, MODE>)
-             : (res ? &kernel_of<E, 1, FP8, true, MODE> : &kernel_of<E, 1, FP8, false, MODE>);
   Geometry g;
   if (!choose_geometry(name, rows, hidden, vec_ok ? V : 1, kernels, &g, 16,
                        /*wide_nv4=*/false)) {

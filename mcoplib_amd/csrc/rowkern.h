@@ -396,9 +396,10 @@ using KernelOfNv = const void* (*)(int nv);
 bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, KernelOfNv kernels,
                      Geometry* g, int min_tpr = 16, bool wide_nv4 = true);
 
-// True when a row of `hidden` elements fits the register-resident kernels at vector width `vec`
-// (some vectors-per-lane candidate holds it within its lanes-per-row limit).
-bool row_fits(int64_t hidden, int vec, int min_tpr = 16);
+// True when a row of `hidden` elements fits the register-resident kernels at vector width `vec`:
+// some vectors-per-lane candidate holds it within its lanes-per-row limit, and that candidate's
+// kernel compiled without spilling registers.  Other rows take the operator's multi-pass kernel.
+bool row_fits(int64_t hidden, int vec, KernelOfNv kernels, int min_tpr = 16);
 
 // Launch check of the multi-pass kernels for rows too wide for the register-resident ones
 // (one 1024-lane workgroup per row): false, with the message set, beyond 2^31 - 1 rows.

@@ -230,7 +230,8 @@ extern "C" int mcop_scale_dynamic_quant(int8_t* out, float* scales, const void* 
   constexpr int V = BF16::VEC;
   const bool vec_ok = hidden_size % V == 0 && aligned(16, input, smooth) && aligned(V, out);
   auto st = static_cast<hipStream_t>(stream);
-  if (!row_fits(hidden_size, vec_ok ? V : 1)) {
+  const KernelOfNv kernels = vec_ok ? &kernel_of<V> : &kernel_of<1>;
+  if (!row_fits(hidden_size, vec_ok ? V : 1, kernels)) {
     if (!wide_rows_ok("scale_dynamic_quant", num_tokens)) return MCOP_E_UNSUPPORTED;
     auto* o = reinterpret_cast<uint8_t*>(out);
     auto* xp = static_cast<const uint16_t*>(input);
@@ -244,8 +245,8 @@ extern "C" int mcop_scale_dynamic_quant(int8_t* out, float* scales, const void* 
     return check_launch("scale_dynamic_quant");
   }
   Geometry g;
-  if (!choose_geometry("scale_dynamic_quant", num_tokens, hidden_size, vec_ok ? V : 1,
-                       vec_ok ? &kernel_of<V> : &kernel_of<1>, &g)) {
+  if (!choose_geometry("scale_dynamic_quant", num_tokens, hidden_size, vec_ok ? V : 1, kernels,
+                       &g)) {
     return MCOP_E_UNSUPPORTED;
   }
   if (g.vec == 1) {

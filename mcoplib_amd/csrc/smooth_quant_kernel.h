@@ -11,7 +11,8 @@
 //   u = (b(a) / rho) * w     [literal form; (b(a) * rho) * w with MCOP_SQ_STANDARD_NORM]
 //   after_norm <- b(u);  v = u * smooth                              norm_and_quant :163-186
 //   A = max|v|;  int8: s = A/127, q = sat[-127,127](rne(v * (1/s)))  :125-161, :296-297
-//   fp8 (no reference; same inverted-scale form): s = A/448, q = e4m3fn(clamp(v * (1/s), +-448))
+//   fp8 (the operator's entry accepts int8 only; its kernel's fp8 branch, :299-301, divides):
+//        s = A/448, q = e4m3fn(clamp(v / s, +-448))
 //   A == 0: s = 0 and q = 0.
 // One pass: the row stays in VGPRs between the two reductions, so HBM sees x (and residual)
 // read once and after_res, after_norm, the codes and the scale written once.  The division by
@@ -32,6 +33,19 @@ struct WVec {
   Pack<typename EW::S, VEC> p;
   __device__ __forceinline__ float at(int e) const { return EW::to_f(p.v[e]); }
 };
+
+// fp8 codes of one vector of v: e4m3fn(clamp(v / s, +-448)), the correctly rounded quotient
+// (fp8_quotient_codes; `bounded`: 2^-18 <= s <= 2^100, where the short form is exact); a row
+// whose absmax is 0 has s = 0 and codes 0.
+template <int VEC>
+__device__ __forceinline__ Pack<uint8_t, VEC> sq_fp8_codes(const float* v, float amax, float s,
+                                                           float inv, bool s_ok, bool bounded) {
+  if (amax > 0.0f) return fp8_quotient_codes<VEC>(v, s, inv, s_ok, bounded);
+  Pack<uint8_t, VEC> z;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) z.v[e] = 0;
+  return z;
+}
 
 // One row (or, for tpr < blockDim, one of the workgroup's rows) given the lane's weight and
 // smooth vectors.
@@ -112,6 +126,8 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const WVec<EW, VEC>* wv,
   const float s = mcop_div_rn(amax, FP8 ? 448.0f : 127.0f);
   if (p.live && p.lt == 0) scales[p.row] = s;
   const float inv = amax > 0.0f ? mcop_div_rn(1.0f, s) : 0.0f;
+  const bool s_ok = mcop_divisor_ok(s);
+  const bool bounded = s >= 0x1p-18f && s <= 0x1p100f;
 
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
@@ -119,10 +135,7 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const WVec<EW, VEC>* wv,
     if (p.live && j < nvec) {
       Pack<uint8_t, VEC> q;
       if constexpr (FP8) {
-        float c[VEC];
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) c[e] = clamp_fp8(a[v][e] * inv);
-        q = cvt_fp8<VEC>(c);
+        q = sq_fp8_codes<VEC>(a[v], amax, s, inv, s_ok, bounded);
       } else {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-127>(a[v][e] * inv);
@@ -175,8 +188,9 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
   // The row head (the lane's first NC vectors of x, and of the residual) is loaded once and
   // kept in registers across the three passes, the next NL in LDS; the passes re-read only the
   // rest of the row.
-  // NC is the largest head that compiles without spills at 1024 lanes (128 VGPRs a lane).
-  constexpr int NC = VEC > 1 ? (RES ? 4 : sizeof(typename EW::S) == 4 ? 5 : 6) : 16;
+  // NC is the largest head that compiles without spills at 1024 lanes (128 VGPRs a lane); the
+  // fp8 quotient's correction steps take one vector's worth of registers.
+  constexpr int NC = VEC > 1 ? (RES ? 4 : (sizeof(typename EW::S) == 4 || FP8) ? 5 : 6) : 16;
   __shared__ double red_sum[16];
   __shared__ float red_max[16];
   const int nvec = hidden / VEC;
@@ -297,6 +311,8 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
   const float s = mcop_div_rn(amax, FP8 ? 448.0f : 127.0f);
   if (threadIdx.x == 0) scales[blockIdx.x] = s;
   const float inv = amax > 0.0f ? mcop_div_rn(1.0f, s) : 0.0f;
+  const bool s_ok = mcop_divisor_ok(s);
+  const bool bounded = s >= 0x1p-18f && s <= 0x1p100f;
   auto emit = [&](int64_t o, const float* t) {
     float u[VEC], v[VEC];
     uv_of(o, t, u, v);
@@ -310,10 +326,7 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
     if (anorm != nullptr) st<S, VEC>(anorm + base + o, an);
     Pack<uint8_t, VEC> q;
     if constexpr (FP8) {
-      float c[VEC];
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) c[e] = clamp_fp8(v[e] * inv);
-      q = cvt_fp8<VEC>(c);
+      q = sq_fp8_codes<VEC>(v, amax, s, inv, s_ok, bounded);
     } else {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-127>(v[e] * inv);
@@ -404,7 +417,10 @@ static int dispatch(const Args& a, hipStream_t st) {
   const bool vec_ok = a.hidden % V == 0 && aligned(16, a.x, a.ares, a.anorm, a.res) &&
                       aligned(WB, a.w) && aligned(SB, a.sm) && aligned(V, a.out);
   const bool r = a.res != nullptr;
-  if (!row_fits(a.hidden, vec_ok ? V : 1)) {
+  const KernelOfNv kernels =
+      vec_ok ? (r ? &kernel_of<E, EW, ES, V, FP8, true> : &kernel_of<E, EW, ES, V, FP8, false>)
+             : (r ? &kernel_of<E, EW, ES, 1, FP8, true> : &kernel_of<E, EW, ES, 1, FP8, false>);
+  if (!row_fits(a.hidden, vec_ok ? V : 1, kernels)) {
     const char* name = "rms_norm_dynamic_per_token_quant (smooth)";
     if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
     using S = typename E::S;
@@ -427,9 +443,6 @@ static int dispatch(const Args& a, hipStream_t st) {
 #undef MCOP_WIDE
     return check_launch(name);
   }
-  const KernelOfNv kernels =
-      vec_ok ? (r ? &kernel_of<E, EW, ES, V, FP8, true> : &kernel_of<E, EW, ES, V, FP8, false>)
-             : (r ? &kernel_of<E, EW, ES, 1, FP8, true> : &kernel_of<E, EW, ES, 1, FP8, false>);
   Geometry g;
   if (!choose_geometry("rms_norm_dynamic_per_token_quant (smooth)", a.rows, a.hidden,
                        vec_ok ? V : 1, kernels, &g)) {

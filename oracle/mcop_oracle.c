@@ -336,8 +336,9 @@ void oracle_rms_norm_quant_custom(int8_t* out, float* scales, const void* x, con
      after_norm <- b(u); v = u * sm; A = max|v|;
      int8: s = A / 127.0 (:154; binary64 quotient rounded to binary32 == the binary32 quotient),
            q = sat[-127,127](rne(v * (1/s))) (kernel/utils.h:219-226);
-     fp8 (no reference; the same inverted-scale form): s = A/448, q = e4m3fn(clamp(v*(1/s))).
-     A == 0: s = 0 and q = 0 (the reference computes 0 * inf).
+     fp8 (the entry accepts int8 only, :658; the kernel's fp8 branch, :299-301, passes the scale
+          uninverted to ScaledQuant, which divides): s = A/448, q = e4m3fn(clamp(v / s)).
+     A == 0: s = 0 and q = 0 (the reference computes 0 * inf, or 0 / 0 for fp8).
    w and sm are each stored as w_dt / sm_dt (the input dtype or fp32). */
 void oracle_rms_norm_smooth_quant(void* out, int out_dt, float* scales, const void* x,
                                   const void* w, int w_dt, const void* sm, int sm_dt,
@@ -370,7 +371,7 @@ void oracle_rms_norm_smooth_quant(void* out, int out_dt, float* scales, const vo
       scales[t] = s;
       for (int64_t i = 0; i < H; ++i) {
         if (out_dt == DT_I8) ((int8_t*)out)[t * H + i] = q_int8(a[i] * inv, -127);
-        else ((uint8_t*)out)[t * H + i] = q_fp8(a[i] * inv);
+        else ((uint8_t*)out)[t * H + i] = amax > 0.0f ? q_fp8(a[i] / s) : 0;
       }
     }
     free(a);

@@ -30,7 +30,7 @@ def test_every_declared_symbol_is_exported():
 
 
 def test_abi_version_and_error_channel():
-    assert _lib.lib.mcop_abi_version() == 1
+    assert _lib.lib.mcop_abi_version() == 2
     assert mcoplib_amd.LIBRARY_PATH.endswith("libmcop_norm.so")
 
 
@@ -73,8 +73,8 @@ def test_c_abi_rejects_bad_arguments_without_a_device():
                                         0, None) == -1
     assert "fp32 input" in _err()
     # launch override validation
-    assert L.mcop_set_launch_override(2, 100) == -1
-    assert L.mcop_set_launch_override(0, 0) == 0
+    assert L.mcop_debug_set_launch_override(2, 100) == -1
+    assert L.mcop_debug_set_launch_override(0, 0) == 0
 
 
 def test_c_abi_rejects_shapes_beyond_the_kernels_without_a_device():

@@ -16,8 +16,10 @@ import torch
 
 import oracle
 
-import mcoplib_amd._C  # noqa: F401
-from mcoplib_amd import custom_ops, op
+# the reference's own import lines (README.md:149,155; unit_test/test_rms_norm_custom.py:2)
+from mcoplib import op as ops
+import mcoplib._C  # noqa: F401
+from mcoplib.custom_ops import rms_norm_dynamic_per_token_quant
 from gpu_util import DEV, say
 
 pytestmark = pytest.mark.gpu
@@ -41,7 +43,7 @@ def test_scale_dynamic_quant_reference_suite():
     torch.manual_seed(13)
     h = torch.randn(2, 128, 768, device=DEV, dtype=torch.bfloat16)
     sm = torch.ones(768, device=DEV, dtype=torch.float32)
-    q, s = op.scale_dynamic_quant(h, sm, torch.int8)
+    q, s = ops.scale_dynamic_quant(h, sm, torch.int8)
     assert q.shape == (2, 128, 768) and s.shape == (2 * 128,)
     qr, sr = _loop_oracle(h, sm)
     assert torch.allclose(q.cpu(), qr.cpu(), rtol=0, atol=1)
@@ -50,25 +52,25 @@ def test_scale_dynamic_quant_reference_suite():
     h = torch.tensor([[[1.0, 2.0, 3.0, 4.0], [4.0, 3.0, 2.0, 1.0]]], device=DEV,
                      dtype=torch.bfloat16)
     sm = torch.tensor([1.0, 1.0, 2.0, 2.0], device=DEV, dtype=torch.float32)
-    q, s = op.scale_dynamic_quant(h, sm, torch.int8)
+    q, s = ops.scale_dynamic_quant(h, sm, torch.int8)
     assert abs(s[0].item() - 8.0 / 127) < 1e-5
     assert abs(s[1].item() - 4.0 / 127) < 1e-5
 
-    q, s = op.scale_dynamic_quant(torch.zeros(1, 4, 8, device=DEV, dtype=torch.bfloat16),
+    q, s = ops.scale_dynamic_quant(torch.zeros(1, 4, 8, device=DEV, dtype=torch.bfloat16),
                                   torch.ones(8, device=DEV), torch.int8)
     assert torch.all(q == 0)
-    q, s = op.scale_dynamic_quant(torch.ones(1, 4, 8, device=DEV, dtype=torch.bfloat16) * 1000.0,
+    q, s = ops.scale_dynamic_quant(torch.ones(1, 4, 8, device=DEV, dtype=torch.bfloat16) * 1000.0,
                                   torch.ones(8, device=DEV), torch.int8)
     assert torch.all(torch.abs(q) <= 127)
     for shape in [(1, 1, 768), (4, 512, 768), (1, 2048, 4096), (8, 128, 1024)]:
         h = torch.randn(*shape, device=DEV, dtype=torch.bfloat16)
-        q, s = op.scale_dynamic_quant(h, torch.ones(shape[-1], device=DEV), torch.int8)
+        q, s = ops.scale_dynamic_quant(h, torch.ones(shape[-1], device=DEV), torch.int8)
         assert q.shape == shape and s.shape == (shape[0] * shape[1],)
     h = torch.randn(2, 64, 256, device=DEV, dtype=torch.bfloat16) * 1e-7
-    q, s = op.scale_dynamic_quant(h, torch.ones(256, device=DEV), torch.int8)
+    q, s = ops.scale_dynamic_quant(h, torch.ones(256, device=DEV), torch.int8)
     assert torch.all(torch.isfinite(s)) and torch.all(s > 0)
     with pytest.raises(RuntimeError, match="Only support bfloat16"):
-        op.scale_dynamic_quant(h.float(), torch.ones(256, device=DEV), torch.int8)
+        ops.scale_dynamic_quant(h.float(), torch.ones(256, device=DEV), torch.int8)
 
 
 # ------------------------------------------------------------ test_fused_rms_norm_dq.py
@@ -142,7 +144,7 @@ def test_rms_norm_custom_7168():
     res = torch.randn(tokens, hidden, dtype=torch.bfloat16, device=DEV)
     w = torch.randn(hidden, dtype=torch.bfloat16, device=DEV)
     res_in = res.clone()
-    q, s = custom_ops.rms_norm_dynamic_per_token_quant(x, w, 1e-6, torch.int8, None, res)
+    q, s = rms_norm_dynamic_per_token_quant(x, w, 1e-6, torch.int8, None, res)
     ref_res = (x.float() + res_in.float()).to(torch.bfloat16)
     assert torch.equal(res, ref_res)
     y = torch.rms_norm(ref_res.float(), (hidden,), None, 1e-6).to(torch.bfloat16) * w
@@ -172,7 +174,7 @@ def test_rms_div_convention(m, n):
     scales = torch.empty(m, dtype=torch.float32, device=DEV)
     after_res = torch.empty_like(x)
     after_norm = torch.empty_like(x)
-    op.rms_norm_dynamic_per_token_quant(out, x, w, torch.ones(n, device=DEV), scales, 1e-5,
+    ops.rms_norm_dynamic_per_token_quant(out, x, w, torch.ones(n, device=DEV), scales, 1e-5,
                                         after_res, after_norm, r)
     torch.testing.assert_close(norm_ref, after_norm, atol=1e-5, rtol=1e-5)
     torch.testing.assert_close(after_res_ref.reshape(-1), after_res.reshape(-1), atol=1e-5,

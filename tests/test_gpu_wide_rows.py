@@ -267,3 +267,48 @@ def test_wide_head_rms_norm():
     op.head_rms_norm(out, hs.to(DEV), w.to(DEV), 1e-6, 1, 2)
     torch.cuda.synchronize()
     assert_exact(out, ref, "head_rms_norm")
+
+
+# Widths whose only fitting register-resident kernel spills registers (eight or sixteen vectors
+# a lane; the build's resource remarks list them): the launch code sends these rows to the
+# multi-pass kernel as well.  fp16 SmoothQuant with fp32 weight and smooth needs eight vectors a
+# lane from 16392 on; bf16 H2 fp8 sixteen from 32776 on; the fp16 padded op and the fp16 norm
+# with fp32 weights sixteen from 32776 on.
+@pytest.mark.parametrize("H", [20480, 32768])
+def test_spilling_widths_h4_fp16_fp32_weights(H):
+    say(f"spilling-width H4 fp16 x, fp32 w/smooth, H={H}")
+    x, w = _x(3, H, 30, torch.float16), _w(H, 31, torch.float32)
+    sm = 0.5 + 1.5 * torch.rand(H, generator=gen(32))
+    for qdt in (torch.int8, torch.float8_e4m3fn):
+        q_ref, s_ref, ar_ref, an_ref = oracle.rms_norm_smooth_quant(x, w, sm, 1e-6, qdt)
+        q = torch.empty(x.shape, dtype=qdt, device=DEV)
+        s = torch.empty(3, device=DEV)
+        ar = torch.empty(x.shape, dtype=torch.float16, device=DEV)
+        an = torch.empty_like(ar)
+        op.rms_norm_dynamic_per_token_quant(q, x.to(DEV), w.to(DEV), sm.to(DEV), s, 1e-6, ar, an,
+                                            None)
+        torch.cuda.synchronize()
+        assert_exact(ar, ar_ref, f"{qdt} after_res")
+        assert_exact(an, an_ref, f"{qdt} after_norm")
+        assert_scales(s, s_ref, f"{qdt} scales")
+        assert_codes(q, q_ref, f"{qdt} codes")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_spilling_widths_h2_fp8(dtype):
+    H = 49152
+    say(f"spilling-width H2 {dtype} fp8 H={H}")
+    x, r, w = _x(3, H, 33, dtype), _x(3, H, 34, dtype), _w(H, 35, dtype)
+    for res in (None, r):
+        q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant(x, w, 1e-6,
+                                                                      torch.float8_e4m3fn,
+                                                                      None, res)
+        q = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=DEV)
+        s = torch.empty(3, 1, device=DEV)
+        rd = None if res is None else res.to(DEV)
+        torch.ops._C.rms_norm_dynamic_per_token_quant(q, x.to(DEV), w.to(DEV), s, 1e-6, None, rd)
+        torch.cuda.synchronize()
+        assert_scales(s, s_ref, "scales")
+        assert_codes(q, q_ref, "codes")
+        if res is not None:
+            assert_exact(rd, r_ref, "residual")
