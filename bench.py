@@ -1,20 +1,31 @@
 #!/usr/bin/env python3
-"""Benchmark of the fused add + RMSNorm + per-token int8 quantization path on one MI355X.
+"""Benchmark of the fused add + RMSNorm + per-token quantization path on one MI355X.
 
-Default workload ("cfg3", the headline configuration): x and residual bf16 [8192, 8192] (1% of channels scaled x20
-as outliers), weight bf16 ~N(1, 0.1), eps 1e-5; output int8 [8192, 8192] + fp32 scales [8192, 1]
-+ the bf16 residual written in place.  One step = one call of
-mcoplib_amd.custom_ops.rms_norm_dynamic_per_token_quant (one kernel launch) over one batch that
-is already resident in HBM; three input sets are rotated so consecutive steps do not hit the
-256 MB last-level cache.
+Headline workload ("cfg3"): x and residual bf16 [8192, 8192] (1% of channels scaled x20 as
+outliers), weight bf16 ~N(1, 0.1), eps 1e-5; output int8 [8192, 8192] + fp32 scales [8192, 1] +
+the bf16 residual written in place.  One step = one call of
+mcoplib.op.rms_norm_dynamic_per_token_quant_custom (one kernel launch) over one batch already
+resident in HBM; copies of the input are rotated so consecutive steps do not hit the 256 MB
+last-level cache.
 
-Prints ONE JSON line:  value = algorithmic GB/s of the whole job (bytes = every input read once
-+ every output written once, 7*T*H + 2*H + 4*T for config 3), plus `roofline` (the kernel's
-average launch duration from HIP events recorded around every launch inside the timed region)
-and `cpu_baseline` (the C oracle on a bounded row sample on this host's cores), with
-`cpu_torch` beside it (the same operation in vectorized torch on the CPU).
+The default run prints ONE JSON line: the headline (value = algorithmic GB/s, bytes = every
+input read once + every output written once) with
+  - roofline: the kernel's average launch time from HIP events around the timed launches, next
+    to the rocprofv3 kernel-trace mean and the HBM traffic of the committed profile summary;
+  - guard: whether the headline stays at >= 75% of peak with traffic <= 1.01x the algorithmic
+    bytes (`regressed` true when not);
+  - device_copy / ceilings: a non-temporal streaming copy, read-only and write-only kernels, and
+    compute-free kernels with each timed operator's exact access pattern (libmcop_pattern.so);
+  - cpu_baseline / cpu_torch: the C oracle and a vectorized torch restatement on a row sample of
+    the same inputs, on this host's cores, with a bit-for-bit check of the GPU's first call;
+  - configs: the other configurations -- cfg1 (CPU only), cfg2, cfg4, cfg5 large (GB/s, fraction
+    of peak, traffic, pattern ceiling, CPU baseline, parity of the sampled rows) and cfg5 decode
+    (us per call, eager and replayed from a HIP graph).
+Every configuration's inputs are generated on the CPU from torch.Generator().manual_seed(k) for
+configuration k and copied to the GPU, so the GPU, the oracle and the torch legs see the same bits
+(and the parity tests build the same inputs: tests import `config_inputs`).
 
-  python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--workload cfg3]
+  python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--workload cfg3] [--no-configs] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -31,9 +42,11 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 HBM_PEAK_GBS = 8000.0
 METRIC = "HBM GB/s & % of peak: fused add-RMSNorm+per-token int8 quant, 8192x8192"
+FRAC_GUARD, TRAFFIC_GUARD = 0.75, 1.01
 PAD_SIZE = 3840  # padded workload: bf16 elements per padded row (2 * 3840 bytes)
 BLOCK_GROUP = 128  # block-fp8 workload: elements per scale group
 HEADS = 8  # head-norm workload: heads per token (all normalized, per-head weights)
+DECODE_T = (1, 4, 16, 64)
 
 
 def parse():
@@ -41,22 +54,50 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="cfg3",
-                    choices=["cfg2", "cfg3", "cfg4", "cfg5-large", "cfg5-decode1",
-                             "cfg5-decode4", "cfg5-decode16", "cfg5-decode64", "ptq-int8",
-                             "ptq-int8-azp", "ptq-fp8", "padded", "block-fp8", "norm-res",
-                             "vllm-norm", "head-norm", "sdq", "wide-int8", "wide-fused",
-                             "wide-fp8", "wide-sdq", "wide-norm", "wide-ptq", "wide-padded",
-                             "wide-block"])
+    ap.add_argument("--workload", default="cfg3", choices=sorted(WORKLOADS))
     ap.add_argument("--sets", type=int, default=0,
-                    help="rotated input sets (default: enough for > 1 GiB, at least 3)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+                    help="rotated input copies (default: enough for > 1 GiB, at least 3)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU legs")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="time the chosen workload only (no other configs, ceilings or copy)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="CPU time of the headline's CPU legs (the other configs take a third)")
     ap.add_argument("--warmup-seconds", type=float, default=2.0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run three 1 GiB device-to-device copies (a kernel of known "
                          "traffic, used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     return ap.parse_args()
+
+
+# ------------------------------------------------------------------------------ inputs
+def config_inputs(name: str) -> dict:
+    """Seeded CPU inputs of a configuration (bf16 unless stated; torch.Generator seeded with the
+    configuration number, draws in the order listed):
+      cfg1        x [256, 4096] ~N(0,1); w [4096] ~N(1, 0.1); no residual; eps 1e-6
+      cfg2        x, r [4096, 4096]; w; eps 1e-6
+      cfg3        82 = round(1% of 8192) outlier channels idx = randperm(8192)[:82];
+                  x [8192, 8192] ~N(0,1) with x[:, idx] *= 20 before the bf16 cast; r; w; eps 1e-5
+      cfg4        x [16384, 7168]; w; smooth fp32 [7168] ~U(0.5, 2); eps 1e-6
+      cfg5-decodeT x, r [T, 5120] (T in 1, 4, 16, 64); w; eps 1e-6
+      cfg5-large  x, r [32768, 16384]; w; eps 1e-6
+    Returns a dict of CPU tensors (x, r or None, w, sm or None) and eps."""
+    import torch
+
+    spec = {"cfg1": (1, 256, 4096, False, 1e-6), "cfg2": (2, 4096, 4096, True, 1e-6),
+            "cfg3": (3, 8192, 8192, True, 1e-5), "cfg4": (4, 16384, 7168, False, 1e-6),
+            "cfg5-large": (5, 32768, 16384, True, 1e-6),
+            **{f"cfg5-decode{t}": (5, t, 5120, True, 1e-6) for t in DECODE_T}}
+    seed, T, H, res, eps = spec[name]
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.randperm(H, generator=g)[: round(0.01 * H)] if name == "cfg3" else None
+    x = torch.randn(T, H, generator=g)
+    if idx is not None:
+        x[:, idx] *= 20.0
+    x = x.to(torch.bfloat16)
+    r = torch.randn(T, H, generator=g).to(torch.bfloat16) if res else None
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    sm = (0.5 + 1.5 * torch.rand(H, generator=g)) if name == "cfg4" else None
+    return {"x": x, "r": r, "w": w, "sm": sm, "eps": eps}
 
 
 # ------------------------------------------------------------------------------ workloads
@@ -67,15 +108,25 @@ class Workload:
         self.name, self.T, self.H, self.eps, self.kind = name, T, H, eps, kind
 
     @property
+    def seeded(self) -> bool:
+        """Inputs come from config_inputs (the configurations) rather than the device RNG."""
+        return self.name.startswith("cfg")
+
+    @property
     def pad(self) -> int:
         """Padded row size in bf16 elements (padded workloads): PAD_SIZE, or enough for H + 4."""
         return PAD_SIZE if 2 * PAD_SIZE >= self.H + 4 else (self.H + 4 + 63) // 64 * 32
 
     @property
     def bytes(self) -> int:
-        T, H = self.T, self.H
+        return self.bytes_for(self.T)
+
+    def bytes_for(self, T: int) -> int:
+        H = self.H
         if self.kind == "add_norm_int8":   # read x, r (2H each), w; write r (2H), q (H), s
             return 7 * T * H + 2 * H + 4 * T
+        if self.kind == "norm_int8":       # read x, w; write q, s
+            return 3 * T * H + 2 * H + 4 * T
         if self.kind == "fused_add":       # read x, r; write x, r; read w
             return 8 * T * H + 2 * H
         if self.kind == "smooth_fp8":      # read x; write q, after_res, after_norm; w, smooth, s
@@ -98,24 +149,37 @@ class Workload:
             return 4 * T * H + 2 * HEADS * H
         raise ValueError(self.kind)
 
-    def make(self, torch, dev, seed):
+    def device_sets(self, torch, dev, n_sets, cpu=None):
+        """n_sets input sets on the device: copies of the seeded CPU inputs for the
+        configurations (rotation only changes addresses), device-RNG draws otherwise."""
+        if self.seeded:
+            cpu = cpu or config_inputs(self.name)
+            return [self._alloc(torch, dev, {k: (v.to(dev) if hasattr(v, "to") and v is not None
+                                                 else v) for k, v in cpu.items()})
+                    for _ in range(n_sets)]
+        return [self._alloc(torch, dev, self._draw(torch, dev, 100 + i)) for i in range(n_sets)]
+
+    def _draw(self, torch, dev, seed):
         T, H = self.T, self.H
         g = torch.Generator(device=dev).manual_seed(seed)
-        x = torch.randn(T, H, generator=g, device=dev)
-        if self.name == "cfg3":
-            idx = torch.randperm(H, generator=torch.Generator().manual_seed(3))[: round(0.01 * H)]
-            x[:, idx.to(dev)] *= 20.0
-        x = x.to(torch.bfloat16)
+        x = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
         w = (1 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
-        d = {"x": x, "w": w}
+        d = {"x": x, "w": w, "r": None, "sm": None}
         if self.kind == "head_norm":       # x [T/HEADS tokens, HEADS, H], per-head weights
             d["x"] = x.view(T // HEADS, HEADS, H)
             d["w"] = (1 + 0.1 * torch.randn(HEADS, H, generator=g, device=dev)).to(torch.bfloat16)
-        if self.kind in ("norm_res", "vllm_norm", "head_norm"):
-            d["out"] = torch.empty_like(d["x"])
         if self.kind in ("add_norm_int8", "fused_add", "padded", "block_fp8", "norm_res"):
             d["r"] = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
-        if self.kind == "add_norm_int8":
+        if self.kind in ("sdq", "smooth_fp8"):
+            d["sm"] = 0.5 + 1.5 * torch.rand(H, generator=g, device=dev)
+        return d
+
+    def _alloc(self, torch, dev, d):
+        """Output buffers of one set."""
+        T, H, x = self.T, self.H, d["x"]
+        if self.kind in ("norm_res", "vllm_norm", "head_norm"):
+            d["out"] = torch.empty_like(x)
+        if self.kind in ("add_norm_int8", "norm_int8"):
             d["q"] = torch.empty(T, H, dtype=torch.int8, device=dev)
             d["s"] = torch.empty(T, 1, dtype=torch.float32, device=dev)
         if self.kind == "block_fp8":
@@ -132,10 +196,7 @@ class Workload:
             d["s"] = torch.empty(T, 1, dtype=torch.float32, device=dev)
             d["azp"] = (torch.empty(T, 1, dtype=torch.int32, device=dev)
                         if self.kind == "ptq_int8_azp" else None)
-        if self.kind == "sdq":
-            d["sm"] = 0.5 + 1.5 * torch.rand(H, generator=g, device=dev)
         if self.kind == "smooth_fp8":
-            d["sm"] = 0.5 + 1.5 * torch.rand(H, generator=g, device=dev)
             d["q"] = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=dev)
             d["s"] = torch.empty(T, dtype=torch.float32, device=dev)
             d["ar"] = torch.empty_like(x)
@@ -143,11 +204,14 @@ class Workload:
         return d
 
     def launcher(self, torch, d):
-        from mcoplib_amd import op
-        import mcoplib_amd._C  # noqa: F401
+        from mcoplib import op
+        import mcoplib._C  # noqa: F401
         if self.kind == "add_norm_int8":
             return lambda: op.rms_norm_dynamic_per_token_quant_custom(
                 d["q"], d["x"], d["w"], d["s"], self.eps, None, d["r"])
+        if self.kind == "norm_int8":
+            return lambda: torch.ops._C.rms_norm_dynamic_per_token_quant(
+                d["q"], d["x"], d["w"], d["s"], self.eps, None, None)
         if self.kind == "fused_add":
             return lambda: torch.ops._C.fused_add_rms_norm(d["x"], d["r"], d["w"], self.eps)
         if self.kind == "norm_res":
@@ -175,12 +239,13 @@ class Workload:
 
 
 WORKLOADS = {
+    "cfg1": Workload("cfg1", 256, 4096, 1e-6, "norm_int8"),
     "cfg2": Workload("cfg2", 4096, 4096, 1e-6, "fused_add"),
     "cfg3": Workload("cfg3", 8192, 8192, 1e-5, "add_norm_int8"),
     "cfg4": Workload("cfg4", 16384, 7168, 1e-6, "smooth_fp8"),
     "cfg5-large": Workload("cfg5-large", 32768, 16384, 1e-6, "add_norm_int8"),
     **{f"cfg5-decode{t}": Workload(f"cfg5-decode{t}", t, 5120, 1e-6, "add_norm_int8")
-       for t in (1, 4, 16, 64)},
+       for t in DECODE_T},
     # the standalone quantizers, at the headline shape (the step after an unfused norm)
     "ptq-int8": Workload("ptq-int8", 8192, 8192, 0.0, "ptq_int8"),
     "ptq-int8-azp": Workload("ptq-int8-azp", 8192, 8192, 0.0, "ptq_int8_azp"),
@@ -196,7 +261,7 @@ WORKLOADS = {
     "head-norm": Workload("head-norm", 65536 * 8, 128, 1e-6, "head_norm"),
     # the un-normed SmoothQuant sibling (scale_dynamic_quant) at SmoothQuant's shape
     "sdq": Workload("sdq", 16384, 7168, 0.0, "sdq"),
-    # rows wider than the registers hold: the headline operator's multi-pass kernel
+    # rows wider than the registers hold: each operator's multi-pass kernel
     "wide-int8": Workload("wide-int8", 2048, 131072, 1e-6, "add_norm_int8"),
     "wide-fused": Workload("wide-fused", 2048, 131072, 1e-6, "fused_add"),
     "wide-fp8": Workload("wide-fp8", 2048, 131072, 1e-6, "smooth_fp8"),
@@ -206,153 +271,397 @@ WORKLOADS = {
     "wide-padded": Workload("wide-padded", 2048, 131072, 1e-6, "padded"),
     "wide-block": Workload("wide-block", 2048, 131072, 1e-6, "block_fp8"),
 }
-KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "fused_add": "k_fused_add_rms_norm",
+KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "norm_int8": "k_rms_norm_quant",
+               "fused_add": "k_fused_add_rms_norm",
                "smooth_fp8": "k_rms_norm_smooth_quant", "ptq_int8": "k_per_token_quant",
                "ptq_int8_azp": "k_per_token_quant", "ptq_fp8": "k_per_token_quant",
                "padded": "k_add_rms_norm_quant_padded", "block_fp8": "k_rms_norm_group_quant",
                "norm_res": "k_rms_norm", "vllm_norm": "k_rms_norm", "head_norm": "k_rms_norm",
                "sdq": "k_scale_dynamic_quant"}
-# workloads whose kernel is not their kind's register-resident one
-KERNEL_NAME_OF_WORKLOAD = {"wide-int8": "k_rms_norm_quant_wide",
-                           "wide-fused": "k_fused_add_rms_norm_wide",
-                           "wide-fp8": "k_rms_norm_smooth_quant_wide",
-                           "wide-sdq": "k_scale_dynamic_quant_wide",
-                           "wide-norm": "k_rms_norm_wide", "wide-ptq": "k_per_token_quant_wide",
-                           "wide-padded": "k_add_rms_norm_quant_padded_wide",
-                           "wide-block": "k_rms_norm_group_quant_wide"}
 
 
 def kernel_name(wl) -> str:
-    return KERNEL_NAME_OF_WORKLOAD.get(wl.name, KERNEL_NAME[wl.kind])
+    return KERNEL_NAME[wl.kind] + ("_wide" if wl.name.startswith("wide-") else "")
 
 
-# ------------------------------------------------------------------------------ pieces
-def traffic_from_profiles(wl: Workload):
-    """HBM bytes per dispatch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by
-    a copy kernel's reading), from the committed summary, or None."""
+# Compute-free kernels with a configuration's access pattern (include/mcop_pattern.h), at the
+# launch shape the operator picks for it (vectors per lane, lanes per row).
+PATTERN_OF = {"cfg2": (1, 2, 256), "cfg3": (0, 2, 512), "cfg4": (2, 4, 256),
+              "cfg5-large": (0, 4, 512)}
+PATTERN_COPY, PATTERN_READ, PATTERN_WRITE = 3, 4, 5
+
+
+# ------------------------------------------------------------------------------ profiles
+def profile_summary(wl: Workload):
+    """Figures of the committed rocprofv3 summary profiles/<kernel>_<workload>.txt: HBM bytes per
+    dispatch (FETCH_SIZE + WRITE_SIZE passes, each scaled by a copy kernel's reading) and the
+    kernel-trace mean of the timed launches; None where absent."""
     p = ROOT / "profiles" / f"{kernel_name(wl)}_{wl.name}.txt"
     if not p.exists():
         return None
-    m = re.search(r"^hbm_bytes_per_dispatch:\s*([0-9.eE+]+)", p.read_text(), re.M)
-    return float(m.group(1)) if m else None
+    t = p.read_text()
+    m = re.search(r"^hbm_bytes_per_dispatch:\s*([0-9.eE+]+)", t, re.M)
+    k = re.search(r"^timed legs \((\d+) dispatches\): mean ([0-9.]+) us", t, re.M)
+    return {"file": str(p.relative_to(ROOT)),
+            "hbm_bytes_per_dispatch": float(m.group(1)) if m else None,
+            "trace_mean_us": float(k.group(2)) if k else None}
 
 
-def cpu_baseline(wl: Workload, seconds: float) -> dict:
-    """The C oracle (oracle/mcop_oracle.c, OpenMP over rows) on a bounded row sample of the same
-    workload, on this host's cores; reported in the metric's unit."""
-    import torch
-    import oracle  # CPU baseline leg only
+# ------------------------------------------------------------------------------ GPU timing
+def _ev(torch):
+    return torch.cuda.Event(enable_timing=True)
 
-    cores = len(os.sched_getaffinity(0))
-    oracle.set_threads(cores)
-    rows = min(wl.T, 1024)
-    g = torch.Generator().manual_seed(7)
-    x = torch.randn(rows, wl.H, generator=g).to(torch.bfloat16)
-    r = torch.randn(rows, wl.H, generator=g).to(torch.bfloat16)
-    w = (1 + 0.1 * torch.randn(wl.H, generator=g)).to(torch.bfloat16)
-    sm = 0.5 + 1.5 * torch.rand(wl.H, generator=g)
 
-    def run():
-        if wl.kind == "add_norm_int8":
-            oracle.rms_norm_dynamic_per_token_quant(x, w, wl.eps, torch.int8, residual=r)
-        elif wl.kind == "fused_add":
-            oracle.fused_add_rms_norm(x, r, w, wl.eps)
-        elif wl.kind == "norm_res":
-            oracle.rms_norm(x, w, wl.eps, residual=r)
-        elif wl.kind == "vllm_norm":
-            oracle.vllm_rms_norm(x, w, wl.eps)
-        elif wl.kind == "head_norm":
-            xs = x.reshape(-1, HEADS, wl.H)
-            oracle.head_rms_norm(xs, xs, w.repeat(HEADS).view(HEADS, wl.H), wl.eps, 0, HEADS)
-        elif wl.kind == "block_fp8":
-            oracle.rms_norm_per_block_quant(x, w, wl.eps, torch.float8_e4m3fn, BLOCK_GROUP,
-                                            residual=r)
-        elif wl.kind == "padded":
-            oracle.add_rms_norm_quant_padded(x, r, w, wl.pad, wl.eps)
-        elif wl.kind == "sdq":
-            oracle.scale_dynamic_quant(x, sm)
-        elif wl.kind == "ptq_fp8":
-            oracle.dynamic_per_token_scaled_fp8_quant(x)
-        elif wl.kind.startswith("ptq_int8"):
-            oracle.dynamic_scaled_int8_quant(x, use_azp=wl.kind == "ptq_int8_azp")
-        else:
-            oracle.rms_norm_smooth_quant(x, w, sm, wl.eps, torch.float8_e4m3fn)
+def time_launches(torch, launches, K, warmup, warmup_seconds):
+    """Warm up (the requested launches, continued until the GPU has been busy for
+    `warmup_seconds`), then time K back-to-back launches between two HIP events on torch's
+    current stream (the stream the operators launch on).  Returns (ms per launch, host seconds)."""
+    i, t_w = 0, time.perf_counter()
+    while i < warmup or time.perf_counter() - t_w < warmup_seconds:
+        launches[i % len(launches)]()
+        i += 1
+        if i % 64 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    e0, e1 = _ev(torch), _ev(torch)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(K):
+        launches[i % len(launches)]()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / K, time.perf_counter() - t0
 
-    run()
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 5:
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    sample_bytes = Workload(wl.name, rows, wl.H, wl.eps, wl.kind).bytes
-    cpu_model = ""
+
+def graph_us(torch, launches, K):
+    """us per call of the same K launches replayed from a HIP graph (best of 5 replays)."""
+    g = torch.cuda.CUDAGraph()
+    s_cap = torch.cuda.Stream()
+    s_cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s_cap):
+        with torch.cuda.graph(g, stream=s_cap):
+            for i in range(K):
+                launches[i % len(launches)]()
+    torch.cuda.current_stream().wait_stream(s_cap)
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(5):
+        e0, e1 = _ev(torch), _ev(torch)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / K)
+    return best
+
+
+class Pattern:
+    """ctypes binding of libmcop_pattern.so (compute-free access-pattern kernels)."""
+
+    def __init__(self):
+        import ctypes
+        path = ROOT / "mcoplib_amd" / "libmcop_pattern.so"
+        if not path.exists():
+            raise RuntimeError(f"{path} is not built (python mcoplib_amd/_build.py)")
+        self.lib = ctypes.CDLL(str(path))
+        P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        self.lib.mcop_pattern.argtypes = [I, P, P, P, P, P, P, P, P, I64, I64, I, I, I, P]
+        self.lib.mcop_pattern.restype = I
+        self.lib.mcop_pattern_last_error.restype = ctypes.c_char_p
+
+    def launcher(self, torch, pattern, d, T, H, nv, tpr, lds=0):
+        def p(t):
+            return None if t is None else t.data_ptr()
+        stream = torch.cuda.current_stream().cuda_stream
+        args = (pattern, p(d.get("x")), p(d.get("r")), p(d.get("w")), p(d.get("sm")),
+                p(d.get("o0")), p(d.get("o1")), p(d.get("q")), p(d.get("s")), T, H, nv, tpr,
+                lds, stream)
+
+        def run():
+            rc = self.lib.mcop_pattern(*args)
+            if rc != 0:
+                raise RuntimeError(self.lib.mcop_pattern_last_error().decode())
+        return run
+
+
+def pattern_us(torch, pat, pattern, T, H, nv, tpr, dev, K, with_w=False, with_sm=False, lds=0):
+    """us per launch of a pattern kernel over [T, H] bf16 tensors (rotated copies to defeat the
+    last-level cache), at the given launch shape (and `lds` bytes of LDS per workgroup)."""
+    per_set = T * H * 7
+    n_sets = max(2, -(-(1 << 30) // per_set))
+    sets = []
+    for _ in range(n_sets):
+        d = {"x": torch.zeros(T, H, dtype=torch.bfloat16, device=dev),
+             "r": torch.zeros(T, H, dtype=torch.bfloat16, device=dev),
+             "o0": torch.empty(T, H, dtype=torch.bfloat16, device=dev),
+             "o1": torch.empty(T, H, dtype=torch.bfloat16, device=dev),
+             "q": torch.empty(T, H, dtype=torch.uint8, device=dev),
+             "s": torch.empty(T, dtype=torch.float32, device=dev)}
+        if pattern == 1:  # in place, as the operator writes x and r
+            d["o0"], d["o1"] = d["x"], d["r"]
+        if with_w:
+            d["w"] = torch.ones(H, dtype=torch.bfloat16, device=dev)
+        if with_sm:
+            d["sm"] = torch.ones(H, dtype=torch.float32, device=dev)
+        sets.append(d)
+    launches = [pat.launcher(torch, pattern, d, T, H, nv, tpr, lds) for d in sets]
+    ms, _ = time_launches(torch, launches, K, 5, 0.3)
+    del sets, launches
+    torch.cuda.empty_cache()
+    return ms * 1e3
+
+
+# ------------------------------------------------------------------------------ CPU legs
+def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s", "cores": cores,
-            "kind": "port",
-            "sample": f"{rows} of {wl.T} rows x {wl.H} (same byte model), median of {len(times)} "
-                      f"runs over ~{seconds:.0f} s, oracle/mcop_oracle.c with {cores} OpenMP "
-                      f"threads, {cpu_model}",
-            "tokens_per_s": round(rows / med, 1)}
+    return ""
 
 
-def torch_cpu_add_norm_int8(x, r, w, eps: float):
-    """Add + RMSNorm + per-token int8 restated in vectorized torch (the form of the reference's
-    own torch-native test oracles), following the reference's rounding points
+def _time_cpu(fn, seconds, min_runs=3):
+    fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < min_runs:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def oracle_call(wl: Workload, c: dict):
+    """The C oracle (oracle/mcop_oracle.c) on the rows in c: the operation the workload's GPU
+    launch performs.  Returns its outputs in the order the GPU check compares them."""
+    import torch
+    import oracle  # CPU baseline leg only
+    if wl.kind == "add_norm_int8":
+        q, s, r = oracle.rms_norm_dynamic_per_token_quant_custom(c["x"], c["w"], wl.eps,
+                                                                 residual=c["r"])
+        return {"q": q, "s": s, "r": r}
+    if wl.kind == "norm_int8":
+        q, s, _ = oracle.rms_norm_dynamic_per_token_quant(c["x"], c["w"], wl.eps, torch.int8)
+        return {"q": q, "s": s}
+    if wl.kind == "fused_add":
+        x, r = oracle.fused_add_rms_norm(c["x"], c["r"], c["w"], wl.eps)
+        return {"x": x, "r": r}
+    if wl.kind == "smooth_fp8":
+        q, s, ar, an = oracle.rms_norm_smooth_quant(c["x"], c["w"], c["sm"], wl.eps,
+                                                    torch.float8_e4m3fn)
+        return {"q": q, "s": s, "ar": ar, "an": an}
+    raise ValueError(wl.kind)
+
+
+def cpu_baseline(wl: Workload, cpu: dict, rows: int, seconds: float, gpu_out=None,
+                 threads=None) -> dict:
+    """The C oracle (OpenMP over rows) on the first `rows` rows of the workload's seeded inputs,
+    on this host's cores (or `threads`), in the metric's unit; with gpu_out (the GPU's outputs of
+    its first call on the same rows) also whether the GPU matched it bit for bit."""
+    import torch
+    import oracle  # CPU baseline leg only
+
+    cores = threads or len(os.sched_getaffinity(0))
+    oracle.set_threads(cores)
+    c = {k: (v[:rows] if (torch.is_tensor(v) and v.dim() == 2) else v) for k, v in cpu.items()}
+    med, n = _time_cpu(lambda: oracle_call(wl, c), seconds, 5)
+    oracle.set_threads(len(os.sched_getaffinity(0)))  # the OpenMP runtime may be torch's too
+    out = {"value": round(wl.bytes_for(rows) / med / 1e9, 3), "unit": "GB/s", "cores": cores,
+           "kind": "port", "us_per_call": round(med * 1e6, 2),
+           "sample": f"first {rows} of {wl.T} rows x {wl.H} of the same seeded inputs (same "
+                     f"byte model), median of {n} runs over ~{seconds:.0f} s, "
+                     f"oracle/mcop_oracle.c with {cores} OpenMP threads, {_cpu_model()}",
+           "tokens_per_s": round(rows / med, 1)}
+    if gpu_out is not None:
+        n_chk = next(iter(gpu_out.values())).shape[0]
+        ref = oracle_call(wl, {k: (v[:n_chk] if (torch.is_tensor(v) and v.dim() == 2) else v)
+                               for k, v in cpu.items()})
+        diffs = {}
+        for k, g in gpu_out.items():
+            a, b = g.view(-1), ref[k].reshape(-1)
+            if a.dtype in (torch.bfloat16, torch.float16, torch.float8_e4m3fn):
+                a, b = a.view(torch.uint8 if a.element_size() == 1 else torch.int16), \
+                    b.view(torch.uint8 if b.element_size() == 1 else torch.int16)
+            elif a.dtype == torch.float32:
+                a, b = a.view(torch.int32), b.view(torch.int32)
+            diffs[k] = int((a != b).sum())
+        out["gpu_first_call_vs_oracle"] = {"rows": n_chk, "differing_values": diffs,
+                                           "bit_exact": all(v == 0 for v in diffs.values())}
+    return out
+
+
+def torch_cpu_add_norm_int8(x, r, w, eps: float, floor=None, lo=-128):
+    """(Residual add +) RMSNorm + per-token int8 restated in vectorized torch (the form of the
+    reference's own torch-native test oracles), following the reference's rounding points
     (op/vllm/quantization/fused_kernels/layernorm_utils.cuh:245-276, 436-447, 503-531 and
     fused_layernorm_dynamic_per_token_quant.cu:37): residual b(x + r), rho on the unrounded sum,
-    y = b(b(a * rho) * w), s = max(A / 127, FLT_EPSILON), q = sat(rne(y * (1/s))).
-    Returns (q, s, residual)."""
+    y = b(b(a * rho) * w), s = max(A / 127, floor), q = sat[lo, 127](rne(y * (1/s))).  The floor
+    is FLT_EPSILON for vLLM's operator; mcoplib's own (op/rms_norm_dynamic_per_token_quant.cu,
+    kernel/rms_norm_vllm.cuh:382 and kernel/utils.h:219-226) uses 1.5e-6 and lo = -127.
+    r may be None (no residual).  Returns (q, s, residual or None)."""
     import torch
 
     bf, H = torch.bfloat16, x.shape[-1]
-    a = x.float() + r.float()
-    res = a.to(bf)
+    floor = torch.finfo(torch.float32).eps if floor is None else floor
+    a = x.float() + (r.float() if r is not None else 0.0)
+    res = a.to(bf) if r is not None else None
     ss = (a.double() * a.double()).sum(-1, keepdim=True)
     rho = 1.0 / torch.sqrt((ss / H).float() + eps)
     y = ((a * rho).to(bf).float() * w.float()).to(bf).float()
-    s = torch.clamp(y.abs().amax(-1, keepdim=True) / 127.0, min=torch.finfo(torch.float32).eps)
-    q = torch.round(y * (1.0 / s)).clamp(-128, 127).to(torch.int8)
+    s = torch.clamp(y.abs().amax(-1, keepdim=True) / 127.0, min=floor)
+    q = torch.round(y * (1.0 / s)).clamp(lo, 127).to(torch.int8)
     return q, s, res
 
 
-def cpu_torch(wl: Workload, seconds: float):
-    """torch_cpu_add_norm_int8 timed on this host (torch's intra-op threads) on a bounded row
-    sample, beside the C oracle.  Only the headline operation (kind add_norm_int8) has this leg;
-    None otherwise."""
-    if wl.kind != "add_norm_int8":
-        return None
+def cpu_torch(wl: Workload, cpu: dict, rows: int, seconds: float):
+    """torch_cpu_add_norm_int8 timed on this host (torch's intra-op threads) on the first `rows`
+    rows of the seeded inputs, beside the C oracle (add_norm_int8 and norm_int8 kinds only)."""
     import torch
 
-    rows = min(wl.T, 512)
-    g = torch.Generator().manual_seed(7)
-    x = torch.randn(rows, wl.H, generator=g).to(torch.bfloat16)
-    r = torch.randn(rows, wl.H, generator=g).to(torch.bfloat16)
-    w = (1 + 0.1 * torch.randn(wl.H, generator=g)).to(torch.bfloat16)
-    torch_cpu_add_norm_int8(x, r, w, wl.eps)
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        torch_cpu_add_norm_int8(x, r, w, wl.eps)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    sample_bytes = Workload(wl.name, rows, wl.H, wl.eps, wl.kind).bytes
+    if wl.kind == "add_norm_int8":
+        fn = lambda: torch_cpu_add_norm_int8(cpu["x"][:rows], cpu["r"][:rows], cpu["w"],  # noqa
+                                             wl.eps, floor=1.5e-6, lo=-127)
+    elif wl.kind == "norm_int8":
+        fn = lambda: torch_cpu_add_norm_int8(cpu["x"][:rows], None, cpu["w"], wl.eps)  # noqa
+    else:
+        return None
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    med, n = _time_cpu(fn, seconds, 3)
     threads = torch.get_num_threads()
-    return {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "sample": f"{rows} of {wl.T} rows x {wl.H}, median of {len(times)} runs over "
-                      f"~{seconds:.0f} s, vectorized torch on the CPU with {threads} intra-op "
-                      "threads (bench.py torch_cpu_add_norm_int8)",
+    return {"value": round(wl.bytes_for(rows) / med / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "us_per_call": round(med * 1e6, 2),
+            "sample": f"first {rows} of {wl.T} rows x {wl.H} of the same seeded inputs, median "
+                      f"of {n} runs over ~{seconds:.0f} s, vectorized torch on the CPU with "
+                      f"{threads} intra-op threads (bench.py torch_cpu_add_norm_int8)",
             "tokens_per_s": round(rows / med, 1)}
 
 
+# ------------------------------------------------------------------------------ one config
+def first_call_outputs(torch, wl: Workload, d: dict, rows: int):
+    """The outputs of one launch on a fresh set, first `rows` rows, on the CPU."""
+    keys = {"add_norm_int8": ("q", "s", "r"), "norm_int8": ("q", "s"), "fused_add": ("x", "r"),
+            "smooth_fp8": ("q", "s", "ar", "an")}[wl.kind]
+    wl.launcher(torch, d)()
+    torch.cuda.synchronize()
+    return {k: d[k][:rows].cpu() for k in keys}
+
+
+def measure(torch, wl: Workload, args, dev, cpu=None, check_rows=0, hot=True, warmup_s=None):
+    """Time K launches of a workload over rotated input sets; returns a dict of figures (and
+    the GPU's first-call outputs of `check_rows` rows when asked)."""
+    K = args.steps
+    # > 1 GiB of rotated copies for the bandwidth-bound shapes; decode-sized calls are latency
+    # bound (their inputs sit in the caches whatever the rotation): three copies
+    n_sets = args.sets or (3 if wl.T <= 256 else max(3, -(-(1 << 30) // wl.bytes)))
+    if wl.seeded and cpu is None:
+        cpu = config_inputs(wl.name)
+    sets = wl.device_sets(torch, dev, n_sets, cpu)
+    first = first_call_outputs(torch, wl, sets[0], check_rows) if check_rows else None
+    launches = [wl.launcher(torch, d) for d in sets]
+    ms, wall = time_launches(torch, launches, K, args.warmup,
+                             args.warmup_seconds if warmup_s is None else warmup_s)
+    res = {"ms": ms, "wall": wall, "sets": len(sets), "first": first}
+    if hot:
+        # single-launch spread (an event pair around every launch: also times the event
+        # packets, so its mean sits above the back-to-back figure) and one set only (hot caches)
+        ev = [(_ev(torch), _ev(torch)) for _ in range(K)]
+        for i in range(K):
+            ev[i][0].record()
+            launches[i % len(launches)]()
+            ev[i][1].record()
+        torch.cuda.synchronize()
+        per = sorted(a.elapsed_time(b) for a, b in ev)
+        res["p10_p50_p90_us"] = [round(per[int(q * (K - 1))] * 1e3, 3) for q in (0.1, 0.5, 0.9)]
+        h0, h1 = _ev(torch), _ev(torch)
+        h0.record()
+        for _ in range(K):
+            launches[0]()
+        h1.record()
+        torch.cuda.synchronize()
+        res["hot_ms"] = h0.elapsed_time(h1) / K
+    if wl.T <= 256:
+        res["graph_us"] = graph_us(torch, launches, K)
+    del sets, launches
+    torch.cuda.empty_cache()
+    return res
+
+
+def config_entry(torch, wl: Workload, args, dev, pat, entry: str):
+    """The figures of one GPU configuration for the `configs` object."""
+    cpu = config_inputs(wl.name)
+    check = min(wl.T, 256)
+    m = measure(torch, wl, args, dev, cpu, check_rows=check, hot=False, warmup_s=0.5)
+    us = m["ms"] * 1e3
+    gbs = wl.bytes / (m["ms"] * 1e-3) / 1e9
+    out = {"entry": entry, "kernel": kernel_name(wl),
+           "shape": [wl.T, wl.H], "algorithmic_bytes": wl.bytes, "us_per_call": round(us, 3),
+           "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+           "tokens_per_s": round(wl.T / (m["ms"] * 1e-3), 1), "rotated_input_sets": m["sets"]}
+    prof = profile_summary(wl)
+    if prof:
+        out["profile"] = prof["file"]
+        out["rocprof_trace_mean_us"] = prof["trace_mean_us"]
+        if prof["hbm_bytes_per_dispatch"]:
+            out["traffic_ratio"] = round(prof["hbm_bytes_per_dispatch"] / wl.bytes, 4)
+    if pat is not None and wl.name in PATTERN_OF:
+        p, nv, tpr = PATTERN_OF[wl.name]
+        pus = pattern_us(torch, pat, p, wl.T, wl.H, nv, tpr, dev, args.steps, with_w=True,
+                         with_sm=wl.kind == "smooth_fp8")
+        out["pattern_us"] = round(pus, 3)
+        out["kernel_vs_pattern"] = round(pus / us, 4)
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(wl, cpu, min(wl.T, 512), args.cpu_seconds / 3,
+                                           m["first"])
+    return out
+
+
+def decode_entry(torch, args, dev):
+    """cfg5 decode: us per call, eager (K back-to-back calls between events) and replayed from
+    a HIP graph, for T in DECODE_T at H = 5120; the C oracle on one thread beside it."""
+    out = {"entry": "mcoplib.op.rms_norm_dynamic_per_token_quant_custom with residual",
+           "hidden": 5120}
+    for t in DECODE_T:
+        wl = WORKLOADS[f"cfg5-decode{t}"]
+        cpu = config_inputs(wl.name)
+        m = measure(torch, wl, args, dev, cpu, check_rows=t, hot=False, warmup_s=0.3)
+        e = {"eager_us": round(m["ms"] * 1e3, 3), "graph_us": round(m["graph_us"], 3),
+             "algorithmic_bytes": wl.bytes}
+        if not args.no_cpu:
+            cb = cpu_baseline(wl, cpu, t, 1.0, m["first"], threads=1)
+            e["cpu_us"] = cb["us_per_call"]
+            e["cpu_cores"] = 1
+            e["gpu_first_call_vs_oracle"] = cb["gpu_first_call_vs_oracle"]
+        out[f"T{t}"] = e
+    return out
+
+
+def cfg1_entry(args):
+    """cfg1 runs on the CPU only: the C oracle (all cores, and one) and the torch restatement."""
+    import torch
+
+    wl = WORKLOADS["cfg1"]
+    cpu = config_inputs("cfg1")
+    out = {"entry": "rms_norm_dynamic_per_token_quant (vLLM), no residual, int8", "cpu_only": True,
+           "shape": [wl.T, wl.H], "algorithmic_bytes": wl.bytes}
+    if args.no_cpu:
+        return out
+    secs = args.cpu_seconds / 3
+    out["oracle"] = cpu_baseline(wl, cpu, wl.T, secs)
+    out["oracle_1_thread"] = cpu_baseline(wl, cpu, wl.T, secs, threads=1)
+    out["torch"] = cpu_torch(wl, cpu, wl.T, secs)
+    # the torch restatement and the oracle agree bit for bit on this input
+    q, s, _ = torch_cpu_add_norm_int8(cpu["x"], None, cpu["w"], wl.eps)
+    ref = oracle_call(wl, cpu)
+    out["torch_equals_oracle"] = bool(torch.equal(q, ref["q"]) and
+                                      torch.equal(s.view(-1), ref["s"].view(-1)))
+    return out
+
+
+# ------------------------------------------------------------------------------ main
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -366,7 +675,7 @@ def main() -> int:
         print("bench.py: no HIP device visible", file=sys.stderr)
         return 1
     sys.path.insert(0, str(ROOT))
-    import mcoplib_amd  # noqa: F401  (fails loudly if libmcop_norm.so is missing)
+    import mcoplib  # noqa: F401  (fails loudly if libmcop_norm.so is missing)
 
     dev = "cuda:0"
     torch.cuda.set_device(0)
@@ -378,96 +687,30 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    n_sets = args.sets or max(3, -(-(1 << 30) // wl.bytes))
-    sets = [wl.make(torch, dev, 100 + i) for i in range(n_sets)]
-    launches = [wl.launcher(torch, d) for d in sets]
-    # warm-up: the requested steps, continued until the GPU has been busy for ~2 s so that
-    # clocks and power state have settled before the timed region
-    i, t_w = 0, time.perf_counter()
-    while i < args.warmup or time.perf_counter() - t_w < args.warmup_seconds:
-        launches[i % len(launches)]()
-        i += 1
-        if i % 64 == 0:
-            torch.cuda.synchronize()
-    torch.cuda.synchronize()
+    if wl.kind == "norm_int8":
+        print("bench.py: cfg1 is measured on the CPU only (it is part of the default run's "
+              "`configs`)", file=sys.stderr)
+        return 2
 
-    K = args.steps
-    # (1) whole-job throughput: K back-to-back steps between two events
-    t_start, t_stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    t_start.record()
-    for i in range(K):
-        launches[i % len(launches)]()
-    t_stop.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    total_ms = t_start.elapsed_time(t_stop)
-    ms_per_step = total_ms / K
-    # (2) a second pass with an event pair around every launch: the spread of single-launch
-    # times (each pair also times the event packets themselves, so its mean sits above the
-    # back-to-back figure, which is what rocprofv3's kernel trace reports)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(K)]
-    for i in range(K):
-        ev[i][0].record()
-        launches[i % len(launches)]()
-        ev[i][1].record()
-    torch.cuda.synchronize()
-    per_launch_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    cpu = config_inputs(wl.name) if wl.seeded else None
+    check_rows = min(wl.T, 1024) if (wl.seeded and not args.no_cpu) else 0
+    m = measure(torch, wl, args, dev, cpu, check_rows=check_rows)
+    K, ms = args.steps, m["ms"]
+    value = wl.bytes / (ms * 1e-3) / 1e9
     # one step is exactly one launch of the kernel and nothing else runs on the stream, so the
     # kernel's average launch duration over the timed region is total / K
-    kernel_ms = ms_per_step
-
-    # (2b) the same K steps on one input set only (hot: small sets stay in the 256 MB MALL)
-    h0, h1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    h0.record()
-    for i in range(K):
-        launches[0]()
-    h1.record()
-    torch.cuda.synchronize()
-    hot_ms = h0.elapsed_time(h1) / K
-    # (2c) this GPU's device-copy bandwidth (1 GiB copy_, read + write bytes): the practical
-    # ceiling of a streaming kernel, reported next to the 8 TB/s peak
-    csrc = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    cdst = torch.empty_like(csrc)
-    for _ in range(3):
-        cdst.copy_(csrc)
-    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    c0.record()
-    for _ in range(5):
-        cdst.copy_(csrc)
-    c1.record()
-    torch.cuda.synchronize()
-    copy_gbs = 2 * 5 * (1 << 30) / (c0.elapsed_time(c1) * 1e-3) / 1e9
-    del csrc, cdst
-
-    # (3) decode shapes are launch-bound: also time the same steps replayed from a HIP graph
-    graph_us = None
-    if wl.T <= 256:
-        g = torch.cuda.CUDAGraph()
-        s_cap = torch.cuda.Stream()
-        s_cap.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s_cap):
-            with torch.cuda.graph(g, stream=s_cap):
-                for i in range(K):
-                    launches[i % len(launches)]()
-        torch.cuda.current_stream().wait_stream(s_cap)
-        for _ in range(3):
-            g.replay()
-        torch.cuda.synchronize()
-        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 5
-        g0.record()
-        for _ in range(reps):
-            g.replay()
-        g1.record()
-        torch.cuda.synchronize()
-        graph_us = g0.elapsed_time(g1) * 1e3 / (reps * K)
-
-    value = wl.bytes / (ms_per_step * 1e-3) / 1e9
-    achieved = wl.bytes / (kernel_ms * 1e-3) / 1e9
-    traffic = traffic_from_profiles(wl)
+    kernel_us = ms * 1e3
+    prof = profile_summary(wl)
+    traffic = prof["hbm_bytes_per_dispatch"] if prof else None
+    roof = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "traffic_ratio": round(traffic / wl.bytes, 4) if traffic else None,
+            "kernel": kernel_name(wl), "kernel_avg_us": round(kernel_us, 3),
+            "kernel_avg_us_from": "HIP events around the K timed launches on the launch stream",
+            "rocprof_trace_mean_us": prof["trace_mean_us"] if prof else None,
+            "profile": prof["file"] if prof else None,
+            "single_launch_us_p10_p50_p90": m.get("p10_p50_p90_us"),
+            "algorithmic_bytes_per_launch": wl.bytes}
     out = {
         "metric": METRIC if wl.name == "cfg3" else f"HBM GB/s: {wl.name} ({wl.kind}, {wl.T}x{wl.H})",
         "value": round(value, 2),
@@ -475,38 +718,76 @@ def main() -> int:
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 6),
+        "ms_per_step": round(ms, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic",
+        "data": "synthetic: seeded CPU inputs copied to the GPU, the same bits in every leg"
+                if wl.seeded else "synthetic: device-RNG inputs",
         "config": {"workload": f"{wl.name}: {wl.kind} T={wl.T} H={wl.H} bf16 in"
                                + ("" if wl.kind.startswith("ptq_") or wl.kind == "sdq" else f", eps={wl.eps}")
                                + (", 1% outlier channels x20" if wl.name == "cfg3" else ""),
                    "tokens": wl.T, "hidden": wl.H, "io": "bf16 -> int8/fp8 + fp32 scales",
-                   "rotated_input_sets": len(sets)},
+                   "rotated_input_sets": m["sets"]},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "tokens_per_s": round(wl.T / (ms_per_step * 1e-3), 1),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic,
-                     "kernel": kernel_name(wl),
-                     "kernel_avg_us": round(kernel_ms * 1e3, 3),
-                     "single_launch_us_p10_p50_p90": [
-                         round(per_launch_ms[int(q * (K - 1))] * 1e3, 3) for q in (0.1, 0.5, 0.9)],
-                     "algorithmic_bytes_per_launch": wl.bytes},
-        "device_copy": {"GBs": round(copy_gbs, 1), "frac": round(value / copy_gbs, 4),
-                        "what": "1 GiB torch copy_ on this GPU, read + write bytes"},
-        "hot_value": round(wl.bytes / (hot_ms * 1e-3) / 1e9, 2),
+        "tokens_per_s": round(wl.T / (ms * 1e-3), 1),
+        "roofline": roof,
+        "hot_value": round(wl.bytes / (m["hot_ms"] * 1e-3) / 1e9, 2),
         "hot_note": "the same steps on one input set (not rotated)",
-        "host_wall_s": round(wall, 4),
-        "us_per_call": round(ms_per_step * 1e3, 3),
-        "us_per_call_graph": None if graph_us is None else round(graph_us, 3),
+        "host_wall_s": round(m["wall"], 4),
+        "us_per_call": round(kernel_us, 3),
+        "us_per_call_graph": None if "graph_us" not in m else round(m["graph_us"], 3),
     }
-    if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
-        out["cpu_torch"] = cpu_torch(wl, min(args.cpu_seconds, 10.0))
+    if wl.name == "cfg3":
+        tr = roof["traffic_ratio"]
+        out["guard"] = {"frac_min": FRAC_GUARD, "traffic_ratio_max": TRAFFIC_GUARD,
+                        "frac": roof["frac"], "traffic_ratio": tr,
+                        "regressed": bool(roof["frac"] < FRAC_GUARD or tr is None
+                                          or tr > TRAFFIC_GUARD)}
+    pat = None
+    if not args.no_configs:
+        pat = Pattern()
+        # streaming ceilings over 1 GiB of bf16 (read-only and write-only: 1 GiB moved; copy:
+        # 1 GiB read + 1 GiB written) at the launch shape that streams fastest on this GPU (one
+        # 16-byte vector a lane, 2048-element rows of 256 lanes: measured best of 1-8 vectors a
+        # lane and 64-1024 lanes)
+        T1, H1 = 262144, 2048
+        cu = pattern_us(torch, pat, PATTERN_COPY, T1, H1, 1, 256, dev, K)
+        ru = pattern_us(torch, pat, PATTERN_READ, T1, H1, 1, 256, dev, K)
+        wu = pattern_us(torch, pat, PATTERN_WRITE, T1, H1, 1, 256, dev, K)
+        copy_gbs = 2 * T1 * H1 * 2 / (cu * 1e-6) / 1e9
+        out["device_copy"] = {"GBs": round(copy_gbs, 1), "frac": round(value / copy_gbs, 4),
+                              "what": "non-temporal streaming copy kernel (libmcop_pattern.so), "
+                                      "1 GiB read + 1 GiB written, one 16-byte vector a lane"}
+        ceil = {"read_only_GBs": round(T1 * H1 * 2 / (ru * 1e-6) / 1e9, 1),
+                "write_only_GBs": round(T1 * H1 * 2 / (wu * 1e-6) / 1e9, 1),
+                "copy_GBs": round(copy_gbs, 1)}
+        if wl.name in PATTERN_OF:
+            p, nv, tpr = PATTERN_OF[wl.name]
+            pus = pattern_us(torch, pat, p, wl.T, wl.H, nv, tpr, dev, K, with_w=True,
+                             with_sm=wl.kind == "smooth_fp8")
+            ceil[f"{wl.name}_pattern"] = {
+                "us": round(pus, 3), "GBs": round(wl.bytes / (pus * 1e-6) / 1e9, 1),
+                "kernel_vs_pattern": round(pus / kernel_us, 4),
+                "what": "compute-free kernel with the operator's loads, stores and launch shape"}
+        out["ceilings"] = ceil
+    if not args.no_cpu and wl.seeded:
+        out["cpu_baseline"] = cpu_baseline(wl, cpu, min(wl.T, 1024), args.cpu_seconds,
+                                           m["first"])
+        out["cpu_torch"] = cpu_torch(wl, cpu, min(wl.T, 512), min(args.cpu_seconds, 10.0))
+    if not args.no_configs and wl.name == "cfg3":
+        cfgs = {"cfg1": cfg1_entry(args)}
+        cfgs["cfg2"] = config_entry(torch, WORKLOADS["cfg2"], args, dev, pat,
+                                    "torch.ops._C.fused_add_rms_norm (in place)")
+        cfgs["cfg4"] = config_entry(torch, WORKLOADS["cfg4"], args, dev, pat,
+                                    "mcoplib.op.rms_norm_dynamic_per_token_quant (SmoothQuant, "
+                                    "fp8-e4m3fn, after_res + after_norm)")
+        cfgs["cfg5_decode"] = decode_entry(torch, args, dev)
+        cfgs["cfg5_large"] = config_entry(torch, WORKLOADS["cfg5-large"], args, dev, pat,
+                                          "mcoplib.op.rms_norm_dynamic_per_token_quant_custom "
+                                          "with residual")
+        out["configs"] = cfgs
     print(json.dumps(out), flush=True)
     return 0
 

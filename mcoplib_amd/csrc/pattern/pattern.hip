@@ -1,0 +1,235 @@
+// pattern.hip -- compute-free kernels with the exact HBM access pattern of the row kernels
+// (measurement only; built into libmcop_pattern.so, not into the operator library).
+//
+// Each kernel issues the same loads and stores as one operator's register-resident row kernel --
+// same lane mapping (rowkern.h: vector v of lane lt at v * tpr + lt), the same vectors per lane
+// and lanes per row, the same non-temporal hints, the same issue order of shared and streamed
+// loads, the output streams stored one after another in the operator's order (a loop over the
+// lane's vectors per stream), the row reductions (and their barriers) between the store phases
+// where the operator has them, per-row scale stores -- but replaces the arithmetic by bitwise
+// combinations of the loaded words (no floating point, no conversions).  Timing one
+// against its operator says how close the operator runs to what its access pattern allows on
+// this GPU; the copy, read-only and write-only kernels give the plain streaming ceilings.
+#include <hip/hip_runtime.h>
+
+#include "../../../include/mcop_pattern.h"
+#include "../rowkern.h"
+
+#include <cstdarg>
+#include <cstdio>
+
+namespace mcop {
+namespace {
+thread_local char g_pat_err[256] = "";
+int pat_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_pat_err, sizeof(g_pat_err), fmt, ap);
+  va_end(ap);
+  return MCOP_PATTERN_E_INVALID;
+}
+}  // namespace
+
+// Which tensors a pattern streams: bf16 inputs x (and r), shared bf16 weight and fp32 smooth
+// vectors, bf16 outputs o0 (and o1), one-byte codes q, one fp32 per row; and whether the shared
+// vectors are requested before the streamed ones at every width (H1, H4) or, as H2/H3 do, only
+// from four vectors a lane on.
+// `order`: the output streams in the order the operator stores them (0 = o0, 1 = o1, 2 = q;
+// -1 ends the list); `reduce`: the row reductions the operator runs after each store phase.
+struct Pat {
+  int nin, nout16;
+  bool q8, w, sm, scale, shared_first;
+  int order[3];
+  int reduce[3];
+};
+constexpr Pat kPat[] = {
+    // ADD_NORM_QUANT: H2/H3 with residual (cfg 3, 5): the residual, the sum-of-squares and
+    // absmax reductions, the codes
+    {2, 1, true, true, false, true, false, {0, 2, -1}, {2, 0, 0}},
+    // FUSED_ADD: H1 in place (cfg 2): the residual (o1), the sum of squares, the normalized x
+    {2, 2, false, true, false, false, true, {1, 0, -1}, {1, 0, 0}},
+    // SMOOTH_QUANT: H4 (cfg 4): after_res, sum of squares, after_norm, absmax, codes
+    {1, 2, true, true, true, true, true, {0, 1, 2}, {1, 1, 0}},
+    {1, 1, false, false, false, false, false, {0, -1, -1}, {0, 0, 0}},  // COPY
+    // READ: the loads feed a per-lane value stored only when it matches a constant (so every
+    // lane must load, and practically nothing is written)
+    {1, 0, false, false, false, false, false, {-1, -1, -1}, {0, 0, 0}},
+    {0, 1, false, false, false, false, false, {0, -1, -1}, {0, 0, 0}},  // WRITE
+};
+
+using u16x8 = Pack<uint16_t, 8>;
+
+template <int P, int NV>
+__global__ void __launch_bounds__(max_tpr(8, NV))
+k_pattern(const uint16_t* __restrict__ x, const uint16_t* __restrict__ r,
+          const uint16_t* __restrict__ w, const float* __restrict__ sm, uint16_t* __restrict__ o0,
+          uint16_t* __restrict__ o1, uint8_t* __restrict__ q, float* __restrict__ scales,
+          int64_t rows, int hidden, int tpr) {
+  constexpr Pat pt = kPat[P];
+  __shared__ float red[16];
+  const RowPos p = row_pos(rows, tpr);
+  const int nvec = hidden / 8;
+  const int64_t base = p.row * (int64_t)hidden, lbase = p.lrow * (int64_t)hidden;
+  u16x8 xv[NV], rv[NV], wv[NV];
+  Pack<float, 8> sv[NV];
+  constexpr bool shared_first = pt.shared_first || NV >= 4;
+  if constexpr (shared_first) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * 8;
+      if constexpr (pt.w) wv[v] = ld<uint16_t, 8>(w + lj);
+      if constexpr (pt.sm) sv[v] = ld<float, 8>(sm + lj);
+    }
+    shared_loads_first();
+  }
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * 8;
+    if constexpr (pt.nin >= 1) xv[v] = ld_nt<uint16_t, 8>(x + lbase + lj);
+    if constexpr (pt.nin >= 2) rv[v] = ld_nt<uint16_t, 8>(r + lbase + lj);
+    if constexpr (!shared_first) {
+      if constexpr (pt.w) wv[v] = ld<uint16_t, 8>(w + lj);
+      if constexpr (pt.sm) sv[v] = ld<float, 8>(sm + lj);
+    }
+  }
+  uint32_t acc = 0;
+  u16x8 a[NV], b[NV];
+  Pack<uint8_t, 8> c[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int j = vec_index(v, tpr, p.lt);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint32_t t = pt.nin >= 1 ? xv[v].v[e] : (uint32_t)(j * 8 + e);
+      if constexpr (pt.nin >= 2) t ^= rv[v].v[e];
+      if constexpr (pt.w) t ^= wv[v].v[e];
+      if constexpr (pt.sm) t ^= __builtin_bit_cast(uint32_t, sv[v].v[e]) >> 9;
+      a[v].v[e] = (uint16_t)t;
+      b[v].v[e] = (uint16_t)(t >> 1);
+      c[v].v[e] = (uint8_t)t;
+      acc ^= t;
+    }
+  }
+  uint32_t mix = 0;  // what the row reductions return: the later phases' stores depend on it
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int stream = pt.order[k];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int j = vec_index(v, tpr, p.lt);
+      if (stream < 0 || !p.live || j >= nvec) continue;
+      const int64_t o = base + (int64_t)j * 8;
+      u16x8 av = a[v], bv = b[v];
+      Pack<uint8_t, 8> cv = c[v];
+      av.v[0] ^= (uint16_t)mix;
+      bv.v[0] ^= (uint16_t)mix;
+      cv.v[0] ^= (uint8_t)mix;
+      if (stream == 0) st_nt<uint16_t, 8>(o0 + o, av);
+      if (stream == 1) st_nt<uint16_t, 8>(o1 + o, bv);
+      if (stream == 2) st_nt<uint8_t, 8>(q + o, cv);
+    }
+#pragma unroll
+    for (int rr = 0; rr < pt.reduce[k]; ++rr) {
+      // the operator's row reduction, on a value of this lane (bits of acc as a float)
+      const float f = row_reduce(__builtin_bit_cast(float, (acc >> (rr + 1)) & 0x3f7fffffu), red,
+                                 tpr, MaxOp());
+      mix ^= __builtin_bit_cast(uint32_t, f);
+      if (tpr > 64) __syncthreads();  // the slots are reused by the next reduction
+    }
+  }
+  if constexpr (pt.scale) {
+    if (p.live && p.lt == 0) scales[p.row] = __builtin_bit_cast(float, acc & 0x3fffffffu);
+  }
+  if constexpr (P == MCOP_PATTERN_READ) {
+    // acc is an xor of 16-bit words: compare with a 16-bit constant (a wider one would let the
+    // compiler prove the test false and drop the loads)
+    if (acc == 0x79b9u) scales[p.row] = 1.0f;
+  }
+}
+
+template <int P>
+static int launch(const Geometry& g, const uint16_t* x, const uint16_t* r, const uint16_t* w,
+                  const float* sm, uint16_t* o0, uint16_t* o1, uint8_t* q, float* s, int64_t rows,
+                  int hidden, unsigned lds, hipStream_t st) {
+  const dim3 grid((unsigned)g.blocks), block((unsigned)(g.tpr * g.rpb));
+#define MCOP_PAT(NVV)                                                                         \
+  hipLaunchKernelGGL((k_pattern<P, NVV>), grid, block, lds, st, x, r, w, sm, o0, o1, q, s, rows, \
+                     hidden, g.tpr)
+  switch (g.nv) {
+    case 1: MCOP_PAT(1); break;
+    case 2: MCOP_PAT(2); break;
+    case 4: MCOP_PAT(4); break;
+    default: MCOP_PAT(8); break;
+  }
+#undef MCOP_PAT
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    pat_error("mcop_pattern: launch failed: %s", hipGetErrorString(e));
+    return MCOP_PATTERN_E_LAUNCH;
+  }
+  return 0;
+}
+
+}  // namespace mcop
+
+extern "C" int mcop_pattern(int pattern, const void* x, const void* r, const void* w,
+                            const float* smooth, void* o0, void* o1, void* q, float* scales,
+                            int64_t rows, int64_t hidden, int vectors_per_lane,
+                            int lanes_per_row, int lds_bytes, void* stream) {
+  using namespace mcop;
+  if (pattern < 0 || pattern > MCOP_PATTERN_WRITE) {
+    return pat_error("mcop_pattern: unknown pattern %d", pattern);
+  }
+  const Pat& pt = kPat[pattern];
+  const int nv = vectors_per_lane, tpr = lanes_per_row;
+  if (rows <= 0 || hidden <= 0 || hidden % 8 != 0 || hidden > INT32_MAX ||
+      !(nv == 1 || nv == 2 || nv == 4 || nv == 8) || tpr <= 0 || tpr % 64 != 0 ||
+      tpr > max_tpr(8, nv) || (int64_t)nv * tpr < hidden / 8 || lds_bytes < 0 ||
+      lds_bytes > 163840) {
+    return pat_error("mcop_pattern: bad shape rows=%lld hidden=%lld nv=%d tpr=%d (hidden a "
+                     "multiple of 8, nv in {1,2,4,8}, tpr a multiple of 64 that holds the row, "
+                     "lds_bytes <= 163840)",
+                     (long long)rows, (long long)hidden, nv, tpr);
+  }
+  // every tensor the pattern touches: present and aligned to its access width
+  const struct { const void* p; int align; } need[8] = {
+      {pt.nin >= 1 ? x : o0, 16}, {pt.nin >= 2 ? r : o0, 16}, {pt.w ? w : o0, 16},
+      {pt.sm ? (const void*)smooth : o0, 16}, {pt.nout16 >= 1 ? o0 : x, 16},
+      {pt.nout16 >= 2 ? o1 : x, 16}, {pt.q8 ? q : x, 8},
+      {pt.scale || pattern == MCOP_PATTERN_READ ? (void*)scales : x, 4}};
+  for (const auto& n : need) {
+    if (n.p == nullptr || reinterpret_cast<uintptr_t>(n.p) % (uintptr_t)n.align != 0) {
+      return pat_error("mcop_pattern: a tensor of the pattern is null or misaligned");
+    }
+  }
+  Geometry g;
+  g.vec = 8;
+  g.nv = nv;
+  g.tpr = tpr;
+  g.rpb = tpr < 256 ? 256 / tpr : 1;
+  g.blocks = (rows + g.rpb - 1) / g.rpb;
+  auto st = static_cast<hipStream_t>(stream);
+  auto* xp = static_cast<const uint16_t*>(x);
+  auto* rp = static_cast<const uint16_t*>(r);
+  auto* wp = static_cast<const uint16_t*>(w);
+  auto* o0p = static_cast<uint16_t*>(o0);
+  auto* o1p = static_cast<uint16_t*>(o1);
+  auto* qp = static_cast<uint8_t*>(q);
+  const int h = (int)hidden;
+  switch (pattern) {
+    case MCOP_PATTERN_ADD_NORM_QUANT:
+      return launch<0>(g, xp, rp, wp, smooth, o0p, o1p, qp, scales, rows, h, (unsigned)lds_bytes, st);
+    case MCOP_PATTERN_FUSED_ADD:
+      return launch<1>(g, xp, rp, wp, smooth, o0p, o1p, qp, scales, rows, h, (unsigned)lds_bytes, st);
+    case MCOP_PATTERN_SMOOTH_QUANT:
+      return launch<2>(g, xp, rp, wp, smooth, o0p, o1p, qp, scales, rows, h, (unsigned)lds_bytes, st);
+    case MCOP_PATTERN_COPY:
+      return launch<3>(g, xp, rp, wp, smooth, o0p, o1p, qp, scales, rows, h, (unsigned)lds_bytes, st);
+    case MCOP_PATTERN_READ:
+      return launch<4>(g, xp, rp, wp, smooth, o0p, o1p, qp, scales, rows, h, (unsigned)lds_bytes, st);
+    default:
+      return launch<5>(g, xp, rp, wp, smooth, o0p, o1p, qp, scales, rows, h, (unsigned)lds_bytes, st);
+  }
+}
+
+extern "C" const char* mcop_pattern_last_error(void) { return mcop::g_pat_err; }

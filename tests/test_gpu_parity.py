@@ -1,10 +1,12 @@
 """GPU parity: the HIP kernels (through the drop-in surfaces and the C ABI) against the CPU oracle
-on the same seeded inputs, at the benchmark configurations (cfg1-cfg5) and at the shapes the reference's own
-test enumerates (unit_test/test_fused_rms_norm_dq.py:13-24)."""
+on the same seeded inputs, at the benchmark configurations (cfg1-cfg5, on the exact inputs
+bench.py times: bench.config_inputs) and at the shapes the reference's own test enumerates
+(unit_test/test_fused_rms_norm_dq.py:13-24)."""
 
 import pytest
 import torch
 
+import bench
 import oracle
 import mcoplib_amd._C  # noqa: F401  (registers torch.ops._C.*)
 from mcoplib_amd import _lib, custom_ops, op
@@ -57,25 +59,26 @@ def test_h2_scale_ub_fp8():
 
 
 def test_config1_norm_int8_no_residual():
-    say("config 1: 256x4096 bf16, no residual, int8")
-    _h2_case(256, 4096, torch.bfloat16, torch.int8, False, 1)
-
-
-def _outlier_x(T, H, seed):
-    g = gen(seed)
-    x = torch.randn(T, H, generator=g)
-    idx = torch.randperm(H, generator=g)[: round(0.01 * H)]
-    x[:, idx] *= 20.0
-    return x.to(torch.bfloat16)
+    say("config 1: 256x4096 bf16, no residual, int8 (the bench's inputs)")
+    c = bench.config_inputs("cfg1")
+    x, w = c["x"], c["w"]
+    q_ref, s_ref, _ = oracle.rms_norm_dynamic_per_token_quant(x, w, c["eps"], torch.int8)
+    q = torch.empty(x.shape, dtype=torch.int8, device=DEV)
+    s = torch.empty(x.shape[0], 1, device=DEV)
+    torch.ops._C.rms_norm_dynamic_per_token_quant(q, x.to(DEV), w.to(DEV), s, c["eps"], None,
+                                                  None)
+    torch.cuda.synchronize()
+    assert_scales(s, s_ref, "cfg1 scales")
+    assert_codes(q, q_ref, "cfg1 codes")
 
 
 def test_config3_add_norm_int8_outliers():
-    """Config 3 (the headline workload): x, residual [8192, 8192] bf16, 1% outlier channels x20, eps 1e-5."""
+    """Config 3 (the headline workload) on the bench's exact inputs: x, residual [8192, 8192]
+    bf16, 1% outlier channels x20, eps 1e-5."""
     T = H = 8192
-    say("config 3: 8192x8192 add + rmsnorm + int8, outliers")
-    x = _outlier_x(T, H, 3)
-    r = randn((T, H), 30, torch.bfloat16)
-    w = weight(H, 31, torch.bfloat16)
+    say("config 3: 8192x8192 add + rmsnorm + int8, outliers (the bench's inputs)")
+    c = bench.config_inputs("cfg3")
+    x, r, w = c["x"], c["r"], c["w"]
     q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant_custom(x, w, 1e-5,
                                                                         residual=r)
     xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
@@ -88,12 +91,10 @@ def test_config3_add_norm_int8_outliers():
 
 
 def test_config2_fused_add_rms_norm():
-    """Config 2: in-place fused_add_rms_norm, [4096, 4096] bf16, eps 1e-6."""
-    T = H = 4096
-    say("config 2: fused_add_rms_norm 4096x4096")
-    x = randn((T, H), 20, torch.bfloat16)
-    r = randn((T, H), 21, torch.bfloat16)
-    w = weight(H, 22, torch.bfloat16)
+    """Config 2: in-place fused_add_rms_norm, [4096, 4096] bf16, eps 1e-6 (the bench's inputs)."""
+    say("config 2: fused_add_rms_norm 4096x4096 (the bench's inputs)")
+    c = bench.config_inputs("cfg2")
+    x, r, w = c["x"], c["r"], c["w"]
     x_ref, r_ref = oracle.fused_add_rms_norm(x, r, w, 1e-6)
     xd, rd, wd = x.to(DEV), r.to(DEV), w.to(DEV)
     torch.ops._C.fused_add_rms_norm(xd, rd, wd, 1e-6)
@@ -180,11 +181,24 @@ def test_h4_shapes(T, H, dtype, wdt, sdt):
 
 
 def test_config4_smooth_quant_fp8():
-    """Config 4: fused_rms_norm_dq to fp8-e4m3fn with SmoothQuant, [16384, 7168] bf16,
-    bf16 weight, fp32 smooth ~U(0.5, 2)."""
-    say("config 4: 16384x7168 smooth quant fp8")
-    _h4_case(16384, 7168, torch.bfloat16, torch.bfloat16, torch.float32, torch.float8_e4m3fn,
-             False, False, 4)
+    """Config 4 on the bench's inputs: fused_rms_norm_dq to fp8-e4m3fn with SmoothQuant,
+    [16384, 7168] bf16, bf16 weight, fp32 smooth ~U(0.5, 2)."""
+    say("config 4: 16384x7168 smooth quant fp8 (the bench's inputs)")
+    c = bench.config_inputs("cfg4")
+    x, w, sm = c["x"], c["w"], c["sm"]
+    q_ref, s_ref, ar_ref, an_ref = oracle.rms_norm_smooth_quant(x, w, sm, c["eps"],
+                                                                torch.float8_e4m3fn)
+    q = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=DEV)
+    s = torch.empty(x.shape[0], device=DEV)
+    ar = torch.empty(x.shape, dtype=torch.bfloat16, device=DEV)
+    an = torch.empty_like(ar)
+    op.rms_norm_dynamic_per_token_quant(q, x.to(DEV), w.to(DEV), sm.to(DEV), s, c["eps"], ar, an,
+                                        None)
+    torch.cuda.synchronize()
+    assert_exact(ar, ar_ref, "cfg4 after_res")
+    assert_exact(an, an_ref, "cfg4 after_norm")
+    assert_scales(s, s_ref, "cfg4 scales")
+    assert_codes(q, q_ref, "cfg4 codes")
 
 
 @pytest.mark.parametrize("dtype,wdt,sdt,qdt,with_res,standard", [
@@ -218,22 +232,31 @@ def test_h4_large_row_counts(T, H, ov):
 
 @pytest.mark.parametrize("T", [1, 4, 16, 64])
 def test_config5_decode(T):
-    say(f"config 5 decode T={T}")
+    say(f"config 5 decode T={T} (the bench's inputs)")
+    c = bench.config_inputs(f"cfg5-decode{T}")
+    q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant_custom(c["x"], c["w"], c["eps"],
+                                                                        residual=c["r"])
+    rd = c["r"].to(DEV)
+    q, s = custom_ops.rms_norm_dynamic_per_token_quant(c["x"].to(DEV), c["w"].to(DEV), c["eps"],
+                                                       torch.int8, residual=rd)
+    torch.cuda.synchronize()
+    assert_exact(rd, r_ref, "cfg5 decode residual")
+    assert_scales(s, s_ref, "cfg5 decode scales")
+    assert_codes(q, q_ref, "cfg5 decode codes")
     _h2_case(T, 5120, torch.bfloat16, torch.int8, True, 500 + T)
 
 
 def test_config5_large_sampled_rows():
-    """Config 5 (bandwidth leg): [32768, 16384] bf16 add + norm + int8.  Inputs are
-    generated on the device; the oracle checks a sample of rows (rows are independent)."""
+    """Config 5 (bandwidth leg): [32768, 16384] bf16 add + norm + int8 on the bench's inputs;
+    the oracle checks a sample of rows (rows are independent)."""
     T, H = 32768, 16384
-    say("config 5 large: 32768x16384")
-    g = torch.Generator(device=DEV).manual_seed(5)
-    xd = torch.randn(T, H, generator=g, device=DEV).to(torch.bfloat16)
-    rd = torch.randn(T, H, generator=g, device=DEV).to(torch.bfloat16)
-    wd = (1 + 0.1 * torch.randn(H, generator=g, device=DEV)).to(torch.bfloat16)
+    say("config 5 large: 32768x16384 (the bench's inputs)")
+    c = bench.config_inputs("cfg5-large")
+    xd, rd, wd = c["x"].to(DEV), c["r"].to(DEV), c["w"].to(DEV)
     rows = torch.cat([torch.arange(0, 64), torch.randperm(T, generator=gen(5))[:448],
                       torch.arange(T - 64, T)]).unique()
-    x_s, r_s = xd[rows.to(DEV)].cpu(), rd[rows.to(DEV)].cpu()
+    x_s, r_s = c["x"][rows], c["r"][rows]
+    del c
     q, s = custom_ops.rms_norm_dynamic_per_token_quant(xd, wd, 1e-6, torch.int8, residual=rd)
     torch.cuda.synchronize()
     q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant_custom(x_s, wd.cpu(), 1e-6,
