@@ -47,30 +47,37 @@ __device__ __forceinline__ Pack<uint8_t, VEC> sq_fp8_codes(const float* v, float
   return z;
 }
 
-// One row (or, for tpr < blockDim, one of the workgroup's rows) given the lane's weight and
-// smooth vectors.
-template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES>
-__device__ __forceinline__ void sq_row(const RowPos& p, const WVec<EW, VEC>* wv,
-                                       const WVec<ES, VEC>* sv, uint8_t* __restrict__ out,
-                                       float* __restrict__ scales,
-                                       const typename E::S* __restrict__ x,
-                                       typename E::S* __restrict__ ares,
-                                       typename E::S* __restrict__ anorm,
-                                       const typename E::S* __restrict__ res, int hidden, int tpr,
-                                       float eps, uint32_t flags, double* red_sum,
-                                       float* red_max) {
+// The lane's streamed vectors of one row: x (and the residual).
+template <class E, int VEC, int NV, bool RES>
+__device__ __forceinline__ void sq_load(const RowPos& p, const typename E::S* __restrict__ x,
+                                        const typename E::S* __restrict__ res, int hidden,
+                                        int tpr, Pack<typename E::S, VEC>* xv,
+                                        Pack<typename E::S, VEC>* rv) {
   using S = typename E::S;
   const int nvec = hidden / VEC;
-  const int64_t base = p.row * (int64_t)hidden;
   const int64_t lbase = p.lrow * (int64_t)hidden;
-
-  Pack<S, VEC> xv[NV], rv[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
     xv[v] = ld_nt<S, VEC>(x + lbase + lj);
     if constexpr (RES) rv[v] = ld_nt<S, VEC>(res + lbase + lj);
   }
+}
+
+// One row (or, for tpr < blockDim, one of the workgroup's rows) given the lane's loaded vectors
+// of the row and its weight and smooth vectors.
+template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES>
+__device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S, VEC>* xv,
+                                       const Pack<typename E::S, VEC>* rv,
+                                       const WVec<EW, VEC>* wv, const WVec<ES, VEC>* sv,
+                                       uint8_t* __restrict__ out, float* __restrict__ scales,
+                                       typename E::S* __restrict__ ares,
+                                       typename E::S* __restrict__ anorm, int hidden, int tpr,
+                                       float eps, uint32_t flags, double* red_sum,
+                                       float* red_max) {
+  using S = typename E::S;
+  const int nvec = hidden / VEC;
+  const int64_t base = p.row * (int64_t)hidden;
 
   float a[NV][VEC];
   double ss = 0.0;
@@ -167,7 +174,9 @@ k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
     sv[v].p = ld<typename ES::S, VEC>(sm + lj);
   }
   shared_loads_first();
-  sq_row<E, EW, ES, VEC, NV, FP8, RES>(p, wv, sv, out, scales, x, ares, anorm, res, hidden, tpr,
+  Pack<typename E::S, VEC> xv[NV], rv[NV];
+  sq_load<E, VEC, NV, RES>(p, x, res, hidden, tpr, xv, rv);
+  sq_row<E, EW, ES, VEC, NV, FP8, RES>(p, xv, rv, wv, sv, out, scales, ares, anorm, hidden, tpr,
                                         eps, flags, red_sum, red_max);
 }
 
