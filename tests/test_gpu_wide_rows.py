@@ -312,3 +312,89 @@ def test_spilling_widths_h2_fp8(dtype):
         assert_codes(q, q_ref, "codes")
         if res is not None:
             assert_exact(rd, r_ref, "residual")
+
+
+# Rows whose maximum sits in different places relative to the multi-pass kernel's on-chip head
+# (with a residual the bf16 head is the first 9 x 1024 vectors, 73728 elements; the tail, re-read
+# from memory each pass, starts there): constant rows, zero and tiny tails, near-equal maxima in
+# one lane or spread over lanes, non-finite values, huge and zero weights.  Bit for bit against
+# the oracle.
+TAIL0 = 73728
+
+
+def _tail_rows(H, seed):
+    g = gen(seed)
+    x = torch.randn(10, H, generator=g)
+    r = torch.randn(10, H, generator=g) * 0.5
+    lane0 = [TAIL0 + 8 * 1024 * k for k in range((H - TAIL0) // 8192)]  # lane 0's tail vectors
+    x[1] = 1.0
+    r[1] = 0.0                                  # a constant row
+    x[2, TAIL0:] = 0.0
+    r[2, TAIL0:] = 0.0                          # a zero tail
+    for k, p in enumerate(lane0[:6]):           # six near-equal maxima in one lane
+        x[3, p] = 30.0 - 0.01 * k
+    for k, p in enumerate((TAIL0 + 8 * 5, TAIL0 + 8 * 1500 + 3, H - 1)):  # near-ties, 3 lanes
+        x[4, p] = 40.0 - 0.15 * k
+    x[5] *= 1e-34                               # tiny values: products below 2^-100
+    r[5] *= 1e-34
+    x[6, TAIL0 + 77] = float("inf")             # a non-finite value in the tail
+    x[7, :TAIL0] *= 5.0                         # the maximum in the head, a small tail
+    x[8, TAIL0:] *= 5.0                         # the maximum in the tail
+    x[9, H - 8:] = 50.0                         # the maximum at the row's end
+    return x.to(torch.bfloat16), r.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("qdt", [torch.int8, torch.float8_e4m3fn])
+def test_wide_tail_maxima_h2(qdt):
+    H = 163840
+    x, r = _tail_rows(H, 40)
+    for wname, w in (("normal", _w(H, 41, torch.bfloat16)),
+                     ("large tail weights", _w(H, 42, torch.float32))):
+        if wname != "normal":
+            w = w.clone()
+            w[TAIL0 + 1000::4099] = 3e30  # a few huge weights among the tail
+            w[TAIL0 + 9::7001] = 0.0
+            w = w.to(torch.bfloat16)
+        say(f"wide tail maxima H2 {qdt} weights: {wname}")
+        q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant(x, w, 1e-6, qdt,
+                                                                      residual=r)
+        q = torch.empty(x.shape, dtype=qdt, device=DEV)
+        s = torch.empty(x.shape[0], 1, device=DEV)
+        rd = r.to(DEV)
+        torch.ops._C.rms_norm_dynamic_per_token_quant(q, x.to(DEV), w.to(DEV), s, 1e-6, None, rd)
+        torch.cuda.synchronize()
+        assert_exact(rd, r_ref, "residual")
+        assert_scales(s, s_ref, "scales")
+        assert_codes(q, q_ref, "codes")
+
+
+def test_wide_tail_maxima_h3_and_no_residual():
+    H = 163840
+    x, r = _tail_rows(H, 43)
+    w = _w(H, 44, torch.bfloat16)
+    say("wide tail maxima H3 (custom op)")
+    q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant_custom(x, w, 1e-6, residual=r)
+    rd = r.to(DEV)
+    q, s = custom_ops.rms_norm_dynamic_per_token_quant(x.to(DEV), w.to(DEV), 1e-6, torch.int8,
+                                                       residual=rd)
+    torch.cuda.synchronize()
+    assert_exact(rd, r_ref, "residual")
+    assert_scales(s, s_ref, "scales")
+    assert_codes(q, q_ref, "codes")
+    # without a residual the bf16 head holds 16 x 1024 vectors: a 262144-wide row has a tail
+    H2 = 262144
+    g = gen(45)
+    xs = torch.randn(4, H2, generator=g)
+    xs[1, 131072 + 5] = 80.0
+    xs[2, 131072:] = 2.0                        # a constant tail
+    xs[3, 131072 + 16::8192] = 33.0             # many equal maxima spread over lanes
+    xs = xs.to(torch.bfloat16)
+    w2 = _w(H2, 46, torch.bfloat16)
+    say("wide tail maxima H2 no residual 262144")
+    q_ref, s_ref, _ = oracle.rms_norm_dynamic_per_token_quant(xs, w2, 1e-6, torch.int8)
+    q = torch.empty(xs.shape, dtype=torch.int8, device=DEV)
+    s = torch.empty(4, 1, device=DEV)
+    torch.ops._C.rms_norm_dynamic_per_token_quant(q, xs.to(DEV), w2.to(DEV), s, 1e-6, None, None)
+    torch.cuda.synchronize()
+    assert_scales(s, s_ref, "scales")
+    assert_codes(q, q_ref, "codes")
