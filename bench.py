@@ -15,7 +15,9 @@ input read once + every output written once) with
   - guard: whether the headline stays at >= 75% of peak with traffic <= 1.01x the algorithmic
     bytes (`regressed` true when not);
   - device_copy / ceilings: a non-temporal streaming copy, read-only and write-only kernels, and
-    compute-free kernels with each timed operator's exact access pattern (libmcop_pattern.so);
+    compute-free kernels with each timed operator's exact access pattern (libmcop_pattern.so),
+    also run over the same elements reshaped to 2048-wide rows (the operator's traffic mix at
+    the fastest streaming shape);
   - cpu_baseline / cpu_torch: the C oracle and a vectorized torch restatement on a row sample of
     the same inputs, on this host's cores, with a bit-for-bit check of the GPU's first call;
   - configs: the other configurations -- cfg1 (CPU only), cfg2, cfg4, cfg5 large (GB/s, fraction
@@ -289,6 +291,7 @@ def kernel_name(wl) -> str:
 PATTERN_OF = {"cfg2": (1, 2, 256), "cfg3": (0, 2, 512), "cfg4": (2, 4, 256),
               "cfg5-large": (0, 4, 512)}
 PATTERN_COPY, PATTERN_READ, PATTERN_WRITE = 3, 4, 5
+MIX_H = 2048  # row width of the reshaped ("mix") pattern: one 16-byte vector a lane, 256 lanes
 
 
 # ------------------------------------------------------------------------------ profiles
@@ -411,6 +414,18 @@ def pattern_us(torch, pat, pattern, T, H, nv, tpr, dev, K, with_w=False, with_sm
     del sets, launches
     torch.cuda.empty_cache()
     return ms * 1e3
+
+
+def mix_us(torch, pat, wl: Workload, dev, K):
+    """us per launch of a configuration's pattern kernel over the same elements reshaped to
+    MIX_H-wide rows, at one vector a lane and 256 lanes (the shape at which the streaming kernels
+    run fastest): the same input and output streams and per-row reductions, with the smallest
+    workgroup footprint.  No row kernel of the configuration's width can have that footprint (a
+    row's reductions need the whole row in one workgroup), so this bounds what any launch shape of
+    a one-pass kernel could reach on the configuration's traffic mix."""
+    p = PATTERN_OF[wl.name][0]
+    return pattern_us(torch, pat, p, wl.T * wl.H // MIX_H, MIX_H, 1, 256, dev, K, with_w=True,
+                      with_sm=wl.kind == "smooth_fp8")
 
 
 # ------------------------------------------------------------------------------ CPU legs
@@ -613,6 +628,9 @@ def config_entry(torch, wl: Workload, args, dev, pat, entry: str):
                          with_sm=wl.kind == "smooth_fp8")
         out["pattern_us"] = round(pus, 3)
         out["kernel_vs_pattern"] = round(pus / us, 4)
+        mus = mix_us(torch, pat, wl, dev, args.steps)
+        out["mix_us"] = round(mus, 3)
+        out["kernel_vs_mix"] = round(mus / us, 4)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(wl, cpu, min(wl.T, 512), args.cpu_seconds / 3,
                                            m["first"])
@@ -771,6 +789,13 @@ def main() -> int:
                 "us": round(pus, 3), "GBs": round(wl.bytes / (pus * 1e-6) / 1e9, 1),
                 "kernel_vs_pattern": round(pus / kernel_us, 4),
                 "what": "compute-free kernel with the operator's loads, stores and launch shape"}
+            mus = mix_us(torch, pat, wl, dev, K)
+            ceil[f"{wl.name}_mix"] = {
+                "us": round(mus, 3), "GBs": round(wl.bytes / (mus * 1e-6) / 1e9, 1),
+                "kernel_vs_mix": round(mus / kernel_us, 4),
+                "what": f"the same compute-free kernel over the same elements reshaped to "
+                        f"{MIX_H}-wide rows (one vector a lane, 256 lanes): the operator's "
+                        f"traffic mix at the fastest streaming shape"}
         out["ceilings"] = ceil
     if not args.no_cpu and wl.seeded:
         out["cpu_baseline"] = cpu_baseline(wl, cpu, min(wl.T, 1024), args.cpu_seconds,

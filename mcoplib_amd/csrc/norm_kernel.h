@@ -157,6 +157,20 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
   ss = row_reduce(ss, red_sum, tpr, SumOp());
   const float rho = mcop_inv_rms(ss, hidden, eps);
   const float inv_rho = mcop_div_rn(1.0f, rho);
+  // The division form: the wave divides in the short form when every lane's elements are in its
+  // domain (every |a| <= sqrt(ss) (1 + 2^-8), rounded or not).
+  bool short_div = false;
+  if (mode != NORM_VLLM && mode != NORM_MC && rms_div) {
+    float amin = __builtin_inff();
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) amin = __builtin_fminf(amin, __builtin_fabsf(a[v][e]));
+    }
+    short_div = __builtin_amdgcn_ballot_w64(!div_domain_ok(amin,
+                                                           __builtin_sqrt(ss) * (1.0 + 0x1p-7),
+                                                           inv_rho, mcop_divisor_ok(rho))) == 0;
+  }
 
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
@@ -174,7 +188,11 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
       for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f((a[v][e] * d) * wv[v].at(e));
     } else {
       float n[VEC];
-      div_by_const<VEC>(n, a[v], rho, inv_rho, mcop_divisor_ok(rho));
+      if (short_div) {
+        div_in_domain<VEC>(n, a[v], rho, inv_rho);
+      } else {
+        div_by_const<VEC>(n, a[v], rho, inv_rho, mcop_divisor_ok(rho));
+      }
 #pragma unroll
       for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(n[e] * wv[v].at(e));
     }

@@ -150,7 +150,8 @@ __device__ __forceinline__ uint8_t q_i8_in_range(float y, float inv) {
   return (uint8_t)__builtin_bit_cast(uint32_t, t + 12582912.0f);
 }
 
-// OCP fp8 e4m3fn codes of N values already clamped to [-448, 448] (v_cvt_pk_fp8_f32: RNE).
+// OCP fp8 e4m3fn codes of N values in [-448 - 2^-15, 448] (v_cvt_pk_fp8_f32: RNE, so a value
+// one ulp beyond -448 codes -448).
 template <int N>
 __device__ __forceinline__ Pack<uint8_t, N> cvt_fp8(const float* c) {
   Pack<uint8_t, N> p;
@@ -196,6 +197,33 @@ __device__ __forceinline__ void div_by_const(float* q, const float* a, float b, 
   }
 }
 
+// Whether every element a lane divides by the row's b > 0 lies in the domain of the 3-operation
+// form of div_by_const (|a| and |a/b| in [2^-100, 2^100], b_ok), from bounds the row already has,
+// so that the per-element tests can be skipped: `amin` <= every |a| of the lane (0 for a lane
+// holding a zero, which then fails: the form would drop the sign of -0), `amax_bound` >= every
+// |a| of the row (non-finite for a row holding NaN or infinity, which then fails).  The computed
+// quotient is within one ulp of a/b and inv = RN(1/b) within half an ulp of 1/b, so the tests
+// below on amin * inv and amax_bound * inv (in binary64, with margins of 2^-20) imply the
+// per-element ones; div_by_const then takes its 3-operation form for every element, so skipping
+// its tests changes no result.
+__device__ __forceinline__ bool div_domain_ok(float amin, double amax_bound, float inv,
+                                              bool b_ok) {
+  const double lo = (double)amin * (double)inv * (1.0 - 0x1p-20);
+  const double hi = amax_bound * (double)inv * (1.0 + 0x1p-20);
+  return b_ok && amin >= 0x1p-100f && lo >= 0x1p-100 && hi <= 0x1p100;
+}
+
+// q[e] = a[e] / b for one vector in the 3-operation form; only for elements div_domain_ok
+// admits (else div_by_const).
+template <int N>
+__device__ __forceinline__ void div_in_domain(float* q, const float* a, float b, float inv) {
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    const float q0 = a[e] * inv;
+    q[e] = __builtin_fmaf(__builtin_fmaf(-q0, b, a[e]), inv, q0);
+  }
+}
+
 // clamp(v, -448, 448) with fmin/fmax semantics (a NaN operand yields the other operand), as
 // the reference's float_to_fp8 does before its conversion.
 __device__ __forceinline__ float clamp_fp8(float v) {
@@ -209,8 +237,10 @@ __device__ __forceinline__ float clamp_fp8(float v) {
 // with |a| >= 2^-100 and |a/b| >= 2^-100 (|q| <= 449: no intermediate overflow or underflow);
 // every other element has |a/b| < 2^-82, the form then yields some |q| < 2^-80, and any such
 // value codes to a zero.  copysign gives that zero a's sign (the correction step turns -0 into
-// +0).  NaN elements stay NaN and clamp to +448 as in the division.  Rows that are not bounded
-// take div_by_const.
+// +0).  In a bounded row every quotient that is not NaN lies within [-448 - u, 448 + u] (u =
+// 2^-15, one ulp of 448), where the clamp to [-448, 448] and the conversion's round-to-nearest
+// give the same code, so only the upper clamp is applied: it sends NaN to +448 as the two-sided
+// clamp does.  Rows that are not bounded take div_by_const and the two-sided clamp.
 template <int N>
 __device__ __forceinline__ Pack<uint8_t, N> fp8_quotient_codes(const float* a, float b, float inv,
                                                                bool b_ok, bool bounded) {
@@ -220,13 +250,13 @@ __device__ __forceinline__ Pack<uint8_t, N> fp8_quotient_codes(const float* a, f
     for (int e = 0; e < N; ++e) {
       const float q0 = a[e] * inv;
       const float r = __builtin_fmaf(-q0, b, a[e]);
-      c[e] = __builtin_copysignf(__builtin_fmaf(r, inv, q0), a[e]);
+      c[e] = __builtin_fminf(__builtin_copysignf(__builtin_fmaf(r, inv, q0), a[e]), 448.0f);
     }
   } else {
     div_by_const<N>(c, a, b, inv, b_ok);
-  }
 #pragma unroll
-  for (int e = 0; e < N; ++e) c[e] = clamp_fp8(c[e]);
+    for (int e = 0; e < N; ++e) c[e] = clamp_fp8(c[e]);
+  }
   return cvt_fp8<N>(c);
 }
 
@@ -275,11 +305,24 @@ __device__ __forceinline__ T reduce16(T v, Op op) {
   return op(v, dpp_mov<kDppMirror>(v));
 }
 
+// The value lane `lane` holds, read into scalar registers (v_readlane_b32: no LDS round trip).
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+__device__ __forceinline__ double lane_value(double v, int lane) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// All-reduce over the wave: after reduce16 every lane of a 16-lane segment holds that
+// segment's value (bit for bit: each step combines the same two operands in both lanes), so the
+// wave's value combines lanes 0, 16, 32 and 48, in that fixed order, and is uniform.
 template <class T, class Op>
 __device__ __forceinline__ T wave_reduce(T v, Op op) {
   v = reduce16(v, op);
-  v = op(v, __shfl_xor(v, 16, 64));
-  return op(v, __shfl_xor(v, 32, 64));
+  return op(op(lane_value(v, 0), lane_value(v, 16)), op(lane_value(v, 32), lane_value(v, 48)));
 }
 
 template <class T, class Op>

@@ -105,6 +105,20 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
   const float inv_rho = mcop_div_rn(1.0f, rho);
   const bool rho_ok = mcop_divisor_ok(rho);
   const bool standard = (flags & MCOP_SQ_STANDARD_NORM) != 0;
+  // The literal form: the wave divides in the short form when every lane's elements are in its
+  // domain (every |b(a)| <= |a| (1 + 2^-8) <= sqrt(ss) (1 + 2^-8)).
+  bool short_div = false;
+  if (!standard) {
+    float amin = __builtin_inff();
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) amin = __builtin_fminf(amin, __builtin_fabsf(a[v][e]));
+    }
+    short_div = __builtin_amdgcn_ballot_w64(!div_domain_ok(amin,
+                                                           __builtin_sqrt(ss) * (1.0 + 0x1p-7),
+                                                           inv_rho, rho_ok)) == 0;
+  }
 
   float amax = 0.0f;
 #pragma unroll
@@ -115,6 +129,8 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
     if (standard) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) n[e] = a[v][e] * rho;
+    } else if (short_div) {
+      div_in_domain<VEC>(n, a[v], rho, inv_rho);
     } else {
       div_by_const<VEC>(n, a[v], rho, inv_rho, rho_ok);
     }

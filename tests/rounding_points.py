@@ -139,6 +139,19 @@ def fp8_quantizer_divides():
     }
 
 
+def fp8_quotient_beyond_448():
+    """The fp8 quotient of a row's absmax element can land one ulp above 448: with
+    A = 1.0234375 (= 131/128, a bf16 value), s = RN(A/448) is below A/448, and RN(A/s) =
+    448 + 2^-15.  Such a quotient codes +-448 (the clamp to [-448, 448], or the conversion's
+    round-to-nearest: the next e4m3 magnitude would be 480, the midpoint 464), never NaN.
+    Two rows: the absmax negative, then positive; the other element 0.5 gives 0.5/s = 218.87,
+    coding 224 (between 208 and 224, above the midpoint 216)."""
+    H = 8
+    x = torch.cat([_bf16([-1.0234375, 0.5], H), _bf16([1.0234375, -0.5], H)])
+    return {"x": x, "quotient": 448.0 + 2.0 ** -15,
+            "values": [[-448.0, 224.0] + [0.0] * (H - 2), [448.0, -224.0] + [0.0] * (H - 2)]}
+
+
 def h4_fp8_divides(u: torch.Tensor):
     """H4's fp8 branch (op/fused_rms_norm_dq.cu:299-301: the scale is passed uninverted to
     ScaledQuant<fp8, false>, which divides): q = e4m3(clamp(v / s)).

@@ -82,6 +82,27 @@ def test_fp8_quantizer_rounding_points_on_gpu():
     assert q.cpu().float().view(-1).tolist() == c["values"]
 
 
+def test_fp8_quotient_beyond_448_on_gpu():
+    """A quotient one ulp beyond +-448 codes +-448 in the bounded short form of the fp8
+    epilogues (the standalone quantizer here); H2's fp8 codes of the same rows against the
+    oracle."""
+    c = rp.fp8_quotient_beyond_448()
+    say("fp8 quotient one ulp beyond 448, 2 x 8 bf16")
+    x = c["x"].to(DEV)
+    q = torch.empty(2, 8, dtype=torch.float8_e4m3fn, device=DEV)
+    s = torch.empty(2, 1, dtype=torch.float32, device=DEV)
+    torch.ops._C.dynamic_per_token_scaled_fp8_quant(q, x, s, None)
+    assert q.cpu().float().tolist() == c["values"]
+    import oracle  # the expected H2 codes of the same rows
+
+    w = torch.ones(8, dtype=torch.bfloat16)
+    q_ref, s_ref, _ = oracle.rms_norm_dynamic_per_token_quant(c["x"], w, 0.0,
+                                                              torch.float8_e4m3fn)
+    torch.ops._C.rms_norm_dynamic_per_token_quant(q, x, w.to(DEV), s, 0.0, None, None)
+    assert torch.equal(s.cpu(), s_ref) and torch.equal(q.cpu().view(torch.uint8),
+                                                       q_ref.view(torch.uint8))
+
+
 def test_h4_fp8_rounding_points_on_gpu():
     import oracle  # only to obtain the row's after_norm, from which the smooth scales are built
 

@@ -7,6 +7,7 @@ lines are cited in the case builders."""
 
 import math
 
+import numpy as np
 import torch
 
 import oracle
@@ -107,6 +108,16 @@ def test_fp8_quantizer_divides_by_the_scale():
     alt = (c["x"].float() * (1.0 / s)).clamp(-448, 448).to(torch.float8_e4m3fn).float()
     assert alt.view(-1).tolist() == c["values_alt"] != c["values"]
     # H2's fp8 stage divides the same way (its quantizer is this one's, applied to y)
+
+
+def test_fp8_quotient_beyond_448():
+    c = rp.fp8_quotient_beyond_448()
+    A = np.float32(1.0234375)
+    s = A / np.float32(448.0)
+    assert s.dtype == np.float32 and float(A / s) == c["quotient"]  # one ulp above 448
+    q, sc = oracle.dynamic_per_token_scaled_fp8_quant(c["x"])
+    assert sc.view(-1).tolist() == [float(s)] * 2
+    assert q.float().tolist() == c["values"]
 
 
 def test_h4_fp8_divides_by_the_scale():
