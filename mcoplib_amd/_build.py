@@ -51,7 +51,7 @@ COMPILE_FLAGS = [
 # Kernels that ask for four waves per SIMD (amdgpu_waves_per_eu(4), i.e. at most 128 VGPRs): each
 # must meet that bound without spilling registers to scratch.  Patterns match demangled names.
 FOUR_WAVE_KERNELS = (
-    r"^void mcop::k_rms_norm_quant<mcop::BF16, 8, 8, false, (true|false), [0-9]>\(",
+    r"^void mcop::k_rms_norm_quant<mcop::BF16, 8, 8, false, (true|false), [0-9], (true|false)>\(",
     r"^void mcop::k_fused_add_rms_norm<mcop::BF16, 8, 8>\(",
 )
 RESOURCES = "resource_usage.json"

@@ -87,7 +87,12 @@ __device__ __forceinline__ Pack<uint8_t, VEC> row_codes(const float* y, float rh
 // 512-lane workgroup per CU, and rows of 20480-32768 bf16 elements ran 14-20% slower.  The fp8
 // forms, and fp16 (whose conversions need more registers), would spill under that bound and keep
 // the default.
-template <class E, int VEC, int NV, bool FP8, bool RES, int MODE>
+// EX (exact): the workgroup holds one row and every lane owns NV vectors of it (tpr ==
+// blockDim.x, NV * tpr == hidden / VEC, one workgroup per row).  The row index is then uniform,
+// so the row's base addresses are scalar and each vector's 32-bit offset serves every tensor,
+// and the bounds tests and the out-of-row handling drop out: a shorter per-row chain (measured
+// 12% less per decode call at T = 1-64 x 5120, about 0.5% at 8192 x 8192).
+template <class E, int VEC, int NV, bool FP8, bool RES, int MODE, bool EX = false>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
 __attribute__((amdgpu_waves_per_eu(NV == 8 && !FP8 && std::is_same<E, BF16>::value ? 4 : 1)))
 k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
@@ -97,28 +102,44 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   using S = typename E::S;
   __shared__ double red_sum[16];
   __shared__ float red_max[16];
-  const RowPos p = row_pos(rows, tpr);
+  RowPos p;
+  if constexpr (EX) {
+    p = row_pos_one();
+  } else {
+    p = row_pos(rows, tpr);
+  }
   const int nvec = hidden / VEC;
   const int64_t base = p.row * (int64_t)hidden;
   const int64_t lbase = p.lrow * (int64_t)hidden;
+  // Element j of a row starting at `row`: in the EX form a uniform row pointer plus a 32-bit
+  // offset (j < hidden, an int); otherwise one 64-bit address per lane.
+  auto at = [](auto* t, int64_t row, int j) {
+    if constexpr (EX) {
+      return (t + row) + (uint32_t)j;
+    } else {
+      return t + row + (int64_t)j;
+    }
+  };
+  auto lj_of = [&](int v) {  // element offset of the lane's vector v (loads)
+    const int j = vec_index(v, tpr, p.lt);
+    return (EX ? j : load_index(j, nvec)) * VEC;
+  };
 
   // All loads first, unconditionally (out-of-row lanes re-read vector 0 of their row).
   Pack<S, VEC> xv[NV], rv[NV], wv[NV];
   if constexpr (NV >= 4) {
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      wv[v] = ld<S, VEC>(w + (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC);
-    }
+    for (int v = 0; v < NV; ++v) wv[v] = ld<S, VEC>(at(w, 0, lj_of(v)));
     shared_loads_first();
   }
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
-    xv[v] = ld_nt<S, VEC>(x + lbase + lj);
-    if constexpr (RES) rv[v] = ld_nt<S, VEC>(res + lbase + lj);
+    const int lj = lj_of(v);
+    xv[v] = ld_nt<S, VEC>(at(x, lbase, lj));
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(at(res, lbase, lj));
     // with fewer vectors per lane the weight loads interleave with the streamed ones (measured
     // 1.5% faster at 8192 x 8192, two vectors per lane; shared-first won at four)
-    if constexpr (NV < 4) wv[v] = ld<S, VEC>(w + lj);
+    if constexpr (NV < 4) wv[v] = ld<S, VEC>(at(w, 0, lj));
   }
 
   float a[NV][VEC];
@@ -126,7 +147,7 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
-    const bool in = j < nvec;
+    const bool in = EX || j < nvec;
     // Lanes past the row end hold a copy of vector 0: it must not count in the sum.
     double vs = 0.0;
 #pragma unroll
@@ -143,18 +164,18 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
         Pack<S, VEC> o;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(a[v][e]);
-        st_nt<S, VEC>(res + base + (int64_t)j * VEC, o);
+        st_nt<S, VEC>(at(res, base, j * VEC), o);
       }
     }
   }
 
-  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  ss = row_reduce<EX>(ss, red_sum, tpr, SumOp());
   const float rho = mcop_inv_rms(ss, hidden, eps);
 
   // The absmax must skip the copies of vector 0 held past the row end: with an in-place
   // residual that copy may read vector 0's residual after its owner stored the sum there.
   // Rows that fill every lane (the common case) skip the test.
-  const bool full = (int64_t)NV * tpr == nvec;
+  const bool full = EX || (int64_t)NV * tpr == nvec;
   float amax = 0.0f;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
@@ -169,7 +190,7 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
       amax = __builtin_fmaxf(amax, in ? __builtin_fabsf(y) : 0.0f);
     }
   }
-  amax = row_reduce(amax, red_max, tpr, MaxOp());
+  amax = row_reduce<EX>(amax, red_max, tpr, MaxOp());
 
   float A;
   const float s = row_scale<FP8, MODE>(amax, rho, scale_ub, &A);
@@ -181,10 +202,10 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
-    if (p.live && j < nvec) {
+    if (p.live && (EX || j < nvec)) {
       const Pack<uint8_t, VEC> q =
           row_codes<E, VEC, FP8, MODE>(a[v], rho, s, inv, s_ok, bounded, scale_ub != nullptr);
-      st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
+      st_nt<uint8_t, VEC>(at(out, base, j * VEC), q);
     }
   }
 }
@@ -352,18 +373,24 @@ static void launch_nv(const Geometry& g, void* out, float* scales, const void* x
   auto* xp = static_cast<const S*>(x);
   auto* wp = static_cast<const S*>(w);
   auto* rp = static_cast<S*>(res);
-#define MCOP_LAUNCH(NVV)                                                                   \
-  hipLaunchKernelGGL((k_rms_norm_quant<E, VEC, NVV, FP8, RES, MODE>), grid, block, 0, st, o, \
+#define MCOP_LAUNCH(NVV, EXX)                                                                  \
+  hipLaunchKernelGGL((k_rms_norm_quant<E, VEC, NVV, FP8, RES, MODE, EXX>), grid, block, 0, st, o, \
                      scales, xp, wp, scale_ub, rp, rows, hidden, g.tpr, eps)
   if constexpr (VEC == 1) {
-    if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
+    if (g.nv == 4) MCOP_LAUNCH(4, false); else MCOP_LAUNCH(16, false);
   } else {
+    // exact rows (one row per workgroup, every lane in it) take the EX form at two vectors a
+    // lane, and at four or eight for at most 256 rows (the latency path): at four and eight it
+    // takes more registers (fewer resident waves) for no gain on bandwidth-bound shapes.  The
+    // 7168 chain's rows never fill their 256 lanes.
+    const bool ex = MODE != QM_MC_7168 && g.rpb == 1 && (int64_t)g.nv * g.tpr == hidden / VEC &&
+                    (g.nv == 2 || rows <= 256);
     switch (g.nv) {
-      case 1: MCOP_LAUNCH(1); break;
-      case 2: MCOP_LAUNCH(2); break;
-      case 4: MCOP_LAUNCH(4); break;
-      case 8: MCOP_LAUNCH(8); break;
-      default: MCOP_LAUNCH(16); break;
+      case 1: MCOP_LAUNCH(1, false); break;
+      case 2: if (ex) MCOP_LAUNCH(2, MODE != QM_MC_7168); else MCOP_LAUNCH(2, false); break;
+      case 4: if (ex) MCOP_LAUNCH(4, MODE != QM_MC_7168); else MCOP_LAUNCH(4, false); break;
+      case 8: if (ex) MCOP_LAUNCH(8, MODE != QM_MC_7168); else MCOP_LAUNCH(8, false); break;
+      default: MCOP_LAUNCH(16, false); break;
     }
   }
 #undef MCOP_LAUNCH

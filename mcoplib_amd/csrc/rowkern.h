@@ -325,9 +325,10 @@ __device__ __forceinline__ T wave_reduce(T v, Op op) {
   return op(op(lane_value(v, 0), lane_value(v, 16)), op(lane_value(v, 32), lane_value(v, 48)));
 }
 
-template <class T, class Op>
+// ONE: the workgroup holds exactly one row (tpr == blockDim.x), so its first wave is wave 0.
+template <bool ONE = false, class T, class Op>
 __device__ __forceinline__ T row_reduce(T v, T* lds, int tpr, Op op) {
-  if (tpr < 64) {  // several rows per wave: all-reduce within each row's aligned lane segment
+  if (!ONE && tpr < 64) {  // several rows per wave: all-reduce within each row's aligned segment
     v = reduce16(v, op);
     if (tpr == 32) v = op(v, __shfl_xor(v, 16, 64));
     return v;
@@ -338,7 +339,7 @@ __device__ __forceinline__ T row_reduce(T v, T* lds, int tpr, Op op) {
   if ((threadIdx.x & 63) == 0) lds[wave] = v;
   __syncthreads();
   const int wpr = tpr >> 6;
-  const int first = (wave / wpr) * wpr;
+  const int first = ONE ? 0 : (wave / wpr) * wpr;
   T t = lds[first];
   for (int i = 1; i < wpr; ++i) t = op(t, lds[first + i]);
   return t;
@@ -381,6 +382,17 @@ __device__ __forceinline__ RowPos row_pos(int64_t num_rows, int tpr) {
   }
   p.live = p.row < num_rows;
   p.lrow = p.live ? p.row : num_rows - 1;
+  return p;
+}
+
+// Position of this thread when its workgroup holds exactly one row (tpr == blockDim.x, the grid
+// one workgroup per row): the row index is uniform, so row base addresses are scalar.
+__device__ __forceinline__ RowPos row_pos_one() {
+  RowPos p;
+  p.row = blockIdx.x;
+  p.lrow = p.row;
+  p.lt = threadIdx.x;
+  p.live = true;
   return p;
 }
 

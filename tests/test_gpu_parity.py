@@ -339,6 +339,38 @@ def test_launch_shape_does_not_change_bits(T):
             assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("T", [1, 64, 256])
+def test_exact_row_forms_match_the_generic_form(T):
+    """Rows that fill their workgroup exactly (one row per workgroup, every lane in it) take the
+    kernel's exact-row form on the latency path (at most 256 rows) at two, four and eight
+    vectors a lane; the generic form (several rows per workgroup, or lanes past the row end) must
+    give the same bits, and both the oracle's."""
+    H = 16384
+    say(f"exact-row forms T={T}")
+    x = randn((T, H), 64, torch.bfloat16)
+    r0 = randn((T, H), 65, torch.bfloat16)
+    w = weight(H, 66, torch.bfloat16)
+    q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant_custom(x, w, 1e-6, residual=r0)
+    xd, wd = x.to(DEV), w.to(DEV)
+    # 2048 vectors a row: (0, 0) = (2, 1024), (4, 512), (8, 256) exact; (8, 512): lanes past the
+    # row end; (16, 128): two rows per workgroup
+    shapes = [(0, 0), (4, 512), (8, 256), (8, 512), (16, 128)]
+    try:
+        for nv, tpr in shapes:
+            _lib.set_launch_override(nv, tpr)
+            rd = r0.to(DEV)
+            q = torch.empty(T, H, dtype=torch.int8, device=DEV)
+            s = torch.empty(T, 1, dtype=torch.float32, device=DEV)
+            op.rms_norm_dynamic_per_token_quant_custom(q, xd, wd, s, 1e-6, None, rd)
+            torch.cuda.synchronize()
+            tag = f"T={T} nv={nv} tpr={tpr}"
+            assert_scales(s, s_ref, tag + " scales")
+            assert_codes(q, q_ref, tag + " codes")
+            assert_exact(rd, r_ref, tag + " residual")
+    finally:
+        _lib.set_launch_override(0, 0)
+
+
 def test_repeatable():
     T, H = 1024, 8192
     x = randn((T, H), 70, torch.bfloat16).to(DEV)
