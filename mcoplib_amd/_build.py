@@ -52,7 +52,7 @@ COMPILE_FLAGS = [
 # must meet that bound without spilling registers to scratch.  Patterns match demangled names.
 FOUR_WAVE_KERNELS = (
     r"^void mcop::k_rms_norm_quant<mcop::BF16, 8, 8, false, (true|false), [0-9], (true|false)>\(",
-    r"^void mcop::k_fused_add_rms_norm<mcop::BF16, 8, 8>\(",
+    r"^void mcop::k_fused_add_rms_norm<mcop::BF16, 8, 8, (true|false)>\(",
 )
 RESOURCES = "resource_usage.json"
 

@@ -22,7 +22,9 @@ namespace mcop {
 // With eight vectors a lane the kernel asks for four waves per SIMD (at most 128 VGPRs, met
 // without spilling; 138 and three waves left free): rows of 20480-24576 bf16 elements ran 5-9%
 // faster.  fp16 would spill under that bound and keeps the default.
-template <class E, int VEC, int NV>
+// EX (exact): one row per workgroup and every lane in the row (tpr == blockDim.x, NV * tpr ==
+// hidden / VEC): uniform row index, scalar base addresses with 32-bit offsets, no bounds tests.
+template <class E, int VEC, int NV, bool EX = false>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
 __attribute__((amdgpu_waves_per_eu(NV == 8 && !std::is_same<E, F16>::value ? 4 : 1)))
 k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
@@ -30,22 +32,37 @@ k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
                      int64_t rows, int hidden, int tpr, float eps) {
   using S = typename E::S;
   __shared__ double red_sum[16];
-  const RowPos p = row_pos(rows, tpr);
+  RowPos p;
+  if constexpr (EX) {
+    p = row_pos_one();
+  } else {
+    p = row_pos(rows, tpr);
+  }
   const int nvec = hidden / VEC;
   const int64_t xbase = p.row * x_stride, xlbase = p.lrow * x_stride;
   const int64_t rbase = p.row * (int64_t)hidden, rlbase = p.lrow * (int64_t)hidden;
+  // element j of a row starting at `row` (EX: a uniform row pointer plus a 32-bit offset)
+  auto at = [](auto* t, int64_t row, int j) {
+    if constexpr (EX) {
+      return (t + row) + (uint32_t)j;
+    } else {
+      return t + row + (int64_t)j;
+    }
+  };
+  auto lj_of = [&](int v) {
+    const int j = vec_index(v, tpr, p.lt);
+    return (EX ? j : load_index(j, nvec)) * VEC;
+  };
 
   Pack<S, VEC> xv[NV], rv[NV], wv[NV];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    wv[v] = ld<S, VEC>(w + (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC);
-  }
+  for (int v = 0; v < NV; ++v) wv[v] = ld<S, VEC>(at(w, 0, lj_of(v)));
   shared_loads_first();
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
-    xv[v] = ld_nt<S, VEC>(x + xlbase + lj);
-    rv[v] = ld_nt<S, VEC>(res + rlbase + lj);
+    const int lj = lj_of(v);
+    xv[v] = ld_nt<S, VEC>(at(x, xlbase, lj));
+    rv[v] = ld_nt<S, VEC>(at(res, rlbase, lj));
   }
 
   float z[NV][VEC];
@@ -53,7 +70,7 @@ k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
-    const bool in = j < nvec;
+    const bool in = EX || j < nvec;
     Pack<S, VEC> o;
     double vs = 0.0;  // lanes past the row end (a copy of vector 0) do not count
 #pragma unroll
@@ -65,22 +82,22 @@ k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
       vs = __builtin_fma(d, d, vs);
     }
     ss += in ? vs : 0.0;
-    if (p.live && in) st_nt<S, VEC>(res + rbase + (int64_t)j * VEC, o);
+    if (p.live && in) st_nt<S, VEC>(at(res, rbase, j * VEC), o);
   }
 
-  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  ss = row_reduce<EX>(ss, red_sum, tpr, SumOp());
   const float rho = mcop_inv_rms(ss, hidden, eps);
 
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
-    if (p.live && j < nvec) {
+    if (p.live && (EX || j < nvec)) {
       Pack<S, VEC> o;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         o.v[e] = E::from_f(rnd<E>(z[v][e] * rho) * E::to_f(wv[v].v[e]));
       }
-      st_nt<S, VEC>(x + xbase + (int64_t)j * VEC, o);
+      st_nt<S, VEC>(at(x, xbase, j * VEC), o);
     }
   }
 }
@@ -241,18 +258,22 @@ static void launch_nv(const Geometry& g, void* x, int64_t xs, void* res, const v
   auto* xp = static_cast<S*>(x);
   auto* rp = static_cast<S*>(res);
   auto* wp = static_cast<const S*>(w);
-#define MCOP_LAUNCH(NVV)                                                                    \
-  hipLaunchKernelGGL((k_fused_add_rms_norm<E, VEC, NVV>), grid, block, 0, st, xp, xs, rp, wp, \
+#define MCOP_LAUNCH(NVV, EXX)                                                                   \
+  hipLaunchKernelGGL((k_fused_add_rms_norm<E, VEC, NVV, EXX>), grid, block, 0, st, xp, xs, rp, wp, \
                      rows, hidden, g.tpr, eps)
   if constexpr (VEC == 1) {
-    if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
+    if (g.nv == 4) MCOP_LAUNCH(4, false); else MCOP_LAUNCH(16, false);
   } else {
+    // exact rows (one row per workgroup, every lane in it): the EX form at two vectors a lane,
+    // and at four or eight on the latency path (at most 256 rows)
+    const bool ex = g.rpb == 1 && (int64_t)g.nv * g.tpr == hidden / VEC &&
+                    (g.nv == 2 || rows <= 256);
     switch (g.nv) {
-      case 1: MCOP_LAUNCH(1); break;
-      case 2: MCOP_LAUNCH(2); break;
-      case 4: MCOP_LAUNCH(4); break;
-      case 8: MCOP_LAUNCH(8); break;
-      default: MCOP_LAUNCH(16); break;
+      case 1: MCOP_LAUNCH(1, false); break;
+      case 2: if (ex) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
+      case 4: if (ex) MCOP_LAUNCH(4, true); else MCOP_LAUNCH(4, false); break;
+      case 8: if (ex) MCOP_LAUNCH(8, true); else MCOP_LAUNCH(8, false); break;
+      default: MCOP_LAUNCH(16, false); break;
     }
   }
 #undef MCOP_LAUNCH

@@ -35,7 +35,7 @@ def test_built_kernels_pass_the_resource_check():
     # (both forms of the norm-quant kernel: generic and exact-row)
     for pat in (r"k_rms_norm_quant<mcop::BF16, 8, 2, false, true, 1, ",      # cfg 3 (custom op)
                 r"k_rms_norm_quant<mcop::BF16, 8, 4, false, true, 0, ",      # cfg 5 large
-                r"k_fused_add_rms_norm<mcop::BF16, 8, 2>",                   # cfg 2
+                r"k_fused_add_rms_norm<mcop::BF16, 8, 2, ",                  # cfg 2
                 r"k_rms_norm_smooth_quant<mcop::BF16, mcop::BF16, mcop::F32, 8, 4, true, false>"):
         hits = [r for r in recs if pat in r["kernel"]]
         assert hits and all(r["scratch"] == 0 for r in hits), pat
@@ -43,10 +43,10 @@ def test_built_kernels_pass_the_resource_check():
 
 def test_resource_check_catches_spills():
     b = _build_module()
-    ok_four = {"kernel": "void mcop::k_rms_norm_quant<mcop::BF16, 8, 8, false, true, 1, false>(...)",
-               "mangled": "x", "scratch": 0, "occupancy": 4}
-    ok_h1 = {"kernel": "void mcop::k_fused_add_rms_norm<mcop::BF16, 8, 8>(...)", "mangled": "y",
-             "scratch": 0, "occupancy": 4}
+    ok_four = {"kernel": "void mcop::k_rms_norm_quant<mcop::BF16, 8, 8, false, true, 1, "
+                         "false>(...)", "mangled": "x", "scratch": 0, "occupancy": 4}
+    ok_h1 = {"kernel": "void mcop::k_fused_add_rms_norm<mcop::BF16, 8, 8, false>(...)",
+             "mangled": "y", "scratch": 0, "occupancy": 4}
     assert b.check_resources([ok_four, ok_h1]) == []
     wide = {"kernel": "void mcop::k_rms_norm_quant_wide<mcop::F16, 8, true, false, 0>(...)",
             "mangled": "z", "scratch": 16, "occupancy": 4}
