@@ -158,7 +158,7 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
   const float rho = mcop_inv_rms(ss, hidden, eps);
   const float inv_rho = mcop_div_rn(1.0f, rho);
   // The division form: the wave divides in the short form when every lane's elements are in its
-  // domain (every |a| <= sqrt(ss) (1 + 2^-8), rounded or not).
+  // domain (every a^2 <= ss (1 + 2^-6), rounded or not).
   bool short_div = false;
   if (mode != NORM_VLLM && mode != NORM_MC && rms_div) {
     float amin = __builtin_inff();
@@ -168,7 +168,7 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
       for (int e = 0; e < VEC; ++e) amin = __builtin_fminf(amin, __builtin_fabsf(a[v][e]));
     }
     short_div = __builtin_amdgcn_ballot_w64(!div_domain_ok(amin,
-                                                           __builtin_sqrt(ss) * (1.0 + 0x1p-7),
+                                                           ss * (1.0 + 0x1p-6),
                                                            inv_rho, mcop_divisor_ok(rho))) == 0;
   }
 

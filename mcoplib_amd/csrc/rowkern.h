@@ -200,17 +200,16 @@ __device__ __forceinline__ void div_by_const(float* q, const float* a, float b, 
 // Whether every element a lane divides by the row's b > 0 lies in the domain of the 3-operation
 // form of div_by_const (|a| and |a/b| in [2^-100, 2^100], b_ok), from bounds the row already has,
 // so that the per-element tests can be skipped: `amin` <= every |a| of the lane (0 for a lane
-// holding a zero, which then fails: the form would drop the sign of -0), `amax_bound` >= every
-// |a| of the row (non-finite for a row holding NaN or infinity, which then fails).  The computed
+// holding a zero, which then fails: the form would drop the sign of -0), `amax_sq` >= every
+// a^2 of the row (non-finite for a row holding NaN or infinity, which then fails).  The computed
 // quotient is within one ulp of a/b and inv = RN(1/b) within half an ulp of 1/b, so the tests
-// below on amin * inv and amax_bound * inv (in binary64, with margins of 2^-20) imply the
-// per-element ones; div_by_const then takes its 3-operation form for every element, so skipping
-// its tests changes no result.
-__device__ __forceinline__ bool div_domain_ok(float amin, double amax_bound, float inv,
-                                              bool b_ok) {
+// below on amin * inv and on amax_sq * inv^2 against 2^200 (in binary64, with margins of 2^-20
+// and 2^-17; no square root) imply the per-element ones; div_by_const then takes its
+// 3-operation form for every element, so skipping its tests changes no result.
+__device__ __forceinline__ bool div_domain_ok(float amin, double amax_sq, float inv, bool b_ok) {
   const double lo = (double)amin * (double)inv * (1.0 - 0x1p-20);
-  const double hi = amax_bound * (double)inv * (1.0 + 0x1p-20);
-  return b_ok && amin >= 0x1p-100f && lo >= 0x1p-100 && hi <= 0x1p100;
+  const double hi_sq = amax_sq * ((double)inv * (double)inv) * (1.0 + 0x1p-17);
+  return b_ok && amin >= 0x1p-100f && lo >= 0x1p-100 && hi_sq <= 0x1p200;
 }
 
 // q[e] = a[e] / b for one vector in the 3-operation form; only for elements div_domain_ok

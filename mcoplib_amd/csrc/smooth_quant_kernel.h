@@ -106,7 +106,7 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
   const bool rho_ok = mcop_divisor_ok(rho);
   const bool standard = (flags & MCOP_SQ_STANDARD_NORM) != 0;
   // The literal form: the wave divides in the short form when every lane's elements are in its
-  // domain (every |b(a)| <= |a| (1 + 2^-8) <= sqrt(ss) (1 + 2^-8)).
+  // domain (every b(a)^2 <= a^2 (1 + 2^-8)^2 <= ss (1 + 2^-6)).
   bool short_div = false;
   if (!standard) {
     float amin = __builtin_inff();
@@ -116,7 +116,7 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
       for (int e = 0; e < VEC; ++e) amin = __builtin_fminf(amin, __builtin_fabsf(a[v][e]));
     }
     short_div = __builtin_amdgcn_ballot_w64(!div_domain_ok(amin,
-                                                           __builtin_sqrt(ss) * (1.0 + 0x1p-7),
+                                                           ss * (1.0 + 0x1p-6),
                                                            inv_rho, rho_ok)) == 0;
   }
 
