@@ -382,14 +382,15 @@ static void launch_nv(const Geometry& g, void* out, float* scales, const void* x
     // exact rows (one row per workgroup, every lane in it) take the EX form at two vectors a
     // lane, and at four or eight for at most 256 rows (the latency path): at four and eight it
     // takes more registers (fewer resident waves) for no gain on bandwidth-bound shapes.  The
-    // 7168 chain's rows never fill their 256 lanes.
-    const bool ex = MODE != QM_MC_7168 && g.rpb == 1 && (int64_t)g.nv * g.tpr == hidden / VEC &&
-                    (g.nv == 2 || rows <= 256);
+    // 7168 chain's rows (896 vectors) are exact only at two vectors over 448 lanes.
+    constexpr bool wide_ex = MODE != QM_MC_7168;
+    const bool ex = g.rpb == 1 && (int64_t)g.nv * g.tpr == hidden / VEC &&
+                    (g.nv == 2 || (wide_ex && rows <= 256));
     switch (g.nv) {
       case 1: MCOP_LAUNCH(1, false); break;
-      case 2: if (ex) MCOP_LAUNCH(2, MODE != QM_MC_7168); else MCOP_LAUNCH(2, false); break;
-      case 4: if (ex) MCOP_LAUNCH(4, MODE != QM_MC_7168); else MCOP_LAUNCH(4, false); break;
-      case 8: if (ex) MCOP_LAUNCH(8, MODE != QM_MC_7168); else MCOP_LAUNCH(8, false); break;
+      case 2: if (ex) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
+      case 4: if (ex) MCOP_LAUNCH(4, wide_ex); else MCOP_LAUNCH(4, false); break;
+      case 8: if (ex) MCOP_LAUNCH(8, wide_ex); else MCOP_LAUNCH(8, false); break;
       default: MCOP_LAUNCH(16, false); break;
     }
   }
