@@ -98,7 +98,9 @@ __device__ __forceinline__ Pack<typename E::S, VEC> norm_out(const float* a,
   return o;
 }
 
-template <class E, class EW, int VEC, int NV, bool RES>
+// EX (exact): one row per workgroup and every lane in the row (tpr == blockDim.x, NV * tpr ==
+// hidden / VEC): uniform row index, scalar base addresses with 32-bit offsets, no bounds tests.
+template <class E, class EW, int VEC, int NV, bool RES, bool EX = false>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
 k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
            const typename E::S* __restrict__ x, const typename EW::S* __restrict__ w,
@@ -106,26 +108,42 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
            float eps, int mode, int rms_div) {
   using S = typename E::S;
   __shared__ double red_sum[16];
-  const RowPos p = row_pos(rows, tpr);
+  RowPos p;
+  if constexpr (EX) {
+    p = row_pos_one();
+  } else {
+    p = row_pos(rows, tpr);
+  }
   const int nvec = hidden / VEC;
   const RowOffsets lo = row_offsets(map, p.lrow);
   const int64_t out_base = p.row == p.lrow ? lo.out : 0;
   const int64_t rbase = p.row * (int64_t)hidden;
   const int64_t lrbase = p.lrow * (int64_t)hidden;
+  // element j of a row starting at `row` (EX: a uniform row pointer plus a 32-bit offset)
+  auto at = [](auto* t, int64_t row, int j) {
+    if constexpr (EX) {
+      return (t + row) + (uint32_t)j;
+    } else {
+      return t + row + (int64_t)j;
+    }
+  };
+  auto lj_of = [&](int v) {
+    const int j = vec_index(v, tpr, p.lt);
+    return (EX ? j : load_index(j, nvec)) * VEC;
+  };
 
   Pack<S, VEC> xv[NV], rv[NV];
   NormW<EW, VEC> wv[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    wv[v].p = ld<typename EW::S, VEC>(
-        w + lo.w + (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC);
+    wv[v].p = ld<typename EW::S, VEC>(at(w, lo.w, lj_of(v)));
   }
   shared_loads_first();
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
-    xv[v] = ld_nt<S, VEC>(x + lo.in + lj);
-    if constexpr (RES) rv[v] = ld_nt<S, VEC>(res + lrbase + lj);
+    const int lj = lj_of(v);
+    xv[v] = ld_nt<S, VEC>(at(x, lo.in, lj));
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(at(res, lrbase, lj));
   }
 
   float a[NV][VEC];
@@ -133,7 +151,7 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
-    const bool in = j < nvec;
+    const bool in = EX || j < nvec;
     double vs = 0.0;  // lanes past the row end (a copy of vector 0) do not count
     Pack<S, VEC> o;
 #pragma unroll
@@ -151,10 +169,10 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
     }
     ss += in ? vs : 0.0;
     if constexpr (RES) {
-      if (p.live && in) st_nt<S, VEC>(ares + rbase + (int64_t)j * VEC, o);
+      if (p.live && in) st_nt<S, VEC>(at(ares, rbase, j * VEC), o);
     }
   }
-  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  ss = row_reduce<EX>(ss, red_sum, tpr, SumOp());
   const float rho = mcop_inv_rms(ss, hidden, eps);
   const float inv_rho = mcop_div_rn(1.0f, rho);
   // The division form: the wave divides in the short form when every lane's elements are in its
@@ -175,7 +193,7 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
-    if (!(p.live && j < nvec)) continue;
+    if (!(p.live && (EX || j < nvec))) continue;
     // kept inline (norm_out computes the same): through the helper the compiler issued this
     // kernel's streamed load before the shared weight load
     Pack<S, VEC> o;
@@ -196,7 +214,7 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
 #pragma unroll
       for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(n[e] * wv[v].at(e));
     }
-    st_nt<S, VEC>(out + out_base + (int64_t)j * VEC, o);
+    st_nt<S, VEC>(at(out, out_base, j * VEC), o);
   }
 }
 
@@ -337,18 +355,22 @@ static void norm_launch_nv(const Geometry& g, const NormArgs& a, hipStream_t st)
   auto* xp = static_cast<const S*>(a.x);
   auto* wp = static_cast<const typename EW::S*>(a.w);
   auto* rp = static_cast<const S*>(a.res);
-#define MCOP_LAUNCH(NVV)                                                                       \
-  hipLaunchKernelGGL((k_rms_norm<E, EW, VEC, NVV, RES>), grid, block, 0, st, o, arp, xp, wp, rp, \
-                     a.map, a.rows, a.hidden, g.tpr, a.eps, a.mode, a.rms_div)
+#define MCOP_LAUNCH(NVV, EXX)                                                                  \
+  hipLaunchKernelGGL((k_rms_norm<E, EW, VEC, NVV, RES, EXX>), grid, block, 0, st, o, arp, xp, wp, \
+                     rp, a.map, a.rows, a.hidden, g.tpr, a.eps, a.mode, a.rms_div)
   if constexpr (VEC == 1) {
-    if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
+    if (g.nv == 4) MCOP_LAUNCH(4, false); else MCOP_LAUNCH(16, false);
   } else {
+    // exact rows (one row per workgroup, every lane in it): the EX form at two vectors a lane,
+    // and at four or eight on the latency path (at most 256 rows)
+    const bool ex = g.rpb == 1 && (int64_t)g.nv * g.tpr == a.hidden / VEC &&
+                    (g.nv == 2 || a.rows <= 256);
     switch (g.nv) {
-      case 1: MCOP_LAUNCH(1); break;
-      case 2: MCOP_LAUNCH(2); break;
-      case 4: MCOP_LAUNCH(4); break;
-      case 8: MCOP_LAUNCH(8); break;
-      default: MCOP_LAUNCH(16); break;
+      case 1: MCOP_LAUNCH(1, false); break;
+      case 2: if (ex) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
+      case 4: if (ex) MCOP_LAUNCH(4, true); else MCOP_LAUNCH(4, false); break;
+      case 8: if (ex) MCOP_LAUNCH(8, true); else MCOP_LAUNCH(8, false); break;
+      default: MCOP_LAUNCH(16, false); break;
     }
   }
 #undef MCOP_LAUNCH

@@ -107,7 +107,9 @@ __device__ __forceinline__ void ptq_fold(float t, float& mx, float& nmn) {
   }
 }
 
-template <class E, int VEC, int NV, int MODE>
+// EX (exact): one row per workgroup and every lane in the row (tpr == blockDim.x, NV * tpr ==
+// hidden / VEC): uniform row index, scalar base addresses with 32-bit offsets, no bounds tests.
+template <class E, int VEC, int NV, int MODE, bool EX = false>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
 k_per_token_quant(uint8_t* __restrict__ out, float* __restrict__ scales, int32_t* __restrict__ azp,
                   const typename E::S* __restrict__ x, const float* __restrict__ scale_ub,
@@ -115,16 +117,29 @@ k_per_token_quant(uint8_t* __restrict__ out, float* __restrict__ scales, int32_t
   using S = typename E::S;
   __shared__ float red_a[16];
   __shared__ float red_b[16];
-  const RowPos p = row_pos(rows, tpr);
+  RowPos p;
+  if constexpr (EX) {
+    p = row_pos_one();
+  } else {
+    p = row_pos(rows, tpr);
+  }
   const int nvec = hidden / VEC;
   const int64_t lbase = p.lrow * in_stride;
   const int64_t obase = p.row * out_stride;
+  // element j of a row starting at `row` (EX: a uniform row pointer plus a 32-bit offset)
+  auto at = [](auto* t, int64_t row, int j) {
+    if constexpr (EX) {
+      return (t + row) + (uint32_t)j;
+    } else {
+      return t + row + (int64_t)j;
+    }
+  };
 
   Pack<S, VEC> xv[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
-    xv[v] = ld_nt<S, VEC>(x + lbase + lj);
+    const int j = vec_index(v, tpr, p.lt);
+    xv[v] = ld_nt<S, VEC>(at(x, lbase, (EX ? j : load_index(j, nvec)) * VEC));
   }
   // Lanes past the row end hold a copy of vector 0 (read only: no effect on max or min).
   float a[NV][VEC];
@@ -138,8 +153,8 @@ k_per_token_quant(uint8_t* __restrict__ out, float* __restrict__ scales, int32_t
       ptq_fold<MODE>(a[v][e], mx, nmn);
     }
   }
-  mx = row_reduce(mx, red_a, tpr, MaxOp());
-  if constexpr (MODE == PTQ_INT8_AZP) nmn = row_reduce(nmn, red_b, tpr, MaxOp());
+  mx = row_reduce<EX>(mx, red_a, tpr, MaxOp());
+  if constexpr (MODE == PTQ_INT8_AZP) nmn = row_reduce<EX>(nmn, red_b, tpr, MaxOp());
   const PtqRow r = ptq_row<MODE>(mx, nmn, scale_ub);
   if (p.live && p.lt == 0) {
     scales[p.row] = r.s;
@@ -148,8 +163,8 @@ k_per_token_quant(uint8_t* __restrict__ out, float* __restrict__ scales, int32_t
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
-    if (p.live && j < nvec) {
-      st_nt<uint8_t, VEC>(out + obase + (int64_t)j * VEC, ptq_codes<E, VEC, MODE>(a[v], r));
+    if (p.live && (EX || j < nvec)) {
+      st_nt<uint8_t, VEC>(at(out, obase, j * VEC), ptq_codes<E, VEC, MODE>(a[v], r));
     }
   }
 }
@@ -257,18 +272,22 @@ static void launch_nv(const Geometry& g, const PtqArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)g.blocks), block((unsigned)(g.tpr * g.rpb));
   auto* o = static_cast<uint8_t*>(a.out);
   auto* xp = static_cast<const S*>(a.x);
-#define MCOP_LAUNCH(NVV)                                                                     \
-  hipLaunchKernelGGL((k_per_token_quant<E, VEC, NVV, MODE>), grid, block, 0, st, o, a.scales, \
+#define MCOP_LAUNCH(NVV, EXX)                                                                   \
+  hipLaunchKernelGGL((k_per_token_quant<E, VEC, NVV, MODE, EXX>), grid, block, 0, st, o, a.scales, \
                      a.azp, xp, a.scale_ub, a.rows, a.hidden, a.in_stride, a.out_stride, g.tpr)
   if constexpr (VEC == 1) {
-    if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
+    if (g.nv == 4) MCOP_LAUNCH(4, false); else MCOP_LAUNCH(16, false);
   } else {
+    // exact rows (one row per workgroup, every lane in it): the EX form at two vectors a lane,
+    // and at four or eight on the latency path (at most 256 rows)
+    const bool ex = g.rpb == 1 && (int64_t)g.nv * g.tpr == a.hidden / VEC &&
+                    (g.nv == 2 || a.rows <= 256);
     switch (g.nv) {
-      case 1: MCOP_LAUNCH(1); break;
-      case 2: MCOP_LAUNCH(2); break;
-      case 4: MCOP_LAUNCH(4); break;
-      case 8: MCOP_LAUNCH(8); break;
-      default: MCOP_LAUNCH(16); break;
+      case 1: MCOP_LAUNCH(1, false); break;
+      case 2: if (ex) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
+      case 4: if (ex) MCOP_LAUNCH(4, true); else MCOP_LAUNCH(4, false); break;
+      case 8: if (ex) MCOP_LAUNCH(8, true); else MCOP_LAUNCH(8, false); break;
+      default: MCOP_LAUNCH(16, false); break;
     }
   }
 #undef MCOP_LAUNCH
