@@ -120,16 +120,16 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
   const int64_t rbase = p.row * (int64_t)hidden;
   const int64_t lrbase = p.lrow * (int64_t)hidden;
   // element j of a row starting at `row` (EX: a uniform row pointer plus a 32-bit offset)
-  auto at = [](auto* t, int64_t row, int j) {
+  auto at = [](auto* t, int64_t row, int64_t j) {
     if constexpr (EX) {
       return (t + row) + (uint32_t)j;
     } else {
-      return t + row + (int64_t)j;
+      return t + row + j;
     }
   };
   auto lj_of = [&](int v) {
     const int j = vec_index(v, tpr, p.lt);
-    return (EX ? j : load_index(j, nvec)) * VEC;
+    return (int64_t)(EX ? j : load_index(j, nvec)) * VEC;
   };
 
   Pack<S, VEC> xv[NV], rv[NV];
@@ -141,7 +141,7 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
   shared_loads_first();
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int lj = lj_of(v);
+    const int64_t lj = lj_of(v);
     xv[v] = ld_nt<S, VEC>(at(x, lo.in, lj));
     if constexpr (RES) rv[v] = ld_nt<S, VEC>(at(res, lrbase, lj));
   }
@@ -169,7 +169,7 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
     }
     ss += in ? vs : 0.0;
     if constexpr (RES) {
-      if (p.live && in) st_nt<S, VEC>(at(ares, rbase, j * VEC), o);
+      if (p.live && in) st_nt<S, VEC>(at(ares, rbase, (int64_t)j * VEC), o);
     }
   }
   ss = row_reduce<EX>(ss, red_sum, tpr, SumOp());
@@ -214,7 +214,7 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
 #pragma unroll
       for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(n[e] * wv[v].at(e));
     }
-    st_nt<S, VEC>(at(out, out_base, j * VEC), o);
+    st_nt<S, VEC>(at(out, out_base, (int64_t)j * VEC), o);
   }
 }
 

@@ -113,16 +113,16 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   const int64_t lbase = p.lrow * (int64_t)hidden;
   // Element j of a row starting at `row`: in the EX form a uniform row pointer plus a 32-bit
   // offset (j < hidden, an int); otherwise one 64-bit address per lane.
-  auto at = [](auto* t, int64_t row, int j) {
+  auto at = [](auto* t, int64_t row, int64_t j) {
     if constexpr (EX) {
       return (t + row) + (uint32_t)j;
     } else {
-      return t + row + (int64_t)j;
+      return t + row + j;
     }
   };
   auto lj_of = [&](int v) {  // element offset of the lane's vector v (loads)
     const int j = vec_index(v, tpr, p.lt);
-    return (EX ? j : load_index(j, nvec)) * VEC;
+    return (int64_t)(EX ? j : load_index(j, nvec)) * VEC;
   };
 
   // All loads first, unconditionally (out-of-row lanes re-read vector 0 of their row).
@@ -134,7 +134,7 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   }
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int lj = lj_of(v);
+    const int64_t lj = lj_of(v);
     xv[v] = ld_nt<S, VEC>(at(x, lbase, lj));
     if constexpr (RES) rv[v] = ld_nt<S, VEC>(at(res, lbase, lj));
     // with fewer vectors per lane the weight loads interleave with the streamed ones (measured
@@ -164,7 +164,7 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
         Pack<S, VEC> o;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(a[v][e]);
-        st_nt<S, VEC>(at(res, base, j * VEC), o);
+        st_nt<S, VEC>(at(res, base, (int64_t)j * VEC), o);
       }
     }
   }
@@ -205,7 +205,7 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
     if (p.live && (EX || j < nvec)) {
       const Pack<uint8_t, VEC> q =
           row_codes<E, VEC, FP8, MODE>(a[v], rho, s, inv, s_ok, bounded, scale_ub != nullptr);
-      st_nt<uint8_t, VEC>(at(out, base, j * VEC), q);
+      st_nt<uint8_t, VEC>(at(out, base, (int64_t)j * VEC), q);
     }
   }
 }

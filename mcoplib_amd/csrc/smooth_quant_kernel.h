@@ -48,7 +48,18 @@ __device__ __forceinline__ Pack<uint8_t, VEC> sq_fp8_codes(const float* v, float
 }
 
 // The lane's streamed vectors of one row: x (and the residual).
-template <class E, int VEC, int NV, bool RES>
+// Element j of a row starting at `row`: in the EX form (one row per workgroup, every lane in
+// the row) a uniform row pointer plus a 32-bit offset; otherwise one 64-bit address per lane.
+template <bool EX, class T>
+__device__ __forceinline__ T* sq_at(T* t, int64_t row, int64_t j) {
+  if constexpr (EX) {
+    return (t + row) + (uint32_t)j;
+  } else {
+    return t + row + j;
+  }
+}
+
+template <class E, int VEC, int NV, bool RES, bool EX>
 __device__ __forceinline__ void sq_load(const RowPos& p, const typename E::S* __restrict__ x,
                                         const typename E::S* __restrict__ res, int hidden,
                                         int tpr, Pack<typename E::S, VEC>* xv,
@@ -58,15 +69,16 @@ __device__ __forceinline__ void sq_load(const RowPos& p, const typename E::S* __
   const int64_t lbase = p.lrow * (int64_t)hidden;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
-    xv[v] = ld_nt<S, VEC>(x + lbase + lj);
-    if constexpr (RES) rv[v] = ld_nt<S, VEC>(res + lbase + lj);
+    const int j = vec_index(v, tpr, p.lt);
+    const int64_t lj = (int64_t)(EX ? j : load_index(j, nvec)) * VEC;
+    xv[v] = ld_nt<S, VEC>(sq_at<EX>(x, lbase, lj));
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(sq_at<EX>(res, lbase, lj));
   }
 }
 
 // One row (or, for tpr < blockDim, one of the workgroup's rows) given the lane's loaded vectors
 // of the row and its weight and smooth vectors.
-template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES>
+template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES, bool EX>
 __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S, VEC>* xv,
                                        const Pack<typename E::S, VEC>* rv,
                                        const WVec<EW, VEC>* wv, const WVec<ES, VEC>* sv,
@@ -84,7 +96,7 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
-    const bool in = j < nvec;
+    const bool in = EX || j < nvec;
     Pack<S, VEC> o;
     double vs = 0.0;  // lanes past the row end (a copy of vector 0) do not count
 #pragma unroll
@@ -97,10 +109,10 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
       a[v][e] = E::to_f(o.v[e]);  // b(a): what the later passes of the reference re-read
     }
     ss += in ? vs : 0.0;
-    if (ares != nullptr && p.live && in) st_nt<S, VEC>(ares + base + (int64_t)j * VEC, o);
+    if (ares != nullptr && p.live && in) st_nt<S, VEC>(sq_at<EX>(ares, base, (int64_t)j * VEC), o);
   }
 
-  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  ss = row_reduce<EX>(ss, red_sum, tpr, SumOp());
   const float rho = mcop_inv_rms(ss, hidden, eps);
   const float inv_rho = mcop_div_rn(1.0f, rho);
   const bool rho_ok = mcop_divisor_ok(rho);
@@ -142,9 +154,11 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
       a[v][e] = vv;
       amax = __builtin_fmaxf(amax, __builtin_fabsf(vv));
     }
-    if (anorm != nullptr && p.live && j < nvec) st_nt<S, VEC>(anorm + base + (int64_t)j * VEC, o);
+    if (anorm != nullptr && p.live && (EX || j < nvec)) {
+      st_nt<S, VEC>(sq_at<EX>(anorm, base, (int64_t)j * VEC), o);
+    }
   }
-  amax = row_reduce(amax, red_max, tpr, MaxOp());
+  amax = row_reduce<EX>(amax, red_max, tpr, MaxOp());
 
   const float s = mcop_div_rn(amax, FP8 ? 448.0f : 127.0f);
   if (p.live && p.lt == 0) scales[p.row] = s;
@@ -155,7 +169,7 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
-    if (p.live && j < nvec) {
+    if (p.live && (EX || j < nvec)) {
       Pack<uint8_t, VEC> q;
       if constexpr (FP8) {
         q = sq_fp8_codes<VEC>(a[v], amax, s, inv, s_ok, bounded);
@@ -163,14 +177,16 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
 #pragma unroll
         for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-127>(a[v][e] * inv);
       }
-      st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
+      st_nt<uint8_t, VEC>(sq_at<EX>(out, base, (int64_t)j * VEC), q);
     }
   }
 }
 
 // The weight and smooth vectors (L2-resident, shared by every row) are requested before the
 // row's own streamed loads.
-template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES>
+// EX (exact): one row per workgroup and every lane in the row (tpr == blockDim.x, NV * tpr ==
+// hidden / VEC): uniform row index, scalar base addresses with 32-bit offsets, no bounds tests.
+template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES, bool EX = false>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
 k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
                         const typename E::S* __restrict__ x, const typename EW::S* __restrict__ w,
@@ -182,18 +198,24 @@ k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   const int nvec = hidden / VEC;
   WVec<EW, VEC> wv[NV];
   WVec<ES, VEC> sv[NV];
-  const RowPos p = row_pos(rows, tpr);
+  RowPos p;
+  if constexpr (EX) {
+    p = row_pos_one();
+  } else {
+    p = row_pos(rows, tpr);
+  }
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
-    wv[v].p = ld<typename EW::S, VEC>(w + lj);
-    sv[v].p = ld<typename ES::S, VEC>(sm + lj);
+    const int j = vec_index(v, tpr, p.lt);
+    const int64_t lj = (int64_t)(EX ? j : load_index(j, nvec)) * VEC;
+    wv[v].p = ld<typename EW::S, VEC>(sq_at<EX>(w, 0, lj));
+    sv[v].p = ld<typename ES::S, VEC>(sq_at<EX>(sm, 0, lj));
   }
   shared_loads_first();
   Pack<typename E::S, VEC> xv[NV], rv[NV];
-  sq_load<E, VEC, NV, RES>(p, x, res, hidden, tpr, xv, rv);
-  sq_row<E, EW, ES, VEC, NV, FP8, RES>(p, xv, rv, wv, sv, out, scales, ares, anorm, hidden, tpr,
-                                        eps, flags, red_sum, red_max);
+  sq_load<E, VEC, NV, RES, EX>(p, x, res, hidden, tpr, xv, rv);
+  sq_row<E, EW, ES, VEC, NV, FP8, RES, EX>(p, xv, rv, wv, sv, out, scales, ares, anorm, hidden,
+                                            tpr, eps, flags, red_sum, red_max);
 }
 
 // Rows too wide for the registers: one 1024-lane workgroup per row and three passes over it --
@@ -400,19 +422,23 @@ static void launch_nv(const Geometry& g, const Args& a, hipStream_t st) {
   auto* arp = static_cast<S*>(a.ares);
   auto* anp = static_cast<S*>(a.anorm);
   auto* rp = static_cast<const S*>(a.res);
-#define MCOP_LAUNCH(NVV)                                                                        \
-  hipLaunchKernelGGL((k_rms_norm_smooth_quant<E, EW, ES, VEC, NVV, FP8, RES>), grid,      \
+#define MCOP_LAUNCH(NVV, EXX)                                                                   \
+  hipLaunchKernelGGL((k_rms_norm_smooth_quant<E, EW, ES, VEC, NVV, FP8, RES, EXX>), grid,      \
                      block, 0, st, o, a.scales, xp, wp, sp, arp, anp, rp, a.rows, a.hidden,      \
                      g.tpr, a.eps, a.flags)
   if constexpr (VEC == 1) {
-    if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
+    if (g.nv == 4) MCOP_LAUNCH(4, false); else MCOP_LAUNCH(16, false);
   } else {
+    // exact rows (one row per workgroup, every lane in it) on the latency path (at most 256
+    // rows) take the EX form; bandwidth-bound shapes keep the generic one (a uniform-row form
+    // measured slower at cfg 4's width)
+    const bool ex = g.rpb == 1 && (int64_t)g.nv * g.tpr == a.hidden / VEC && a.rows <= 256;
     switch (g.nv) {
-      case 1: MCOP_LAUNCH(1); break;
-      case 2: MCOP_LAUNCH(2); break;
-      case 4: MCOP_LAUNCH(4); break;
-      case 8: MCOP_LAUNCH(8); break;
-      default: MCOP_LAUNCH(16); break;
+      case 1: MCOP_LAUNCH(1, false); break;
+      case 2: if (ex) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
+      case 4: if (ex) MCOP_LAUNCH(4, true); else MCOP_LAUNCH(4, false); break;
+      case 8: if (ex) MCOP_LAUNCH(8, true); else MCOP_LAUNCH(8, false); break;
+      default: MCOP_LAUNCH(16, false); break;
     }
   }
 #undef MCOP_LAUNCH

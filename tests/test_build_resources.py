@@ -36,7 +36,7 @@ def test_built_kernels_pass_the_resource_check():
     for pat in (r"k_rms_norm_quant<mcop::BF16, 8, 2, false, true, 1, ",      # cfg 3 (custom op)
                 r"k_rms_norm_quant<mcop::BF16, 8, 4, false, true, 0, ",      # cfg 5 large
                 r"k_fused_add_rms_norm<mcop::BF16, 8, 2, ",                  # cfg 2
-                r"k_rms_norm_smooth_quant<mcop::BF16, mcop::BF16, mcop::F32, 8, 4, true, false>"):
+                r"k_rms_norm_smooth_quant<mcop::BF16, mcop::BF16, mcop::F32, 8, 4, true, false, "):
         hits = [r for r in recs if pat in r["kernel"]]
         assert hits and all(r["scratch"] == 0 for r in hits), pat
 
