@@ -41,14 +41,6 @@ k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
   const int nvec = hidden / VEC;
   const int64_t xbase = p.row * x_stride, xlbase = p.lrow * x_stride;
   const int64_t rbase = p.row * (int64_t)hidden, rlbase = p.lrow * (int64_t)hidden;
-  // element j of a row starting at `row` (EX: a uniform row pointer plus a 32-bit offset)
-  auto at = [](auto* t, int64_t row, int64_t j) {
-    if constexpr (EX) {
-      return (t + row) + (uint32_t)j;
-    } else {
-      return t + row + j;
-    }
-  };
   auto lj_of = [&](int v) {
     const int j = vec_index(v, tpr, p.lt);
     return (int64_t)(EX ? j : load_index(j, nvec)) * VEC;
@@ -56,13 +48,13 @@ k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
 
   Pack<S, VEC> xv[NV], rv[NV], wv[NV];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) wv[v] = ld<S, VEC>(at(w, 0, lj_of(v)));
+  for (int v = 0; v < NV; ++v) wv[v] = ld<S, VEC>(row_elem<EX>(w, 0, lj_of(v)));
   shared_loads_first();
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int64_t lj = lj_of(v);
-    xv[v] = ld_nt<S, VEC>(at(x, xlbase, lj));
-    rv[v] = ld_nt<S, VEC>(at(res, rlbase, lj));
+    xv[v] = ld_nt<S, VEC>(row_elem<EX>(x, xlbase, lj));
+    rv[v] = ld_nt<S, VEC>(row_elem<EX>(res, rlbase, lj));
   }
 
   float z[NV][VEC];
@@ -82,7 +74,7 @@ k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
       vs = __builtin_fma(d, d, vs);
     }
     ss += in ? vs : 0.0;
-    if (p.live && in) st_nt<S, VEC>(at(res, rbase, (int64_t)j * VEC), o);
+    if (p.live && in) st_nt<S, VEC>(row_elem<EX>(res, rbase, (int64_t)j * VEC), o);
   }
 
   ss = row_reduce<EX>(ss, red_sum, tpr, SumOp());
@@ -97,7 +89,7 @@ k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
       for (int e = 0; e < VEC; ++e) {
         o.v[e] = E::from_f(rnd<E>(z[v][e] * rho) * E::to_f(wv[v].v[e]));
       }
-      st_nt<S, VEC>(at(x, xbase, (int64_t)j * VEC), o);
+      st_nt<S, VEC>(row_elem<EX>(x, xbase, (int64_t)j * VEC), o);
     }
   }
 }

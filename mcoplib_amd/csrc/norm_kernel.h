@@ -119,14 +119,6 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
   const int64_t out_base = p.row == p.lrow ? lo.out : 0;
   const int64_t rbase = p.row * (int64_t)hidden;
   const int64_t lrbase = p.lrow * (int64_t)hidden;
-  // element j of a row starting at `row` (EX: a uniform row pointer plus a 32-bit offset)
-  auto at = [](auto* t, int64_t row, int64_t j) {
-    if constexpr (EX) {
-      return (t + row) + (uint32_t)j;
-    } else {
-      return t + row + j;
-    }
-  };
   auto lj_of = [&](int v) {
     const int j = vec_index(v, tpr, p.lt);
     return (int64_t)(EX ? j : load_index(j, nvec)) * VEC;
@@ -136,14 +128,14 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
   NormW<EW, VEC> wv[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    wv[v].p = ld<typename EW::S, VEC>(at(w, lo.w, lj_of(v)));
+    wv[v].p = ld<typename EW::S, VEC>(row_elem<EX>(w, lo.w, lj_of(v)));
   }
   shared_loads_first();
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int64_t lj = lj_of(v);
-    xv[v] = ld_nt<S, VEC>(at(x, lo.in, lj));
-    if constexpr (RES) rv[v] = ld_nt<S, VEC>(at(res, lrbase, lj));
+    xv[v] = ld_nt<S, VEC>(row_elem<EX>(x, lo.in, lj));
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(row_elem<EX>(res, lrbase, lj));
   }
 
   float a[NV][VEC];
@@ -169,7 +161,7 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
     }
     ss += in ? vs : 0.0;
     if constexpr (RES) {
-      if (p.live && in) st_nt<S, VEC>(at(ares, rbase, (int64_t)j * VEC), o);
+      if (p.live && in) st_nt<S, VEC>(row_elem<EX>(ares, rbase, (int64_t)j * VEC), o);
     }
   }
   ss = row_reduce<EX>(ss, red_sum, tpr, SumOp());
@@ -214,7 +206,7 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
 #pragma unroll
       for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(n[e] * wv[v].at(e));
     }
-    st_nt<S, VEC>(at(out, out_base, (int64_t)j * VEC), o);
+    st_nt<S, VEC>(row_elem<EX>(out, out_base, (int64_t)j * VEC), o);
   }
 }
 

@@ -126,20 +126,12 @@ k_per_token_quant(uint8_t* __restrict__ out, float* __restrict__ scales, int32_t
   const int nvec = hidden / VEC;
   const int64_t lbase = p.lrow * in_stride;
   const int64_t obase = p.row * out_stride;
-  // element j of a row starting at `row` (EX: a uniform row pointer plus a 32-bit offset)
-  auto at = [](auto* t, int64_t row, int64_t j) {
-    if constexpr (EX) {
-      return (t + row) + (uint32_t)j;
-    } else {
-      return t + row + j;
-    }
-  };
 
   Pack<S, VEC> xv[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
-    xv[v] = ld_nt<S, VEC>(at(x, lbase, (int64_t)(EX ? j : load_index(j, nvec)) * VEC));
+    xv[v] = ld_nt<S, VEC>(row_elem<EX>(x, lbase, (int64_t)(EX ? j : load_index(j, nvec)) * VEC));
   }
   // Lanes past the row end hold a copy of vector 0 (read only: no effect on max or min).
   float a[NV][VEC];
@@ -164,7 +156,7 @@ k_per_token_quant(uint8_t* __restrict__ out, float* __restrict__ scales, int32_t
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
     if (p.live && (EX || j < nvec)) {
-      st_nt<uint8_t, VEC>(at(out, obase, (int64_t)j * VEC), ptq_codes<E, VEC, MODE>(a[v], r));
+      st_nt<uint8_t, VEC>(row_elem<EX>(out, obase, (int64_t)j * VEC), ptq_codes<E, VEC, MODE>(a[v], r));
     }
   }
 }

@@ -111,15 +111,6 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   const int nvec = hidden / VEC;
   const int64_t base = p.row * (int64_t)hidden;
   const int64_t lbase = p.lrow * (int64_t)hidden;
-  // Element j of a row starting at `row`: in the EX form a uniform row pointer plus a 32-bit
-  // offset (j < hidden, an int); otherwise one 64-bit address per lane.
-  auto at = [](auto* t, int64_t row, int64_t j) {
-    if constexpr (EX) {
-      return (t + row) + (uint32_t)j;
-    } else {
-      return t + row + j;
-    }
-  };
   auto lj_of = [&](int v) {  // element offset of the lane's vector v (loads)
     const int j = vec_index(v, tpr, p.lt);
     return (int64_t)(EX ? j : load_index(j, nvec)) * VEC;
@@ -129,17 +120,17 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   Pack<S, VEC> xv[NV], rv[NV], wv[NV];
   if constexpr (NV >= 4) {
 #pragma unroll
-    for (int v = 0; v < NV; ++v) wv[v] = ld<S, VEC>(at(w, 0, lj_of(v)));
+    for (int v = 0; v < NV; ++v) wv[v] = ld<S, VEC>(row_elem<EX>(w, 0, lj_of(v)));
     shared_loads_first();
   }
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int64_t lj = lj_of(v);
-    xv[v] = ld_nt<S, VEC>(at(x, lbase, lj));
-    if constexpr (RES) rv[v] = ld_nt<S, VEC>(at(res, lbase, lj));
+    xv[v] = ld_nt<S, VEC>(row_elem<EX>(x, lbase, lj));
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(row_elem<EX>(res, lbase, lj));
     // with fewer vectors per lane the weight loads interleave with the streamed ones (measured
     // 1.5% faster at 8192 x 8192, two vectors per lane; shared-first won at four)
-    if constexpr (NV < 4) wv[v] = ld<S, VEC>(at(w, 0, lj));
+    if constexpr (NV < 4) wv[v] = ld<S, VEC>(row_elem<EX>(w, 0, lj));
   }
 
   float a[NV][VEC];
@@ -164,7 +155,7 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
         Pack<S, VEC> o;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(a[v][e]);
-        st_nt<S, VEC>(at(res, base, (int64_t)j * VEC), o);
+        st_nt<S, VEC>(row_elem<EX>(res, base, (int64_t)j * VEC), o);
       }
     }
   }
@@ -205,7 +196,7 @@ k_rms_norm_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
     if (p.live && (EX || j < nvec)) {
       const Pack<uint8_t, VEC> q =
           row_codes<E, VEC, FP8, MODE>(a[v], rho, s, inv, s_ok, bounded, scale_ub != nullptr);
-      st_nt<uint8_t, VEC>(at(out, base, (int64_t)j * VEC), q);
+      st_nt<uint8_t, VEC>(row_elem<EX>(out, base, (int64_t)j * VEC), q);
     }
   }
 }

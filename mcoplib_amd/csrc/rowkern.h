@@ -395,6 +395,19 @@ __device__ __forceinline__ RowPos row_pos_one() {
   return p;
 }
 
+// Element j of a row that starts at element `row` of tensor t.  In the exact-row form of a kernel
+// (EX: the workgroup holds one row, so `row` is uniform) a row pointer plus a 32-bit offset (j <
+// hidden, an int), which keeps the row base in scalar registers and lets one offset serve every
+// tensor; otherwise one 64-bit address per lane, as the generic form has always computed it.
+template <bool EX, class T>
+__device__ __forceinline__ T* row_elem(T* t, int64_t row, int64_t j) {
+  if constexpr (EX) {
+    return (t + row) + (uint32_t)j;
+  } else {
+    return t + row + j;
+  }
+}
+
 // Position of the k-th of R rows that each lane handles: workgroup b covers R runs of rpb
 // adjacent rows (run k = rows [(b*R + k) * rpb, +rpb)), so each load instruction of a wave reads
 // rows that sit next to each other.  row_pos_of(n, tpr, 0, 1) == row_pos(n, tpr).

@@ -48,17 +48,6 @@ __device__ __forceinline__ Pack<uint8_t, VEC> sq_fp8_codes(const float* v, float
 }
 
 // The lane's streamed vectors of one row: x (and the residual).
-// Element j of a row starting at `row`: in the EX form (one row per workgroup, every lane in
-// the row) a uniform row pointer plus a 32-bit offset; otherwise one 64-bit address per lane.
-template <bool EX, class T>
-__device__ __forceinline__ T* sq_at(T* t, int64_t row, int64_t j) {
-  if constexpr (EX) {
-    return (t + row) + (uint32_t)j;
-  } else {
-    return t + row + j;
-  }
-}
-
 template <class E, int VEC, int NV, bool RES, bool EX>
 __device__ __forceinline__ void sq_load(const RowPos& p, const typename E::S* __restrict__ x,
                                         const typename E::S* __restrict__ res, int hidden,
@@ -71,8 +60,8 @@ __device__ __forceinline__ void sq_load(const RowPos& p, const typename E::S* __
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
     const int64_t lj = (int64_t)(EX ? j : load_index(j, nvec)) * VEC;
-    xv[v] = ld_nt<S, VEC>(sq_at<EX>(x, lbase, lj));
-    if constexpr (RES) rv[v] = ld_nt<S, VEC>(sq_at<EX>(res, lbase, lj));
+    xv[v] = ld_nt<S, VEC>(row_elem<EX>(x, lbase, lj));
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(row_elem<EX>(res, lbase, lj));
   }
 }
 
@@ -109,7 +98,7 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
       a[v][e] = E::to_f(o.v[e]);  // b(a): what the later passes of the reference re-read
     }
     ss += in ? vs : 0.0;
-    if (ares != nullptr && p.live && in) st_nt<S, VEC>(sq_at<EX>(ares, base, (int64_t)j * VEC), o);
+    if (ares != nullptr && p.live && in) st_nt<S, VEC>(row_elem<EX>(ares, base, (int64_t)j * VEC), o);
   }
 
   ss = row_reduce<EX>(ss, red_sum, tpr, SumOp());
@@ -155,7 +144,7 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
       amax = __builtin_fmaxf(amax, __builtin_fabsf(vv));
     }
     if (anorm != nullptr && p.live && (EX || j < nvec)) {
-      st_nt<S, VEC>(sq_at<EX>(anorm, base, (int64_t)j * VEC), o);
+      st_nt<S, VEC>(row_elem<EX>(anorm, base, (int64_t)j * VEC), o);
     }
   }
   amax = row_reduce<EX>(amax, red_max, tpr, MaxOp());
@@ -177,7 +166,7 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
 #pragma unroll
         for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-127>(a[v][e] * inv);
       }
-      st_nt<uint8_t, VEC>(sq_at<EX>(out, base, (int64_t)j * VEC), q);
+      st_nt<uint8_t, VEC>(row_elem<EX>(out, base, (int64_t)j * VEC), q);
     }
   }
 }
@@ -208,8 +197,8 @@ k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
     const int64_t lj = (int64_t)(EX ? j : load_index(j, nvec)) * VEC;
-    wv[v].p = ld<typename EW::S, VEC>(sq_at<EX>(w, 0, lj));
-    sv[v].p = ld<typename ES::S, VEC>(sq_at<EX>(sm, 0, lj));
+    wv[v].p = ld<typename EW::S, VEC>(row_elem<EX>(w, 0, lj));
+    sv[v].p = ld<typename ES::S, VEC>(row_elem<EX>(sm, 0, lj));
   }
   shared_loads_first();
   Pack<typename E::S, VEC> xv[NV], rv[NV];
