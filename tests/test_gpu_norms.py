@@ -122,6 +122,20 @@ def _vllm_case(x_dev, w, tag):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_vllm_rms_norm_exact_row_layouts(dtype):
+    """Rows that fill their workgroup exactly (4096-wide, at most 256 of them) take the kernel's
+    exact-row form: 2-D row-strided and 3-D views of a fused buffer."""
+    say(f"vllm rms_norm exact-row layouts {dtype}")
+    g = _gen(6)
+    H = 4096
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(dtype)
+    wide = (torch.randn(64, 3 * H, generator=g)).to(dtype).to(DEV)
+    _vllm_case(wide[:, H:2 * H], w, "2-D strided rows")
+    qkv = torch.randn(16, 3 * 8 * H, generator=g).to(dtype).to(DEV)
+    _vllm_case(qkv[:, : 8 * H].view(16, 8, H), w, "3-D q view of qkv")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_vllm_rms_norm_layouts(dtype):
     say(f"vllm rms_norm layouts {dtype}")
     g = _gen(5)

@@ -119,11 +119,12 @@ def test_h1_shapes(T, H, dtype):
     assert_exact(xd, x_ref, "output")
 
 
+@pytest.mark.parametrize("T,H", [(128, 2048), (64, 4096)])
 @pytest.mark.parametrize("pad", [64, 3])
-def test_h1_row_strided_input(pad):
-    """vLLM passes `input` as a row-strided view (input.stride(-2) != hidden_size)."""
-    T, H = 128, 2048
-    say(f"h1 strided pad={pad}")
+def test_h1_row_strided_input(pad, T, H):
+    """vLLM passes `input` as a row-strided view (input.stride(-2) != hidden_size); 64 x 4096
+    takes the kernel's exact-row form (one row per workgroup, every lane in the row)."""
+    say(f"h1 strided pad={pad} T={T} H={H}")
     big = randn((T, H + pad), 40, torch.bfloat16)
     x = big[:, :H]
     r = randn((T, H), 41, torch.bfloat16)

@@ -116,6 +116,27 @@ def test_fp8_row_strided_output():
     assert int(big[:, H:].view(torch.uint8).count_nonzero()) == 0, "wrote past the row"
 
 
+@pytest.mark.parametrize("pad", [64, 8])
+def test_exact_rows_with_strided_views(pad):
+    """64 x 4096 rows take the exact-row form (one row per workgroup, every lane in the row):
+    row-strided input and output views, fp8 and int8 with and without azp."""
+    T, H = 64, 4096
+    say(f"exact-row quantizers, strided views pad={pad}")
+    base = randn((T, H + pad), 27 + pad, torch.bfloat16, scale=2.0).to(DEV)
+    view = base[:, pad:pad + H]
+    q_ref, s_ref = oracle.dynamic_per_token_scaled_fp8_quant(view.cpu())
+    big = torch.zeros((T, H + 128), dtype=torch.float8_e4m3fn, device=DEV)
+    q = big[:, :H]
+    s = torch.empty((T, 1), dtype=torch.float32, device=DEV)
+    torch.ops._C.dynamic_per_token_scaled_fp8_quant(q, view, s, None)
+    torch.cuda.synchronize()
+    assert_scales(s, s_ref, "fp8 scales")
+    assert_codes(q, q_ref, "fp8 codes")
+    assert int(big[:, H:].view(torch.uint8).count_nonzero()) == 0, "wrote past the row"
+    for use_azp in (False, True):
+        _int8_case(view.cpu(), use_azp, f"int8 azp={use_azp}")
+
+
 def test_misaligned_views_take_the_scalar_path():
     say("misaligned views")
     base = randn((65 * 1001 + 1,), 31, torch.bfloat16)
