@@ -66,7 +66,9 @@ __device__ __forceinline__ Pack<uint8_t, VEC> group_codes(const float* y, float 
   return q;
 }
 
-template <class E, int VEC, int NV, bool FP8, bool RES>
+// EX (exact): one row per workgroup and every lane in the row (tpr == blockDim.x, NV * tpr ==
+// hidden / VEC): uniform row index, scalar base addresses with 32-bit offsets, no bounds tests.
+template <class E, int VEC, int NV, bool FP8, bool RES, bool EX = false>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
 k_rms_norm_group_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
                        const typename E::S* __restrict__ x, const typename E::S* __restrict__ w,
@@ -76,21 +78,27 @@ k_rms_norm_group_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   using S = typename E::S;
   constexpr bool BLOCKED = VEC == 1;
   __shared__ double red_sum[16];
-  const RowPos p = row_pos(rows, tpr);
+  RowPos p;
+  if constexpr (EX) {
+    p = row_pos_one();
+  } else {
+    p = row_pos(rows, tpr);
+  }
   const int nvec = hidden / VEC;
   const int64_t base = p.row * (int64_t)hidden;
   const int64_t lbase = p.lrow * (int64_t)hidden;
   auto index = [&](int v) { return BLOCKED ? p.lt * NV + v : vec_index(v, tpr, p.lt); };
+  auto lj_of = [&](int v) { return (int64_t)(EX ? index(v) : load_index(index(v), nvec)) * VEC; };
 
   Pack<S, VEC> xv[NV], rv[NV], wv[NV];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) wv[v] = ld<S, VEC>(w + (int64_t)load_index(index(v), nvec) * VEC);
+  for (int v = 0; v < NV; ++v) wv[v] = ld<S, VEC>(row_elem<EX>(w, 0, lj_of(v)));
   shared_loads_first();
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int64_t lj = (int64_t)load_index(index(v), nvec) * VEC;
-    xv[v] = ld_nt<S, VEC>(x + lbase + lj);
-    if constexpr (RES) rv[v] = ld_nt<S, VEC>(res + lbase + lj);
+    const int64_t lj = lj_of(v);
+    xv[v] = ld_nt<S, VEC>(row_elem<EX>(x, lbase, lj));
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(row_elem<EX>(res, lbase, lj));
   }
 
   float a[NV][VEC];
@@ -98,7 +106,7 @@ k_rms_norm_group_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int j = index(v);
-    const bool in = j < nvec;
+    const bool in = EX || j < nvec;
     double vs = 0.0;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
@@ -114,11 +122,11 @@ k_rms_norm_group_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
         Pack<S, VEC> o;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(a[v][e]);
-        st_nt<S, VEC>(res + base + (int64_t)j * VEC, o);
+        st_nt<S, VEC>(row_elem<EX>(res, base, (int64_t)j * VEC), o);
       }
     }
   }
-  ss = row_reduce(ss, red_sum, tpr, SumOp());
+  ss = row_reduce<EX>(ss, red_sum, tpr, SumOp());
   const float rho = mcop_inv_rms(ss, hidden, eps);
 
   // Groups are whole (hidden % group == 0), so a group's lanes are all inside the row or all
@@ -150,7 +158,7 @@ k_rms_norm_group_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int j = index(v);
-    if (!(p.live && j < nvec)) continue;
+    if (!(p.live && (EX || j < nvec))) continue;
     // kept inline (group_codes computes the same): the helper's order (codes before the scale
     // store) measured 1.4% slower here
     const float A = scale_ub != nullptr ? __builtin_fminf(m[v], ub) : m[v];
@@ -173,7 +181,7 @@ k_rms_norm_group_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 #pragma unroll
       for (int e = 0; e < VEC; ++e) q.v[e] = q_i8_in_range(a[v][e], inv);
     }
-    st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
+    st_nt<uint8_t, VEC>(row_elem<EX>(out, base, (int64_t)j * VEC), q);
   }
 }
 
@@ -360,19 +368,22 @@ static void launch_nv(const Geometry& g, const GqArgs& a, hipStream_t st) {
   auto* xp = static_cast<const S*>(a.x);
   auto* wp = static_cast<const S*>(a.w);
   auto* rp = static_cast<S*>(a.res);
-#define MCOP_LAUNCH(NVV)                                                                        \
-  hipLaunchKernelGGL((k_rms_norm_group_quant<E, VEC, NVV, FP8, RES>), grid, block, 0, st, o,    \
+#define MCOP_LAUNCH(NVV, EXX)                                                                   \
+  hipLaunchKernelGGL((k_rms_norm_group_quant<E, VEC, NVV, FP8, RES, EXX>), grid, block, 0, st, o, \
                      a.scales, xp, wp, a.scale_ub, rp, a.rows, a.hidden, g.tpr, a.eps, a.group, \
                      a.srow, a.sgrp)
   if constexpr (VEC == 1) {
-    if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
+    if (g.nv == 4) MCOP_LAUNCH(4, false); else MCOP_LAUNCH(16, false);
   } else {
+    // exact rows (one row per workgroup, every lane in it) on the latency path (at most 256
+    // rows) take the EX form
+    const bool ex = g.rpb == 1 && (int64_t)g.nv * g.tpr == a.hidden / VEC && a.rows <= 256;
     switch (g.nv) {
-      case 1: MCOP_LAUNCH(1); break;
-      case 2: MCOP_LAUNCH(2); break;
-      case 4: MCOP_LAUNCH(4); break;
-      case 8: MCOP_LAUNCH(8); break;
-      default: MCOP_LAUNCH(16); break;
+      case 1: MCOP_LAUNCH(1, false); break;
+      case 2: if (ex) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
+      case 4: if (ex) MCOP_LAUNCH(4, true); else MCOP_LAUNCH(4, false); break;
+      case 8: if (ex) MCOP_LAUNCH(8, true); else MCOP_LAUNCH(8, false); break;
+      default: MCOP_LAUNCH(16, false); break;
     }
   }
 #undef MCOP_LAUNCH

@@ -27,7 +27,9 @@
 
 namespace mcop {
 
-template <int VEC, int NV, bool OPT>
+// EX (exact): one row per workgroup and every lane in the row (tpr == blockDim.x, NV * tpr ==
+// hidden / VEC): uniform row index, scalar base addresses with 32-bit offsets, no bounds tests.
+template <int VEC, int NV, bool OPT, bool EX = false>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
 k_add_rms_norm_quant_padded(uint8_t* __restrict__ padded, uint16_t* __restrict__ rms,
                             uint8_t* __restrict__ q_out, float* __restrict__ scales,
@@ -37,34 +39,41 @@ k_add_rms_norm_quant_padded(uint8_t* __restrict__ padded, uint16_t* __restrict__
   using E = BF16;
   __shared__ double red_sum[16];
   __shared__ float red_max[16];
-  const RowPos p = row_pos(rows, tpr);
+  RowPos p;
+  if constexpr (EX) {
+    p = row_pos_one();
+  } else {
+    p = row_pos(rows, tpr);
+  }
   const int nvec = hidden / VEC;
   const int64_t base = p.row * (int64_t)hidden;
   const int64_t lbase = p.lrow * (int64_t)hidden;
   const int64_t pbase = p.row * pad_bytes;
+  auto lj_of = [&](int v) {
+    const int j = vec_index(v, tpr, p.lt);
+    return (int64_t)(EX ? j : load_index(j, nvec)) * VEC;
+  };
 
   Pack<uint16_t, VEC> xv[NV], rv[NV], wv[NV];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    wv[v] = ld<uint16_t, VEC>(w + (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC);
-  }
+  for (int v = 0; v < NV; ++v) wv[v] = ld<uint16_t, VEC>(row_elem<EX>(w, 0, lj_of(v)));
   shared_loads_first();
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * VEC;
-    xv[v] = ld_nt<uint16_t, VEC>(x + lbase + lj);
-    rv[v] = ld_nt<uint16_t, VEC>(res + lbase + lj);
+    const int64_t lj = lj_of(v);
+    xv[v] = ld_nt<uint16_t, VEC>(row_elem<EX>(x, lbase, lj));
+    rv[v] = ld_nt<uint16_t, VEC>(row_elem<EX>(res, lbase, lj));
   }
 
   // a: opt keeps p = a * w (fp32); generic keeps b(a) (the residual value it re-reads)
-  const bool full = (int64_t)NV * tpr == nvec;
+  const bool full = EX || (int64_t)NV * tpr == nvec;
   float a[NV][VEC];
   double ss = 0.0;
   float amax = 0.0f;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
-    const bool in = j < nvec;
+    const bool in = EX || j < nvec;
     double vs = 0.0;
     Pack<uint16_t, VEC> o;
 #pragma unroll
@@ -86,10 +95,10 @@ k_add_rms_norm_quant_padded(uint8_t* __restrict__ padded, uint16_t* __restrict__
       amax = __builtin_fmaxf(amax, (full || in) ? __builtin_fabsf(m) : 0.0f);
     }
     ss += in ? vs : 0.0;
-    if (p.live && in) st_nt<uint16_t, VEC>(res + base + (int64_t)j * VEC, o);
+    if (p.live && in) st_nt<uint16_t, VEC>(row_elem<EX>(res, base, (int64_t)j * VEC), o);
   }
-  ss = row_reduce(ss, red_sum, tpr, SumOp());
-  amax = row_reduce(amax, red_max, tpr, MaxOp());
+  ss = row_reduce<EX>(ss, red_sum, tpr, SumOp());
+  amax = row_reduce<EX>(amax, red_max, tpr, MaxOp());
   const float rho = mcop_inv_rms(ss, hidden, eps);
   const float s = __builtin_fmaxf(mcop_div_rn(amax * rho, 127.0f), FLT_EPSILON);
   const float inv = mcop_div_rn(1.0f, s);
@@ -108,7 +117,7 @@ k_add_rms_norm_quant_padded(uint8_t* __restrict__ padded, uint16_t* __restrict__
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int j = vec_index(v, tpr, p.lt);
-    if (p.live && j < nvec) {
+    if (p.live && (EX || j < nvec)) {
       Pack<uint16_t, VEC> o;
       Pack<uint8_t, VEC> q;
 #pragma unroll
@@ -123,9 +132,9 @@ k_add_rms_norm_quant_padded(uint8_t* __restrict__ padded, uint16_t* __restrict__
         }
         q.v[e] = q_i8<-127>(y * inv);
       }
-      st_nt<uint16_t, VEC>(rms + base + (int64_t)j * VEC, o);
-      st_nt<uint8_t, VEC>(q_out + base + (int64_t)j * VEC, q);
-      st_nt<uint8_t, VEC>(padded + pbase + (int64_t)j * VEC, q);
+      st_nt<uint16_t, VEC>(row_elem<EX>(rms, base, (int64_t)j * VEC), o);
+      st_nt<uint8_t, VEC>(row_elem<EX>(q_out, base, (int64_t)j * VEC), q);
+      st_nt<uint8_t, VEC>(row_elem<EX>(padded, pbase, (int64_t)j * VEC), q);
     }
   }
 }
@@ -262,19 +271,22 @@ struct PadArgs {
 template <int VEC, bool OPT>
 static void launch_nv(const Geometry& g, const PadArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)g.blocks), block((unsigned)(g.tpr * g.rpb));
-#define MCOP_LAUNCH(NVV)                                                                       \
-  hipLaunchKernelGGL((k_add_rms_norm_quant_padded<VEC, NVV, OPT>), grid, block, 0, st,          \
+#define MCOP_LAUNCH(NVV, EXX)                                                                  \
+  hipLaunchKernelGGL((k_add_rms_norm_quant_padded<VEC, NVV, OPT, EXX>), grid, block, 0, st,     \
                      a.padded, a.rms, a.q, a.scales, a.x, a.res, a.w, a.rows, a.hidden,       \
                      a.pad_bytes, g.tpr, a.eps)
   if constexpr (VEC == 1) {
-    if (g.nv == 4) MCOP_LAUNCH(4); else MCOP_LAUNCH(16);
+    if (g.nv == 4) MCOP_LAUNCH(4, false); else MCOP_LAUNCH(16, false);
   } else {
+    // exact rows (one row per workgroup, every lane in it) on the latency path (at most 256
+    // rows) take the EX form
+    const bool ex = g.rpb == 1 && (int64_t)g.nv * g.tpr == a.hidden / VEC && a.rows <= 256;
     switch (g.nv) {
-      case 1: MCOP_LAUNCH(1); break;
-      case 2: MCOP_LAUNCH(2); break;
-      case 4: MCOP_LAUNCH(4); break;
-      case 8: MCOP_LAUNCH(8); break;
-      default: MCOP_LAUNCH(16); break;
+      case 1: MCOP_LAUNCH(1, false); break;
+      case 2: if (ex) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
+      case 4: if (ex) MCOP_LAUNCH(4, true); else MCOP_LAUNCH(4, false); break;
+      case 8: if (ex) MCOP_LAUNCH(8, true); else MCOP_LAUNCH(8, false); break;
+      default: MCOP_LAUNCH(16, false); break;
     }
   }
 #undef MCOP_LAUNCH
