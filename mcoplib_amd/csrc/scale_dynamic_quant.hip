@@ -102,26 +102,28 @@ k_scale_dynamic_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales
 #pragma unroll
     for (int e = 0; e < VEC; ++e) v[e] = BF16::to_f(xv.v[e]) * sv.v[e];
   };
+  // Head slots past the row end hold a copy of the row's vector 0 (which leaves the absmax
+  // unchanged), so every load is unconditional: loads under a per-lane branch each wait for
+  // completion where the branch rejoins, which serializes their latencies.
   Pack<uint16_t, VEC> xc[NC];
 #pragma unroll
   for (int c = 0; c < NC + NL; ++c) {
-    const int j = c * tpr + tid;
-    if (j < nvec) {
-      const Pack<uint16_t, VEC> xv = ld<uint16_t, VEC>(x + base + (int64_t)j * VEC);
-      if (c < NC) xc[c] = xv; else lds[c - NC][tid] = xv;
-    }
+    const int64_t o = (int64_t)load_index(c * tpr + tid, nvec) * VEC;
+    const Pack<uint16_t, VEC> xv = ld<uint16_t, VEC>(x + base + o);
+    if (c < NC) xc[c] = xv; else lds[c - NC][tid] = xv;
   }
   auto head = [&](int c) -> Pack<uint16_t, VEC> { return c < NC ? xc[c] : lds[c - NC][tid]; };
+  // The lane index, opaque to the compiler per pass: each pass recomputes its vectors' offsets
+  // instead of holding 16 address pairs from the loads above.
+  int lt = tid;
+  __asm__ volatile("" : "+v"(lt));
   float amax = 0.0f;
 #pragma unroll
   for (int c = 0; c < NC + NL; ++c) {
-    const int j = c * tpr + tid;
-    if (j < nvec) {
-      float v[VEC];
-      v_from(head(c), (int64_t)j * VEC, v);
+    float v[VEC];
+    v_from(head(c), (int64_t)load_index(c * tpr + lt, nvec) * VEC, v);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[e]));
-    }
+    for (int e = 0; e < VEC; ++e) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[e]));
   }
   const int tail0 = (NC + NL) * tpr + tid;
   for (int j = tail0; j < nvec; j += tpr) {
@@ -133,21 +135,27 @@ k_scale_dynamic_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales
   amax = row_reduce(amax, red_max, tpr, MaxOp());
   if (threadIdx.x == 0) scales[blockIdx.x] = amax * 0.00787401574803f;
   const float inv = amax > 0.0f ? mcop_div_rn(127.0f, amax) : 0.0f;
-  auto emit = [&](const Pack<uint16_t, VEC>& xv, int64_t o) {
+  auto emit = [&](const Pack<uint16_t, VEC>& xv, int64_t o, bool in) {
     float v[VEC];
     v_from(xv, o, v);
     Pack<uint8_t, VEC> q;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(v[e] * inv);
-    st<uint8_t, VEC>(out + base + o, q);
+    if (in) st<uint8_t, VEC>(out + base + o, q);
   };
+  __asm__ volatile("" : "+v"(lt));
+  if ((NC + NL) * tpr <= nvec) {  // the head is whole: no store needs a lane test
 #pragma unroll
-  for (int c = 0; c < NC + NL; ++c) {
-    const int j = c * tpr + tid;
-    if (j < nvec) emit(head(c), (int64_t)j * VEC);
+    for (int c = 0; c < NC + NL; ++c) emit(head(c), (int64_t)(c * tpr + lt) * VEC, true);
+  } else {
+#pragma unroll
+    for (int c = 0; c < NC + NL; ++c) {
+      const int j = c * tpr + lt;
+      emit(head(c), (int64_t)load_index(j, nvec) * VEC, j < nvec);
+    }
   }
   for (int j = tail0; j < nvec; j += tpr) {
-    emit(ld<uint16_t, VEC>(x + base + (int64_t)j * VEC), (int64_t)j * VEC);
+    emit(ld<uint16_t, VEC>(x + base + (int64_t)j * VEC), (int64_t)j * VEC, true);
   }
 }
 
