@@ -181,25 +181,25 @@ k_per_token_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
   const int tpr = (int)blockDim.x, tid = (int)threadIdx.x;
   const S* xr = x + (int64_t)blockIdx.x * in_stride;
   uint8_t* orow = out + (int64_t)blockIdx.x * out_stride;
+  // A head slot past the row end holds a copy of the row's vector 0 (which leaves the max and
+  // min unchanged; nothing is stored from it), so every load is unconditional: loads under a
+  // per-lane branch each wait for completion where the branch rejoins, which serializes their
+  // latencies.
+  auto hoff = [&](int c, int lt) { return (int64_t)load_index(c * tpr + lt, nvec) * VEC; };
   Pack<S, VEC> xc[NC];
 #pragma unroll
   for (int c = 0; c < NC + NL; ++c) {
-    const int j = c * tpr + tid;
-    if (j < nvec) {
-      const Pack<S, VEC> xv = ld<S, VEC>(xr + (int64_t)j * VEC);
-      if (c < NC) xc[c] = xv; else lds[c - NC][tid] = xv;
-    }
+    const Pack<S, VEC> xv = ld<S, VEC>(xr + hoff(c, tid));
+    if (c < NC) xc[c] = xv; else lds[c - NC][tid] = xv;
   }
   auto head = [&](int c) -> Pack<S, VEC> { return c < NC ? xc[c] : lds[c - NC][tid]; };
   float mx = MODE == PTQ_INT8_AZP ? -__builtin_inff() : 0.0f;
   float nmn = -__builtin_inff();
 #pragma unroll
   for (int c = 0; c < NC + NL; ++c) {
-    if (c * tpr + tid < nvec) {
-      const Pack<S, VEC> xv = head(c);
+    const Pack<S, VEC> xv = head(c);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) ptq_fold<MODE>(E::to_f(xv.v[e]), mx, nmn);
-    }
+    for (int e = 0; e < VEC; ++e) ptq_fold<MODE>(E::to_f(xv.v[e]), mx, nmn);
   }
   const int tail0 = (NC + NL) * tpr + tid;
   for (int j = tail0; j < nvec; j += tpr) {
@@ -214,19 +214,26 @@ k_per_token_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
     scales[blockIdx.x] = r.s;
     if constexpr (MODE == PTQ_INT8_AZP) azp[blockIdx.x] = r.zp;
   }
-  auto emit = [&](const Pack<S, VEC>& xv, int64_t o) {
+  auto emit = [&](const Pack<S, VEC>& xv, int64_t o, bool in) {
     float a[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) a[e] = E::to_f(xv.v[e]);
-    st<uint8_t, VEC>(orow + o, ptq_codes<E, VEC, MODE>(a, r));
+    const Pack<uint8_t, VEC> q = ptq_codes<E, VEC, MODE>(a, r);
+    if (in) st<uint8_t, VEC>(orow + o, q);
   };
+  // The lane index, opaque to the compiler: the codes pass recomputes its vectors' offsets
+  // instead of holding them from the loads.
+  int lt = tid;
+  __asm__ volatile("" : "+v"(lt));
+  if ((NC + NL) * tpr <= nvec) {  // the head is whole: no store needs a lane test
 #pragma unroll
-  for (int c = 0; c < NC + NL; ++c) {
-    const int j = c * tpr + tid;
-    if (j < nvec) emit(head(c), (int64_t)j * VEC);
+    for (int c = 0; c < NC + NL; ++c) emit(head(c), (int64_t)(c * tpr + lt) * VEC, true);
+  } else {
+#pragma unroll
+    for (int c = 0; c < NC + NL; ++c) emit(head(c), hoff(c, lt), c * tpr + lt < nvec);
   }
   for (int j = tail0; j < nvec; j += tpr) {
-    emit(ld<S, VEC>(xr + (int64_t)j * VEC), (int64_t)j * VEC);
+    emit(ld<S, VEC>(xr + (int64_t)j * VEC), (int64_t)j * VEC, true);
   }
 }
 

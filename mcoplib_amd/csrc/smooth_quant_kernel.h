@@ -232,14 +232,16 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
   const int nvec = hidden / VEC;
   const int tpr = (int)blockDim.x;
   const int64_t base = (int64_t)blockIdx.x * hidden;
+  // A head slot past the row end holds a copy of the row's vector 0 (its sum-of-squares term
+  // is dropped), so the head loads are unconditional: loads under a per-lane branch each wait
+  // for completion where the branch rejoins, which serializes their latencies.
+  const int tid = (int)threadIdx.x;
+  auto hoff = [&](int c, int lt) { return (int64_t)load_index(c * tpr + lt, nvec) * VEC; };
   Pack<S, VEC> xc[NC], rc[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const int j = c * tpr + (int)threadIdx.x;
-    if (j < nvec) {
-      xc[c] = ld<S, VEC>(x + base + (int64_t)j * VEC);
-      if constexpr (RES) rc[c] = ld<S, VEC>(res + base + (int64_t)j * VEC);
-    }
+    xc[c] = ld<S, VEC>(x + base + hoff(c, tid));
+    if constexpr (RES) rc[c] = ld<S, VEC>(res + base + hoff(c, tid));
   }
   // The next NL vectors of every lane are held in LDS: lane-private slots (vector c of lane t
   // at [c][t]: consecutive lanes, consecutive 16-byte slots), so no barrier is needed.  The
@@ -247,14 +249,10 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
   constexpr int NL = VEC > 1 ? (RES ? 4 : 8) : 0;
   constexpr int NLS = NL > 0 ? NL * (RES ? 2 : 1) : 1;
   __shared__ Pack<S, VEC> lds[NLS][kWideLanes];
-  const int tid = (int)threadIdx.x;
 #pragma unroll
   for (int c = 0; c < NL; ++c) {
-    const int j = (NC + c) * tpr + tid;
-    if (j < nvec) {
-      lds[c][tid] = ld<S, VEC>(x + base + (int64_t)j * VEC);
-      if constexpr (RES) lds[NL + c][tid] = ld<S, VEC>(res + base + (int64_t)j * VEC);
-    }
+    lds[c][tid] = ld<S, VEC>(x + base + hoff(NC + c, tid));
+    if constexpr (RES) lds[NL + c][tid] = ld<S, VEC>(res + base + hoff(NC + c, tid));
   }
   auto t_head = [&](int c, float* t) {  // a = x (+ r), unrounded; c < NC + NL
     Pack<S, VEC> xv, rv;
@@ -285,12 +283,12 @@ k_rms_norm_smooth_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scal
   double ss = 0.0;
 #pragma unroll
   for (int c = 0; c < NC + NL; ++c) {
-    if (c * tpr + (int)threadIdx.x < nvec) {
-      float t[VEC];
-      t_head(c, t);
+    float t[VEC];
+    t_head(c, t);
+    double vs = 0.0;
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) ss = __builtin_fma((double)t[e], (double)t[e], ss);
-    }
+    for (int e = 0; e < VEC; ++e) vs = __builtin_fma((double)t[e], (double)t[e], vs);
+    ss += c * tpr + tid < nvec ? vs : 0.0;
   }
   for (int j = tail0; j < nvec; j += tpr) {
     float t[VEC];
