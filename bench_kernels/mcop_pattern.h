@@ -1,10 +1,11 @@
 /*
- * mcop_pattern.h -- C ABI of libmcop_pattern.so: compute-free kernels with the HBM access pattern
- * of the operators' register-resident row kernels, plus plain streaming kernels (copy, read-only,
- * write-only). Measurement only: they have no counterpart in the reference and compute nothing
- * meaningful; bench.py times them beside the operators to give each operator's practical ceiling
- * on the GPU it runs on. Conventions as in mcop_norm.h (device pointers, hipStream_t as void*,
- * asynchronous, 0 = success).
+ * mcop_pattern.h -- C ABI of bench_kernels/libmcop_pattern.so: compute-free kernels with the HBM
+ * access pattern of the operators' register-resident row kernels, plain streaming kernels (copy,
+ * read-only, write-only) and an empty kernel. Measurement only, not part of the operator library:
+ * they have no counterpart in the reference and compute nothing meaningful; bench.py builds and
+ * times them beside the operators to give each operator's practical ceiling (and, for decode
+ * shapes, its latency floor) on the GPU it runs on. Conventions as in include/mcop_norm.h
+ * (device pointers, hipStream_t as void*, asynchronous, 0 = success).
  */
 #ifndef MCOP_PATTERN_H
 #define MCOP_PATTERN_H
@@ -30,7 +31,15 @@ enum {
      the loaded values holds, so every load is needed) */
   MCOP_PATTERN_READ = 4,
   /* writes o0 */
-  MCOP_PATTERN_WRITE = 5
+  MCOP_PATTERN_WRITE = 5,
+  /* touches nothing: an empty kernel launched with the given shape's grid and workgroup size
+     (the floor under any kernel of that launch shape); no tensor is needed */
+  MCOP_PATTERN_EMPTY = 6,
+  /* MCOP_PATTERN_ADD_NORM_QUANT in the operators' exact-row form: one row per workgroup and
+     every lane in the row (vectors_per_lane * lanes_per_row == hidden / 8, lanes_per_row >=
+     256), scalar row bases, no bounds tests -- the form the operator takes for such rows, e.g.
+     decode rows of 5120 at two vectors over 320 lanes */
+  MCOP_PATTERN_ADD_NORM_QUANT_EXACT = 7
 };
 
 enum { MCOP_PATTERN_E_INVALID = -1, MCOP_PATTERN_E_LAUNCH = -3 };

@@ -1,5 +1,5 @@
 // pattern.hip -- compute-free kernels with the exact HBM access pattern of the row kernels
-// (measurement only; built into libmcop_pattern.so, not into the operator library).
+// (measurement only; built into bench_kernels/libmcop_pattern.so, not into the operator library).
 //
 // Each kernel issues the same loads and stores as one operator's register-resident row kernel --
 // same lane mapping (rowkern.h: vector v of lane lt at v * tpr + lt), the same vectors per lane
@@ -12,8 +12,8 @@
 // this GPU; the copy, read-only and write-only kernels give the plain streaming ceilings.
 #include <hip/hip_runtime.h>
 
-#include "../../../include/mcop_pattern.h"
-#include "../rowkern.h"
+#include "mcop_pattern.h"
+#include "../mcoplib_amd/csrc/rowkern.h"
 
 #include <cstdarg>
 #include <cstdio>
@@ -59,7 +59,10 @@ constexpr Pat kPat[] = {
 
 using u16x8 = Pack<uint16_t, 8>;
 
-template <int P, int NV>
+// EX: the exact-row form of the operators' kernels (one row per workgroup, every lane in the row,
+// NV * tpr == hidden / 8): uniform row index, scalar row bases with 32-bit offsets, no bounds
+// tests, the reductions' first wave is 0 -- the form the operators take for such rows.
+template <int P, int NV, bool EX = false>
 __global__ void __launch_bounds__(max_tpr(8, NV))
 k_pattern(const uint16_t* __restrict__ x, const uint16_t* __restrict__ r,
           const uint16_t* __restrict__ w, const float* __restrict__ sm, uint16_t* __restrict__ o0,
@@ -67,29 +70,38 @@ k_pattern(const uint16_t* __restrict__ x, const uint16_t* __restrict__ r,
           int64_t rows, int hidden, int tpr) {
   constexpr Pat pt = kPat[P];
   __shared__ float red[16];
-  const RowPos p = row_pos(rows, tpr);
+  RowPos p;
+  if constexpr (EX) {
+    p = row_pos_one();
+  } else {
+    p = row_pos(rows, tpr);
+  }
   const int nvec = hidden / 8;
   const int64_t base = p.row * (int64_t)hidden, lbase = p.lrow * (int64_t)hidden;
+  auto lj_of = [&](int v) {
+    const int j = vec_index(v, tpr, p.lt);
+    return (int64_t)(EX ? j : load_index(j, nvec)) * 8;
+  };
   u16x8 xv[NV], rv[NV], wv[NV];
   Pack<float, 8> sv[NV];
   constexpr bool shared_first = pt.shared_first || NV >= 4;
   if constexpr (shared_first) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
-      const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * 8;
-      if constexpr (pt.w) wv[v] = ld<uint16_t, 8>(w + lj);
-      if constexpr (pt.sm) sv[v] = ld<float, 8>(sm + lj);
+      const int64_t lj = lj_of(v);
+      if constexpr (pt.w) wv[v] = ld<uint16_t, 8>(row_elem<EX>(w, 0, lj));
+      if constexpr (pt.sm) sv[v] = ld<float, 8>(row_elem<EX>(sm, 0, lj));
     }
     shared_loads_first();
   }
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int64_t lj = (int64_t)load_index(vec_index(v, tpr, p.lt), nvec) * 8;
-    if constexpr (pt.nin >= 1) xv[v] = ld_nt<uint16_t, 8>(x + lbase + lj);
-    if constexpr (pt.nin >= 2) rv[v] = ld_nt<uint16_t, 8>(r + lbase + lj);
+    const int64_t lj = lj_of(v);
+    if constexpr (pt.nin >= 1) xv[v] = ld_nt<uint16_t, 8>(row_elem<EX>(x, lbase, lj));
+    if constexpr (pt.nin >= 2) rv[v] = ld_nt<uint16_t, 8>(row_elem<EX>(r, lbase, lj));
     if constexpr (!shared_first) {
-      if constexpr (pt.w) wv[v] = ld<uint16_t, 8>(w + lj);
-      if constexpr (pt.sm) sv[v] = ld<float, 8>(sm + lj);
+      if constexpr (pt.w) wv[v] = ld<uint16_t, 8>(row_elem<EX>(w, 0, lj));
+      if constexpr (pt.sm) sv[v] = ld<float, 8>(row_elem<EX>(sm, 0, lj));
     }
   }
   uint32_t acc = 0;
@@ -117,22 +129,22 @@ k_pattern(const uint16_t* __restrict__ x, const uint16_t* __restrict__ r,
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int j = vec_index(v, tpr, p.lt);
-      if (stream < 0 || !p.live || j >= nvec) continue;
-      const int64_t o = base + (int64_t)j * 8;
+      if (stream < 0 || !p.live || (!EX && j >= nvec)) continue;
+      const int64_t o = (int64_t)j * 8;
       u16x8 av = a[v], bv = b[v];
       Pack<uint8_t, 8> cv = c[v];
       av.v[0] ^= (uint16_t)mix;
       bv.v[0] ^= (uint16_t)mix;
       cv.v[0] ^= (uint8_t)mix;
-      if (stream == 0) st_nt<uint16_t, 8>(o0 + o, av);
-      if (stream == 1) st_nt<uint16_t, 8>(o1 + o, bv);
-      if (stream == 2) st_nt<uint8_t, 8>(q + o, cv);
+      if (stream == 0) st_nt<uint16_t, 8>(row_elem<EX>(o0, base, o), av);
+      if (stream == 1) st_nt<uint16_t, 8>(row_elem<EX>(o1, base, o), bv);
+      if (stream == 2) st_nt<uint8_t, 8>(row_elem<EX>(q, base, o), cv);
     }
 #pragma unroll
     for (int rr = 0; rr < pt.reduce[k]; ++rr) {
       // the operator's row reduction, on a value of this lane (bits of acc as a float)
-      const float f = row_reduce(__builtin_bit_cast(float, (acc >> (rr + 1)) & 0x3f7fffffu), red,
-                                 tpr, MaxOp());
+      const float f = row_reduce<EX>(__builtin_bit_cast(float, (acc >> (rr + 1)) & 0x3f7fffffu),
+                                     red, tpr, MaxOp());
       mix ^= __builtin_bit_cast(uint32_t, f);
       if (tpr > 64) __syncthreads();  // the slots are reused by the next reduction
     }
@@ -147,14 +159,18 @@ k_pattern(const uint16_t* __restrict__ x, const uint16_t* __restrict__ r,
   }
 }
 
-template <int P>
+// A kernel that does nothing: launched with an operator's grid and workgroup size, its duration
+// is the floor under any kernel of that launch shape (dispatch, wave launch, end of the grid).
+__global__ void __launch_bounds__(1024) k_empty() {}
+
+template <int P, bool EX = false>
 static int launch(const Geometry& g, const uint16_t* x, const uint16_t* r, const uint16_t* w,
                   const float* sm, uint16_t* o0, uint16_t* o1, uint8_t* q, float* s, int64_t rows,
                   int hidden, unsigned lds, hipStream_t st) {
   const dim3 grid((unsigned)g.blocks), block((unsigned)(g.tpr * g.rpb));
 #define MCOP_PAT(NVV)                                                                         \
-  hipLaunchKernelGGL((k_pattern<P, NVV>), grid, block, lds, st, x, r, w, sm, o0, o1, q, s, rows, \
-                     hidden, g.tpr)
+  hipLaunchKernelGGL((k_pattern<P, NVV, EX>), grid, block, lds, st, x, r, w, sm, o0, o1, q, s, \
+                     rows, hidden, g.tpr)
   switch (g.nv) {
     case 1: MCOP_PAT(1); break;
     case 2: MCOP_PAT(2); break;
@@ -177,19 +193,34 @@ extern "C" int mcop_pattern(int pattern, const void* x, const void* r, const voi
                             int64_t rows, int64_t hidden, int vectors_per_lane,
                             int lanes_per_row, int lds_bytes, void* stream) {
   using namespace mcop;
-  if (pattern < 0 || pattern > MCOP_PATTERN_WRITE) {
+  if (pattern < 0 || pattern > MCOP_PATTERN_ADD_NORM_QUANT_EXACT) {
     return pat_error("mcop_pattern: unknown pattern %d", pattern);
   }
-  const Pat& pt = kPat[pattern];
+  const bool exact = pattern == MCOP_PATTERN_ADD_NORM_QUANT_EXACT;
+  const Pat& pt = kPat[exact ? MCOP_PATTERN_ADD_NORM_QUANT
+                             : pattern == MCOP_PATTERN_EMPTY ? MCOP_PATTERN_WRITE : pattern];
   const int nv = vectors_per_lane, tpr = lanes_per_row;
-  if (rows <= 0 || hidden <= 0 || hidden % 8 != 0 || hidden > INT32_MAX ||
+  if (rows <= 0 || rows > INT32_MAX || hidden <= 0 || hidden % 8 != 0 || hidden > INT32_MAX ||
       !(nv == 1 || nv == 2 || nv == 4 || nv == 8) || tpr <= 0 || tpr % 64 != 0 ||
       tpr > max_tpr(8, nv) || (int64_t)nv * tpr < hidden / 8 || lds_bytes < 0 ||
-      lds_bytes > 163840) {
+      lds_bytes > 163840 || (exact && ((int64_t)nv * tpr != hidden / 8 || tpr < 256))) {
     return pat_error("mcop_pattern: bad shape rows=%lld hidden=%lld nv=%d tpr=%d (hidden a "
                      "multiple of 8, nv in {1,2,4,8}, tpr a multiple of 64 that holds the row, "
-                     "lds_bytes <= 163840)",
+                     "lds_bytes <= 163840; the exact-row pattern: nv * tpr == hidden / 8 and "
+                     "tpr >= 256)",
                      (long long)rows, (long long)hidden, nv, tpr);
+  }
+  auto st = static_cast<hipStream_t>(stream);
+  if (pattern == MCOP_PATTERN_EMPTY) {
+    const int rpb = tpr < 256 ? 256 / tpr : 1;
+    hipLaunchKernelGGL(k_empty, dim3((unsigned)((rows + rpb - 1) / rpb)),
+                       dim3((unsigned)(tpr * rpb)), 0, st);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+      pat_error("mcop_pattern: launch failed: %s", hipGetErrorString(e));
+      return MCOP_PATTERN_E_LAUNCH;
+    }
+    return 0;
   }
   // every tensor the pattern touches: present and aligned to its access width
   const struct { const void* p; int align; } need[8] = {
@@ -208,7 +239,6 @@ extern "C" int mcop_pattern(int pattern, const void* x, const void* r, const voi
   g.tpr = tpr;
   g.rpb = tpr < 256 ? 256 / tpr : 1;
   g.blocks = (rows + g.rpb - 1) / g.rpb;
-  auto st = static_cast<hipStream_t>(stream);
   auto* xp = static_cast<const uint16_t*>(x);
   auto* rp = static_cast<const uint16_t*>(r);
   auto* wp = static_cast<const uint16_t*>(w);
@@ -227,6 +257,9 @@ extern "C" int mcop_pattern(int pattern, const void* x, const void* r, const voi
       return launch<3>(g, xp, rp, wp, smooth, o0p, o1p, qp, scales, rows, h, (unsigned)lds_bytes, st);
     case MCOP_PATTERN_READ:
       return launch<4>(g, xp, rp, wp, smooth, o0p, o1p, qp, scales, rows, h, (unsigned)lds_bytes, st);
+    case MCOP_PATTERN_ADD_NORM_QUANT_EXACT:
+      return launch<0, true>(g, xp, rp, wp, smooth, o0p, o1p, qp, scales, rows, h,
+                             (unsigned)lds_bytes, st);
     default:
       return launch<5>(g, xp, rp, wp, smooth, o0p, o1p, qp, scales, rows, h, (unsigned)lds_bytes, st);
   }

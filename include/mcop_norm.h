@@ -88,7 +88,8 @@ int mcop_rms_norm_dynamic_per_token_quant(void* out, mcop_dtype out_dtype, float
  *   rho = 1/sqrt(sum(a^2)/H + eps) on the unrounded a;  a~ = round(a)
  *   u = (a~ / rho) * w   (or (a~ * rho) * w with MCOP_SQ_STANDARD_NORM); after_norm <- round(u)
  *   v = u * smooth;  A = max|v|
- *   int8: s = A/127, q = sat[-127,127](rne(v * (1/s)));  fp8: s = A/448,
+ *   int8: s = A/127, q = sat[-127,127](rne(v * (1/s)));
+ *   fp8 (this library's extension; the reference's operator is int8 only): s = A/448,
  *   q = e4m3fn(clamp(v / s, -448, 448));  A == 0 gives s = 0 and q = 0.
  * `weight_dtype` and `smooth_dtype` are each `in_dtype` or MCOP_F32. after_res, after_norm and
  * residual may be NULL.
@@ -225,27 +226,14 @@ int mcop_fused_add_rms_norm_dynamic_per_token_quant_padding_output(
     const void* input, void* residual, const void* weight, int64_t num_tokens,
     int64_t hidden_size, int64_t pad_size, float epsilon, void* stream);
 
-/* The clamp-and-convert step shared by every fp8 epilogue, elementwise:
- *   out[i] = e4m3fn(clamp(in[i] * mul, -448, 448))   (RNE; clamp with fmin/fmax semantics)
- * No reference counterpart as an entry point (the step is float_to_fp8,
- * op/vllm/quantization/fused_kernels/quant_conversions.cuh:23-28); exported so the hardware
- * conversion can be checked bit for bit against the OCP fp8 definition. */
-int mcop_fp8_e4m3fn_from_f32(uint8_t* out, const float* in, int64_t n, float mul, void* stream);
-
-/* Message of the last failed call on this host thread ("" if none). */
+/* Message of the last failed call on this host thread ("" if none). Stands in for the
+ * reference's TORCH_CHECK messages (c10::Error text), which its entry points raise directly. */
 const char* mcop_last_error(void);
 
-/* ABI version of this header (bumped on any signature change). */
+/* ABI version of this header (bumped on any signature change). The reference's extension has
+ * no such query; callers over a C ABI use it to refuse a library built from another header. */
 int mcop_abi_version(void);
 #define MCOP_ABI_VERSION 2
-
-/* Debug hook, not part of the operator interface (no reference counterpart): forces the launch
- * shape of the row kernels for later calls made BY THE CALLING THREAD only, for the tests that
- * check results do not depend on the launch shape and for tuning sweeps. Other threads keep the
- * automatic choice. vectors_per_lane in {0,1,2,4,8,16}, lanes_per_row in {0, 16, 32} or a
- * multiple of 64 up to 1024; (0, 0) restores the automatic choice. A request the row does not
- * fit falls back to automatic. Results do not change, only speed. */
-int mcop_debug_set_launch_override(int vectors_per_lane, int lanes_per_row);
 
 #ifdef __cplusplus
 }

@@ -6,7 +6,6 @@ Usage: python mcoplib_amd/_build.py [--jobs N]
 
 Each csrc/*.hip translation unit is compiled for gfx950 only, in parallel, then linked into
 mcoplib_amd/libmcop_norm.so next to this file. Objects go to mcoplib_amd/_build/.
-csrc/pattern/pattern.hip (measurement kernels, not operators) becomes libmcop_pattern.so.
 csrc/torch_ops.cpp is host C++ against torch's headers (ROCm build) and links
 libmcop_norm.so through an $ORIGIN run path.
 """
@@ -28,7 +27,6 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libmcop_norm.so"
 EXT = PKG / "_torch_ops.so"
-PATTERN_LIB = PKG / "libmcop_pattern.so"  # compute-free access-pattern kernels (bench only)
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -156,27 +154,6 @@ def build(jobs: int | None = None, verbose: bool = True, out: Path = LIB,
     return out
 
 
-def build_pattern(verbose: bool = True) -> Path:
-    """Compile csrc/pattern/pattern.hip (the compute-free access-pattern kernels bench.py times
-    beside the operators) into mcoplib_amd/libmcop_pattern.so (always rebuilds)."""
-    BUILD.mkdir(parents=True, exist_ok=True)
-    obj, records = _compile(CSRC / "pattern" / "pattern.hip", BUILD)
-    _demangle(records)
-    spills = [r["kernel"] for r in records if r.get("scratch", 0) != 0]
-    if spills:
-        raise RuntimeError("pattern kernels spill: " + "; ".join(spills))
-    tmp = PATTERN_LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC",
-           f"-Wl,-soname,{PATTERN_LIB.name}", "-o", str(tmp), str(obj)]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"link failed:\n{proc.stderr}")
-    os.replace(tmp, PATTERN_LIB)
-    if verbose:
-        print(f"built {PATTERN_LIB}", file=sys.stderr)
-    return PATTERN_LIB
-
-
 def build_extension(verbose: bool = True) -> Path:
     """Compile csrc/torch_ops.cpp into mcoplib_amd/_torch_ops.so (always rebuilds)."""
     import sysconfig
@@ -213,7 +190,6 @@ def main() -> None:
     args = ap.parse_args()
     build(args.jobs)
     build_extension()
-    build_pattern()
 
 
 if __name__ == "__main__":

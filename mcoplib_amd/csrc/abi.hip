@@ -10,6 +10,7 @@
 #include <unordered_map>
 
 #include "../../include/mcop_norm.h"
+#include "mcop_testing.h"
 #include "rowkern.h"
 
 namespace mcop {
@@ -145,6 +146,17 @@ bool row_fits(int64_t hidden, int vec, KernelOfNv kernels, int min_tpr) {
   for (int c = 0; c < ncand; ++c) {
     if (row_lanes(ceil_div(nvec, cands[c]), min_tpr) > max_tpr(vec, cands[c])) continue;
     if (!kernel_info(kernels(cands[c])).spills) return true;
+  }
+  return false;
+}
+
+bool exact_form_ok(const void* ex_kernel) {
+  const KernelInfo k = kernel_info(ex_kernel);
+  if (k.ok && !k.spills) return true;
+  if (trace_enabled()) {
+    fprintf(stdout, "[mcop]   exact-row form %s: generic form\n",
+            k.ok ? "spills registers" : "has no attributes");
+    fflush(stdout);
   }
   return false;
 }

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include "../../include/mcop_norm.h"
+#include "mcop_testing.h"
 #include "rowkern.h"
 
 namespace mcop {

@@ -168,18 +168,27 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
   const float rho = mcop_inv_rms(ss, hidden, eps);
   const float inv_rho = mcop_div_rn(1.0f, rho);
   // The division form: the wave divides in the short form when every lane's elements are in its
-  // domain (every a^2 <= ss (1 + 2^-6), rounded or not).
+  // domain (every a^2 <= ss (1 + 2^-6), rounded or not, for every a that is finite).  Only an
+  // fp16 rounding of the residual sum can turn a finite sum (|x + r| >= 65520) into an infinite
+  // a while ss stays small (bf16: ss/H overflows fp32 or the quotient bound fails; fp32 does not
+  // round), so fp16 rows with a residual also check that every a is finite.
+  constexpr bool kRoundOverflows = RES && sizeof(S) == 2 && !__is_same(E, BF16);
   bool short_div = false;
   if (mode != NORM_VLLM && mode != NORM_MC && rms_div) {
     float amin = __builtin_inff();
+    float amx = 0.0f;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) amin = __builtin_fminf(amin, __builtin_fabsf(a[v][e]));
+      for (int e = 0; e < VEC; ++e) {
+        amin = __builtin_fminf(amin, __builtin_fabsf(a[v][e]));
+        if constexpr (kRoundOverflows) amx = __builtin_fmaxf(amx, __builtin_fabsf(a[v][e]));
+      }
     }
-    short_div = __builtin_amdgcn_ballot_w64(!div_domain_ok(amin,
-                                                           ss * (1.0 + 0x1p-6),
-                                                           inv_rho, mcop_divisor_ok(rho))) == 0;
+    const bool in_domain = div_domain_ok(amin, ss * (1.0 + 0x1p-6), inv_rho,
+                                         mcop_divisor_ok(rho)) &&
+                           (!kRoundOverflows || amx <= 0x1.fffffep127f);
+    short_div = __builtin_amdgcn_ballot_w64(!in_domain) == 0;
   }
 
 #pragma unroll
@@ -354,16 +363,19 @@ static void norm_launch_nv(const Geometry& g, const NormArgs& a, hipStream_t st)
     if (g.nv == 4) MCOP_LAUNCH(4, false); else MCOP_LAUNCH(16, false);
   } else {
     // exact rows (one row per workgroup, every lane in it): the EX form at two vectors a lane,
-    // and at four or eight on the latency path (at most 256 rows)
+    // and at four or eight on the latency path (at most 256 rows), when it keeps its registers
     const bool ex = g.rpb == 1 && (int64_t)g.nv * g.tpr == a.hidden / VEC &&
                     (g.nv == 2 || a.rows <= 256);
+#define MCOP_EX(NVV)                                                                           \
+  (ex && exact_form_ok(reinterpret_cast<const void*>(&k_rms_norm<E, EW, VEC, NVV, RES, true>)))
     switch (g.nv) {
       case 1: MCOP_LAUNCH(1, false); break;
-      case 2: if (ex) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
-      case 4: if (ex) MCOP_LAUNCH(4, true); else MCOP_LAUNCH(4, false); break;
-      case 8: if (ex) MCOP_LAUNCH(8, true); else MCOP_LAUNCH(8, false); break;
+      case 2: if (MCOP_EX(2)) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
+      case 4: if (MCOP_EX(4)) MCOP_LAUNCH(4, true); else MCOP_LAUNCH(4, false); break;
+      case 8: if (MCOP_EX(8)) MCOP_LAUNCH(8, true); else MCOP_LAUNCH(8, false); break;
       default: MCOP_LAUNCH(16, false); break;
     }
+#undef MCOP_EX
   }
 #undef MCOP_LAUNCH
 }

@@ -278,16 +278,19 @@ static void launch_nv(const Geometry& g, const PtqArgs& a, hipStream_t st) {
     if (g.nv == 4) MCOP_LAUNCH(4, false); else MCOP_LAUNCH(16, false);
   } else {
     // exact rows (one row per workgroup, every lane in it): the EX form at two vectors a lane,
-    // and at four or eight on the latency path (at most 256 rows)
+    // and at four or eight on the latency path (at most 256 rows), when it keeps its registers
     const bool ex = g.rpb == 1 && (int64_t)g.nv * g.tpr == a.hidden / VEC &&
                     (g.nv == 2 || a.rows <= 256);
+#define MCOP_EX(NVV)                                                                           \
+  (ex && exact_form_ok(reinterpret_cast<const void*>(&k_per_token_quant<E, VEC, NVV, MODE, true>)))
     switch (g.nv) {
       case 1: MCOP_LAUNCH(1, false); break;
-      case 2: if (ex) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
-      case 4: if (ex) MCOP_LAUNCH(4, true); else MCOP_LAUNCH(4, false); break;
-      case 8: if (ex) MCOP_LAUNCH(8, true); else MCOP_LAUNCH(8, false); break;
+      case 2: if (MCOP_EX(2)) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
+      case 4: if (MCOP_EX(4)) MCOP_LAUNCH(4, true); else MCOP_LAUNCH(4, false); break;
+      case 8: if (MCOP_EX(8)) MCOP_LAUNCH(8, true); else MCOP_LAUNCH(8, false); break;
       default: MCOP_LAUNCH(16, false); break;
     }
+#undef MCOP_EX
   }
 #undef MCOP_LAUNCH
 }

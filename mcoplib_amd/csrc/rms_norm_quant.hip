@@ -375,15 +375,20 @@ static void launch_nv(const Geometry& g, void* out, float* scales, const void* x
     // takes more registers (fewer resident waves) for no gain on bandwidth-bound shapes.  The
     // 7168 chain's rows (896 vectors) are exact only at two vectors over 448 lanes.
     constexpr bool wide_ex = MODE != QM_MC_7168;
+    // The EX form only when it keeps its registers.
     const bool ex = g.rpb == 1 && (int64_t)g.nv * g.tpr == hidden / VEC &&
                     (g.nv == 2 || (wide_ex && rows <= 256));
+#define MCOP_EX(NVV, EXX)                                                                      \
+  (ex && exact_form_ok(                                                                        \
+             reinterpret_cast<const void*>(&k_rms_norm_quant<E, VEC, NVV, FP8, RES, MODE, EXX>)))
     switch (g.nv) {
       case 1: MCOP_LAUNCH(1, false); break;
-      case 2: if (ex) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
-      case 4: if (ex) MCOP_LAUNCH(4, wide_ex); else MCOP_LAUNCH(4, false); break;
-      case 8: if (ex) MCOP_LAUNCH(8, wide_ex); else MCOP_LAUNCH(8, false); break;
+      case 2: if (MCOP_EX(2, true)) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
+      case 4: if (MCOP_EX(4, wide_ex)) MCOP_LAUNCH(4, wide_ex); else MCOP_LAUNCH(4, false); break;
+      case 8: if (MCOP_EX(8, wide_ex)) MCOP_LAUNCH(8, wide_ex); else MCOP_LAUNCH(8, false); break;
       default: MCOP_LAUNCH(16, false); break;
     }
+#undef MCOP_EX
   }
 #undef MCOP_LAUNCH
 }

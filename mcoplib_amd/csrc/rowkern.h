@@ -468,6 +468,11 @@ bool choose_geometry(const char* op, int64_t rows, int64_t hidden, int vec, Kern
 // kernel compiled without spilling registers.  Other rows take the operator's multi-pass kernel.
 bool row_fits(int64_t hidden, int vec, KernelOfNv kernels, int min_tpr = 16);
 
+// True when the exact-row (EX) instantiation `ex_kernel` may replace the generic one the launch
+// shape was chosen for: it compiled without spilling registers.  Otherwise the launch keeps the
+// generic form, which choose_geometry has already checked.
+bool exact_form_ok(const void* ex_kernel);
+
 // Launch check of the multi-pass kernels for rows too wide for the register-resident ones
 // (one 1024-lane workgroup per row): false, with the message set, beyond 2^31 - 1 rows.
 bool wide_rows_ok(const char* op, int64_t rows);

@@ -11,8 +11,10 @@
 //   u = (b(a) / rho) * w     [literal form; (b(a) * rho) * w with MCOP_SQ_STANDARD_NORM]
 //   after_norm <- b(u);  v = u * smooth                              norm_and_quant :163-186
 //   A = max|v|;  int8: s = A/127, q = sat[-127,127](rne(v * (1/s)))  :125-161, :296-297
-//   fp8 (the operator's entry accepts int8 only; its kernel's fp8 branch, :299-301, divides):
-//        s = A/448, q = e4m3fn(clamp(v / s, +-448))
+//   fp8: this library's extension, with no counterpart in the reference (its entry accepts int8
+//        only, :658; ScaledQuant is defined for int8 only, :51-66; its scale is A/127, :154):
+//        s = A/448, q = e4m3fn(clamp(v / s, +-448)), dividing as the path's fp8 quantizers do
+//        (op/vllm/quantization/fused_kernels/quant_conversions.cuh:52-59)
 //   A == 0: s = 0 and q = 0.
 // One pass: the row stays in VGPRs between the two reductions, so HBM sees x (and residual)
 // read once and after_res, after_norm, the codes and the scale written once.  The division by
@@ -107,18 +109,26 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
   const bool rho_ok = mcop_divisor_ok(rho);
   const bool standard = (flags & MCOP_SQ_STANDARD_NORM) != 0;
   // The literal form: the wave divides in the short form when every lane's elements are in its
-  // domain (every b(a)^2 <= a^2 (1 + 2^-8)^2 <= ss (1 + 2^-6)).
+  // domain (every b(a)^2 <= a^2 (1 + 2^-8)^2 <= ss (1 + 2^-6), for every b(a) that is finite).
+  // Only fp16 can round a finite a to an infinite b(a) while ss stays small (|x + r| >= 65520);
+  // for bf16 such an a makes ss/H overflow fp32 or the quotient bound fail, and fp32 does not
+  // round.  So fp16 rows with a residual also check that every b(a) is finite.
+  constexpr bool kRoundOverflows = RES && sizeof(S) == 2 && !__is_same(E, BF16);
   bool short_div = false;
   if (!standard) {
     float amin = __builtin_inff();
+    float amx = 0.0f;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) amin = __builtin_fminf(amin, __builtin_fabsf(a[v][e]));
+      for (int e = 0; e < VEC; ++e) {
+        amin = __builtin_fminf(amin, __builtin_fabsf(a[v][e]));
+        if constexpr (kRoundOverflows) amx = __builtin_fmaxf(amx, __builtin_fabsf(a[v][e]));
+      }
     }
-    short_div = __builtin_amdgcn_ballot_w64(!div_domain_ok(amin,
-                                                           ss * (1.0 + 0x1p-6),
-                                                           inv_rho, rho_ok)) == 0;
+    const bool in_domain = div_domain_ok(amin, ss * (1.0 + 0x1p-6), inv_rho, rho_ok) &&
+                           (!kRoundOverflows || amx <= 0x1.fffffep127f);
+    short_div = __builtin_amdgcn_ballot_w64(!in_domain) == 0;
   }
 
   float amax = 0.0f;
@@ -419,14 +429,19 @@ static void launch_nv(const Geometry& g, const Args& a, hipStream_t st) {
     // exact rows (one row per workgroup, every lane in it) on the latency path (at most 256
     // rows) take the EX form; bandwidth-bound shapes keep the generic one (a uniform-row form
     // measured slower at cfg 4's width)
+    // (and only when the EX form keeps its registers)
     const bool ex = g.rpb == 1 && (int64_t)g.nv * g.tpr == a.hidden / VEC && a.rows <= 256;
+#define MCOP_EX(NVV)                                                                           \
+  (ex && exact_form_ok(reinterpret_cast<const void*>(                                          \
+             &k_rms_norm_smooth_quant<E, EW, ES, VEC, NVV, FP8, RES, true>)))
     switch (g.nv) {
       case 1: MCOP_LAUNCH(1, false); break;
-      case 2: if (ex) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
-      case 4: if (ex) MCOP_LAUNCH(4, true); else MCOP_LAUNCH(4, false); break;
-      case 8: if (ex) MCOP_LAUNCH(8, true); else MCOP_LAUNCH(8, false); break;
+      case 2: if (MCOP_EX(2)) MCOP_LAUNCH(2, true); else MCOP_LAUNCH(2, false); break;
+      case 4: if (MCOP_EX(4)) MCOP_LAUNCH(4, true); else MCOP_LAUNCH(4, false); break;
+      case 8: if (MCOP_EX(8)) MCOP_LAUNCH(8, true); else MCOP_LAUNCH(8, false); break;
       default: MCOP_LAUNCH(16, false); break;
     }
+#undef MCOP_EX
   }
 #undef MCOP_LAUNCH
 }

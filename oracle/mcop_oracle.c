@@ -336,8 +336,12 @@ void oracle_rms_norm_quant_custom(int8_t* out, float* scales, const void* x, con
      after_norm <- b(u); v = u * sm; A = max|v|;
      int8: s = A / 127.0 (:154; binary64 quotient rounded to binary32 == the binary32 quotient),
            q = sat[-127,127](rne(v * (1/s))) (kernel/utils.h:219-226);
-     fp8 (the entry accepts int8 only, :658; the kernel's fp8 branch, :299-301, passes the scale
-          uninverted to ScaledQuant, which divides): s = A/448, q = e4m3fn(clamp(v / s)).
+     fp8: this library's own extension (BASELINE cfg 4), with no counterpart in the reference:
+          its entry accepts int8 only (:658), ScaledQuant is defined for int8 only (:51-66), so
+          the fp8 branch at :299-301 cannot be instantiated, and its scale is A/127 for any
+          output (:154).  Defined here as s = A/448, q = e4m3fn(clamp(v / s)) with the
+          correctly rounded quotient, the form of the path's fp8 quantizers
+          (op/vllm/quantization/fused_kernels/quant_conversions.cuh:52-59).
      A == 0: s = 0 and q = 0 (the reference computes 0 * inf, or 0 / 0 for fp8).
    w and sm are each stored as w_dt / sm_dt (the input dtype or fp32). */
 void oracle_rms_norm_smooth_quant(void* out, int out_dt, float* scales, const void* x,

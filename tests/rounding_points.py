@@ -153,8 +153,9 @@ def fp8_quotient_beyond_448():
 
 
 def h4_fp8_divides(u: torch.Tensor):
-    """H4's fp8 branch (op/fused_rms_norm_dq.cu:299-301: the scale is passed uninverted to
-    ScaledQuant<fp8, false>, which divides): q = e4m3(clamp(v / s)).
+    """H4's fp8 output, this library's extension (the reference's operator has no fp8 form:
+    op/fused_rms_norm_dq.cu:51-66 defines ScaledQuant for int8 only): q = e4m3(clamp(v / s)),
+    dividing by the scale as the path's fp8 quantizers do (quant_conversions.cuh:52-59).
 
     fp32 input; `u` is the row's after_norm (unrounded for fp32 input, independent of the smooth
     scales).  The smooth scales are chosen so that v = RN(u * sm) is 6.125 at one element (the

@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "../../include/mcop_norm.h"
+#include "../../mcoplib_amd/csrc/mcop_testing.h"
 
 namespace {
 

@@ -163,3 +163,61 @@ def test_head_and_vllm_rms_norm_specials():
         torch.ops._C.rms_norm(o, x.to(DEV), wv.to(DEV), 1e-6)
         torch.cuda.synchronize()
         assert_exact(o, ref, f"vLLM rms_norm {dtype}")
+
+
+def _fp16_overflow_rows(H, seed):
+    """fp16 x and residual [5, H] whose sums round to +-inf in fp16 while the fp32 sums (and so
+    the sum of squares) stay finite: one element 60000 + 60000; every element 40000 + 40000; one
+    element 33024 + 32496 = 65520 (the tie between 65504 and the overflow, which rounds to inf);
+    a control row whose sums reach 65504, the largest finite fp16; an ordinary row."""
+    g = gen(seed)
+    x = torch.randn(5, H, generator=g)
+    r = torch.randn(5, H, generator=g)
+    x[0, 3], r[0, 3] = 60000.0, 60000.0
+    x[1], r[1] = 40000.0, 40000.0
+    x[2, H // 2], r[2, H // 2] = 33024.0, 32496.0
+    x[3, 7], r[3, 7] = 32752.0, 32752.0
+    return x.to(torch.float16), r.to(torch.float16)
+
+
+@pytest.mark.parametrize("qdt", [torch.int8, torch.float8_e4m3fn])
+@pytest.mark.parametrize("standard", [False, True])
+def test_h4_fp16_residual_sum_overflow(qdt, standard):
+    """fp16 SmoothQuant with a residual whose rounded sums overflow: after_res is +-inf where the
+    fp32 sum is finite, and the literal form's division must see those infinities (the short
+    division form is only valid for finite b(a))."""
+    say(f"specials: smooth quant fp16 residual overflow {qdt} standard={standard}")
+    H = 2048
+    x, r = _fp16_overflow_rows(H, 21)
+    w = _w(H, 22, torch.float16)
+    sm = 0.5 + 1.5 * torch.rand(H, generator=gen(23))
+    q_ref, s_ref, ar_ref, an_ref = oracle.rms_norm_smooth_quant(x, w, sm, 1e-6, qdt, r, standard)
+    assert torch.isinf(ar_ref[:3].float()).any(dim=1).all(), "rows 0-2 must overflow"
+    q = torch.empty(x.shape, dtype=qdt, device=DEV)
+    s = torch.empty(x.shape[0], device=DEV)
+    ar, an = torch.empty(x.shape, dtype=x.dtype, device=DEV), torch.empty(x.shape, dtype=x.dtype,
+                                                                           device=DEV)
+    op.rms_norm_dynamic_per_token_quant(q, x.to(DEV), w.to(DEV), sm.to(DEV), s, 1e-6, ar, an,
+                                        r.to(DEV), standard_norm=standard)
+    torch.cuda.synchronize()
+    assert_exact(ar, ar_ref, "after_res")
+    assert_exact(an, an_ref, "after_norm")
+    assert_scales(s, s_ref, "scales")
+    assert_codes(q, q_ref, "codes")
+
+
+@pytest.mark.parametrize("H", [4096, 1030])  # the reference's vectorized / element-wise chains
+def test_mc_rms_norm_fp16_residual_sum_overflow(H):
+    """mcoplib rms_norm, fp16, rms_div, with a residual whose rounded sums overflow (the
+    element-wise chain at H = 1030 divides the rounded sum by rho)."""
+    say(f"specials: mcoplib rms_norm fp16 residual overflow H={H}")
+    x, r = _fp16_overflow_rows(H, 24)
+    w = _w(H, 25, torch.float16)
+    out_ref, ares_ref = oracle.rms_norm(x, w, 1e-6, residual=r, rms_div=True)
+    assert torch.isinf(ares_ref[:3].float()).any(dim=1).all(), "rows 0-2 must overflow"
+    out = torch.empty(x.shape, dtype=x.dtype, device=DEV)
+    ares = torch.empty(x.shape, dtype=x.dtype, device=DEV)
+    op.rms_norm(out, x.to(DEV), w.to(DEV), 1e-6, ares, r.to(DEV), True)
+    torch.cuda.synchronize()
+    assert_exact(out, out_ref, "out")
+    assert_exact(ares, ares_ref, "after_res")

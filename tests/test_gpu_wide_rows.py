@@ -398,3 +398,65 @@ def test_wide_tail_maxima_h3_and_no_residual():
     torch.cuda.synchronize()
     assert_scales(s, s_ref, "scales")
     assert_codes(q, q_ref, "codes")
+
+
+# Exact-row (EX) instantiations that spill where their generic form does not (the build's
+# resource remarks list them): fp32 H1 at eight vectors a lane, and fp16 SmoothQuant with fp32
+# weights and fp16 smooth scales at eight.  On the latency path (at most 256 rows) the launch
+# code would take the EX form for these exact rows; it must keep the generic one instead.  A
+# child process with MCOP_DEBUG_TRACE=1 (the trace switch is read once per process) runs both
+# and checks them against the oracle.
+_EX_SPILL_SCRIPT = r"""
+import sys, torch
+sys.path.insert(0, "tests")
+import oracle, mcoplib_amd._C
+from mcoplib_amd import op
+from gpu_util import DEV, assert_codes, assert_exact, assert_scales, gen
+x = torch.randn(4, 16384, generator=gen(40)).float()
+r = torch.randn(4, 16384, generator=gen(41)).float()
+w = (1 + 0.1 * torch.randn(16384, generator=gen(42))).float()
+x_ref, r_ref = oracle.fused_add_rms_norm(x, r, w, 1e-6)
+xd, rd = x.to(DEV), r.to(DEV)
+torch.ops._C.fused_add_rms_norm(xd, rd, w.to(DEV), 1e-6)
+torch.cuda.synchronize()
+assert_exact(rd, r_ref, "H1 residual")
+assert_exact(xd, x_ref, "H1 output")
+H = 20480
+x = torch.randn(4, H, generator=gen(43)).half()
+r = torch.randn(4, H, generator=gen(44)).half()
+w = (1 + 0.1 * torch.randn(H, generator=gen(45))).float()
+sm = (0.5 + 1.5 * torch.rand(H, generator=gen(46))).half()
+q_ref, s_ref, ar_ref, an_ref = oracle.rms_norm_smooth_quant(x, w, sm, 1e-6,
+                                                            torch.float8_e4m3fn, r)
+q = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=DEV)
+s = torch.empty(4, device=DEV)
+ar, an = torch.empty_like(x, device=DEV), torch.empty_like(x, device=DEV)
+op.rms_norm_dynamic_per_token_quant(q, x.to(DEV), w.to(DEV), sm.to(DEV), s, 1e-6, ar, an,
+                                    r.to(DEV))
+torch.cuda.synchronize()
+assert_exact(ar, ar_ref, "H4 after_res")
+assert_exact(an, an_ref, "H4 after_norm")
+assert_scales(s, s_ref, "H4 scales")
+assert_codes(q, q_ref, "H4 codes")
+print("children ok", flush=True)
+"""
+
+
+def test_exact_form_that_spills_takes_the_generic_form():
+    import os
+    import subprocess
+    import sys
+
+    from conftest import ROOT
+
+    say("exact-row forms that spill: H1 fp32 4x16384, H4 fp16 (fp32 w, fp16 smooth) 4x20480")
+    env = dict(os.environ, MCOP_DEBUG_TRACE="1")
+    out = subprocess.run([sys.executable, "-c", _EX_SPILL_SCRIPT], cwd=str(ROOT), env=env,
+                         capture_output=True, text=True, timeout=300)
+    say(out.stdout[-3000:])
+    assert out.returncode == 0, out.stderr[-3000:]
+    assert "children ok" in out.stdout
+    launches = [ln for ln in out.stdout.splitlines() if ln.startswith("[mcop] ")
+                and " rows=4 " in ln and " nv=8 " in ln]
+    assert len(launches) == 2, launches
+    assert out.stdout.count("exact-row form spills registers: generic form") == 2

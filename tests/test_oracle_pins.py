@@ -300,8 +300,8 @@ def test_h4_quant_stage_exact_for_fp32():
     inv = 1.0 / s_ref
     q_ref = torch.round(v * inv[:, None]).clamp(-127, 127).to(torch.int8)
     assert torch.equal(q, q_ref)
-    # fp8 (extension): s = A/448, codes = e4m3fn(clamp(v / s)) -- the kernel's fp8 branch passes
-    # the scale uninverted to a dividing quantizer (op/fused_rms_norm_dq.cu:299-301)
+    # fp8 (this library's extension; the reference's operator has no fp8 form): s = A/448,
+    # codes = e4m3fn(clamp(v / s)), dividing as the path's fp8 quantizers do
     q8, s8, _, _ = oracle.rms_norm_smooth_quant(x, w, sm, 1e-6, torch.float8_e4m3fn)
     s8_ref = A / 448.0
     assert torch.equal(s8, s8_ref)

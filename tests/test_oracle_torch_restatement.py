@@ -101,7 +101,7 @@ def test_h4_restatement(dtype, wdt, sdt, standard):
         assert torch.equal(s, s_ref)
         if qdt == torch.int8:
             assert torch.equal(q, torch.round(t).clamp(-127, 127).to(torch.int8))
-        else:  # the fp8 branch divides by the scale (op/fused_rms_norm_dq.cu:299-301)
+        else:  # fp8 (this library's extension) divides by the scale
             t8 = torch.where(A[:, None] > 0, v / s_ref[:, None], torch.zeros_like(v))
             assert torch.equal(q.view(torch.uint8),
                                t8.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8))
