@@ -13,16 +13,19 @@ input read once + every output written once) with
   - roofline: the kernel's average launch time from HIP events around the timed launches, next
     to the rocprofv3 kernel-trace mean and the HBM traffic of the committed profile summary;
   - guard: whether the headline stays at >= 75% of peak with traffic <= 1.01x the algorithmic
-    bytes (`regressed` true when not);
+    bytes, measured by a profile taken on the current kernel sources (`regressed` true when
+    not, `profile_stale` true when the profile's recorded source hash differs);
   - device_copy / ceilings: a non-temporal streaming copy, read-only and write-only kernels, and
-    compute-free kernels with each timed operator's exact access pattern (libmcop_pattern.so),
-    also run over the same elements reshaped to 2048-wide rows (the operator's traffic mix at
-    the fastest streaming shape);
+    compute-free kernels with each timed operator's exact access pattern
+    (bench_kernels/libmcop_pattern.so), also run over the same elements reshaped to 2048-wide
+    rows (the operator's traffic mix at the fastest streaming shape);
   - cpu_baseline / cpu_torch: the C oracle and a vectorized torch restatement on a row sample of
     the same inputs, on this host's cores, with a bit-for-bit check of the GPU's first call;
   - configs: the other configurations -- cfg1 (CPU only), cfg2, cfg4, cfg5 large (GB/s, fraction
-    of peak, traffic, pattern ceiling, CPU baseline, parity of the sampled rows) and cfg5 decode
-    (us per call, eager and replayed from a HIP graph).
+    of peak, traffic, pattern ceiling, CPU baseline, parity of the sampled rows), cfg5 decode
+    (us per call in fixed batches, eager and replayed from a HIP graph, beside the empty kernel
+    and the compute-free pattern at the same launch shape), and published_h1: the reference's
+    one published measurement (fused_add_rms_norm, 1024 x 512 fp16) timed at its own shape.
 Every configuration's inputs are generated on the CPU from torch.Generator().manual_seed(k) for
 configuration k and copied to the GPU, so the GPU, the oracle and the torch legs see the same bits
 (and the parity tests build the same inputs: tests import `config_inputs`).
@@ -68,6 +71,10 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run three 1 GiB device-to-device copies (a kernel of known "
                          "traffic, used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+    ap.add_argument("--pattern", default=None, choices=["natural", "4", "3", "2"],
+                    help="time only the workload's compute-free access-pattern kernel, at its "
+                         "natural occupancy or capped to 4, 3 or 2 workgroups per CU (for "
+                         "profiling the ceilings on their own); prints one JSON line")
     return ap.parse_args()
 
 
@@ -82,22 +89,26 @@ def config_inputs(name: str) -> dict:
       cfg4        x [16384, 7168]; w; smooth fp32 [7168] ~U(0.5, 2); eps 1e-6
       cfg5-decodeT x, r [T, 5120] (T in 1, 4, 16, 64); w; eps 1e-6
       cfg5-large  x, r [32768, 16384]; w; eps 1e-6
+      published-h1 x, r, w fp16 [1024, 512] (seed 6): the shape of the reference's only
+                  published measurement (fused_add_rms_norm, mxbench/README_MXBENCH.md:160-177)
     Returns a dict of CPU tensors (x, r or None, w, sm or None) and eps."""
     import torch
 
     spec = {"cfg1": (1, 256, 4096, False, 1e-6), "cfg2": (2, 4096, 4096, True, 1e-6),
             "cfg3": (3, 8192, 8192, True, 1e-5), "cfg4": (4, 16384, 7168, False, 1e-6),
             "cfg5-large": (5, 32768, 16384, True, 1e-6),
-            **{f"cfg5-decode{t}": (5, t, 5120, True, 1e-6) for t in DECODE_T}}
+            **{f"cfg5-decode{t}": (5, t, 5120, True, 1e-6) for t in DECODE_T},
+            "published-h1": (6, 1024, 512, True, 1e-6)}
     seed, T, H, res, eps = spec[name]
+    dt = torch.float16 if name == "published-h1" else torch.bfloat16
     g = torch.Generator().manual_seed(seed)
     idx = torch.randperm(H, generator=g)[: round(0.01 * H)] if name == "cfg3" else None
     x = torch.randn(T, H, generator=g)
     if idx is not None:
         x[:, idx] *= 20.0
-    x = x.to(torch.bfloat16)
-    r = torch.randn(T, H, generator=g).to(torch.bfloat16) if res else None
-    w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    x = x.to(dt)
+    r = torch.randn(T, H, generator=g).to(dt) if res else None
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(dt)
     sm = (0.5 + 1.5 * torch.rand(H, generator=g)) if name == "cfg4" else None
     return {"x": x, "r": r, "w": w, "sm": sm, "eps": eps}
 
@@ -111,8 +122,9 @@ class Workload:
 
     @property
     def seeded(self) -> bool:
-        """Inputs come from config_inputs (the configurations) rather than the device RNG."""
-        return self.name.startswith("cfg")
+        """Inputs come from config_inputs (the configurations and the reference's published
+        shape) rather than the device RNG."""
+        return self.name.startswith("cfg") or self.name == "published-h1"
 
     @property
     def pad(self) -> int:
@@ -248,6 +260,10 @@ WORKLOADS = {
     "cfg5-large": Workload("cfg5-large", 32768, 16384, 1e-6, "add_norm_int8"),
     **{f"cfg5-decode{t}": Workload(f"cfg5-decode{t}", t, 5120, 1e-6, "add_norm_int8")
        for t in DECODE_T},
+    # the reference's only published measurement: fused_add_rms_norm, 1024 x 512 fp16
+    # (mxbench/README_MXBENCH.md:160-177; byte model benchmark/fused_add_rms_norm_simple.py:57-61,
+    # 8TH + 2H = 4,195,328 B, the same as this workload's)
+    "published-h1": Workload("published-h1", 1024, 512, 1e-6, "fused_add"),
     # the standalone quantizers, at the headline shape (the step after an unfused norm)
     "ptq-int8": Workload("ptq-int8", 8192, 8192, 0.0, "ptq_int8"),
     "ptq-int8-azp": Workload("ptq-int8-azp", 8192, 8192, 0.0, "ptq_int8_azp"),
@@ -286,28 +302,88 @@ def kernel_name(wl) -> str:
     return KERNEL_NAME[wl.kind] + ("_wide" if wl.name.startswith("wide-") else "")
 
 
-# Compute-free kernels with a configuration's access pattern (include/mcop_pattern.h), at the
+# Compute-free kernels with a configuration's access pattern (bench_kernels/mcop_pattern.h), at the
 # launch shape the operator picks for it (vectors per lane, lanes per row).
 PATTERN_OF = {"cfg2": (1, 2, 256), "cfg3": (0, 2, 512), "cfg4": (2, 4, 256),
               "cfg5-large": (0, 4, 512)}
-PATTERN_COPY, PATTERN_READ, PATTERN_WRITE = 3, 4, 5
+PATTERN_COPY, PATTERN_READ, PATTERN_WRITE, PATTERN_EMPTY, PATTERN_EXACT = 3, 4, 5, 6, 7
 MIX_H = 2048  # row width of the reshaped ("mix") pattern: one 16-byte vector a lane, 256 lanes
+# LDS of a CU (bytes): a pattern launched with LDS_PER_CU // n - 1024 bytes of unused dynamic LDS
+# per workgroup (the 1 KiB margin covers the kernel's own reduction slots) has at most n
+# workgroups on a CU
+LDS_PER_CU = 163840
 
 
 # ------------------------------------------------------------------------------ profiles
-def profile_summary(wl: Workload):
+# The files whose text decides each kernel's code: its translation units (mcoplib_amd/csrc), the
+# device helpers and the launch-shape choice every kernel shares, and the hipcc flags.  A
+# profile summary records the hash of these at the time it was taken (kernel_source_sha16), so
+# a figure measured on other code is reported as stale instead of vouching for the current one.
+KERNEL_SOURCES = {
+    "k_rms_norm_quant": ["rms_norm_quant.hip"],
+    "k_fused_add_rms_norm": ["fused_add_rms_norm.hip"],
+    "k_rms_norm_smooth_quant": ["smooth_quant_kernel.h", "rms_norm_smooth_quant.hip",
+                                "rms_norm_smooth_quant_bf16.hip", "rms_norm_smooth_quant_f16.hip"],
+    "k_scale_dynamic_quant": ["scale_dynamic_quant.hip"],
+    "k_per_token_quant": ["per_token_quant.hip"],
+    "k_add_rms_norm_quant_padded": ["padded_quant.hip"],
+    "k_rms_norm_group_quant": ["group_quant.hip"],
+    "k_rms_norm": ["norm_kernel.h", "rms_norm.hip", "rms_norm_bf16.hip", "rms_norm_f16.hip"],
+}
+SHARED_SOURCES = ["rowkern.h", "numerics.h", "abi.hip"]
+
+
+def kernel_source_hash(kernel: str, root: Path = ROOT) -> str:
+    """First 16 hex digits of the SHA-256 over a kernel's source files (name and text, in name
+    order) and the hipcc flags of mcoplib_amd/_build.py (`kernel` may carry the _wide suffix of
+    the multi-pass form, which lives in the same files)."""
+    import hashlib
+
+    base = kernel[:-len("_wide")] if kernel.endswith("_wide") else kernel
+    h = hashlib.sha256()
+    for name in sorted(KERNEL_SOURCES[base] + SHARED_SOURCES):
+        h.update(name.encode() + b"\0")
+        h.update((root / "mcoplib_amd" / "csrc" / name).read_bytes())
+    build = (root / "mcoplib_amd" / "_build.py").read_text()
+    flags = re.search(r"^COMPILE_FLAGS = \[.*?^\]", build, re.M | re.S)
+    h.update(flags.group(0).encode() if flags else b"")
+    return h.hexdigest()[:16]
+
+
+def profile_summary(wl: Workload, root: Path = ROOT):
     """Figures of the committed rocprofv3 summary profiles/<kernel>_<workload>.txt: HBM bytes per
-    dispatch (FETCH_SIZE + WRITE_SIZE passes, each scaled by a copy kernel's reading) and the
-    kernel-trace mean of the timed launches; None where absent."""
-    p = ROOT / "profiles" / f"{kernel_name(wl)}_{wl.name}.txt"
+    dispatch (FETCH_SIZE + WRITE_SIZE passes, each scaled by a copy kernel's reading), the
+    kernel-trace mean of the timed launches, and whether the summary was taken on the current
+    sources (`stale`: its recorded kernel_source_sha16 differs from the current hash, or it has
+    none); None where absent."""
+    p = root / "profiles" / f"{kernel_name(wl)}_{wl.name}.txt"
     if not p.exists():
         return None
     t = p.read_text()
     m = re.search(r"^hbm_bytes_per_dispatch:\s*([0-9.eE+]+)", t, re.M)
     k = re.search(r"^timed legs \((\d+) dispatches\): mean ([0-9.]+) us", t, re.M)
-    return {"file": str(p.relative_to(ROOT)),
+    h = re.search(r"^kernel_source_sha16:\s*([0-9a-f]{16})\s*$", t, re.M)
+    current = kernel_source_hash(kernel_name(wl), root)
+    return {"file": str(p.relative_to(root)),
             "hbm_bytes_per_dispatch": float(m.group(1)) if m else None,
-            "trace_mean_us": float(k.group(2)) if k else None}
+            "trace_mean_us": float(k.group(2)) if k else None,
+            "source_sha16": h.group(1) if h else None, "current_source_sha16": current,
+            "stale": h is None or h.group(1) != current}
+
+
+def guard_of(frac: float, prof, traffic_bytes: int) -> dict:
+    """The headline's regression guard: `regressed` when the fraction of the 8 TB/s peak falls
+    under FRAC_GUARD, when the committed profile's traffic exceeds TRAFFIC_GUARD times the
+    algorithmic bytes, or when that profile is missing or stale (taken on other sources, so its
+    traffic figure says nothing about the code that ran)."""
+    tr = (round(prof["hbm_bytes_per_dispatch"] / traffic_bytes, 4)
+          if prof and prof["hbm_bytes_per_dispatch"] else None)
+    stale = prof is None or prof["stale"]
+    return {"frac_min": FRAC_GUARD, "traffic_ratio_max": TRAFFIC_GUARD, "frac": frac,
+            "traffic_ratio": tr, "profile_stale": stale,
+            "profile_source_sha16": prof["source_sha16"] if prof else None,
+            "current_source_sha16": prof["current_source_sha16"] if prof else None,
+            "regressed": bool(frac < FRAC_GUARD or tr is None or tr > TRAFFIC_GUARD or stale)}
 
 
 # ------------------------------------------------------------------------------ GPU timing
@@ -361,13 +437,14 @@ def graph_us(torch, launches, K):
 
 
 class Pattern:
-    """ctypes binding of libmcop_pattern.so (compute-free access-pattern kernels)."""
+    """ctypes binding of bench_kernels/libmcop_pattern.so (compute-free access-pattern kernels
+    and an empty kernel; bench_kernels/mcop_pattern.h)."""
 
     def __init__(self):
         import ctypes
-        path = ROOT / "mcoplib_amd" / "libmcop_pattern.so"
+        path = ROOT / "bench_kernels" / "libmcop_pattern.so"
         if not path.exists():
-            raise RuntimeError(f"{path} is not built (python mcoplib_amd/_build.py)")
+            raise RuntimeError(f"{path} is not built (python bench_kernels/build.py)")
         self.lib = ctypes.CDLL(str(path))
         P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
         self.lib.mcop_pattern.argtypes = [I, P, P, P, P, P, P, P, P, I64, I64, I, I, I, P]
@@ -375,15 +452,15 @@ class Pattern:
         self.lib.mcop_pattern_last_error.restype = ctypes.c_char_p
 
     def launcher(self, torch, pattern, d, T, H, nv, tpr, lds=0):
+        """A launch of `pattern` on torch's current stream at call time (so it can be captured
+        into a HIP graph like the operators)."""
         def p(t):
             return None if t is None else t.data_ptr()
-        stream = torch.cuda.current_stream().cuda_stream
         args = (pattern, p(d.get("x")), p(d.get("r")), p(d.get("w")), p(d.get("sm")),
-                p(d.get("o0")), p(d.get("o1")), p(d.get("q")), p(d.get("s")), T, H, nv, tpr,
-                lds, stream)
+                p(d.get("o0")), p(d.get("o1")), p(d.get("q")), p(d.get("s")), T, H, nv, tpr, lds)
 
         def run():
-            rc = self.lib.mcop_pattern(*args)
+            rc = self.lib.mcop_pattern(*args, torch.cuda.current_stream().cuda_stream)
             if rc != 0:
                 raise RuntimeError(self.lib.mcop_pattern_last_error().decode())
         return run
@@ -620,6 +697,7 @@ def config_entry(torch, wl: Workload, args, dev, pat, entry: str):
     if prof:
         out["profile"] = prof["file"]
         out["rocprof_trace_mean_us"] = prof["trace_mean_us"]
+        out["profile_stale"] = prof["stale"]
         if prof["hbm_bytes_per_dispatch"]:
             out["traffic_ratio"] = round(prof["hbm_bytes_per_dispatch"] / wl.bytes, 4)
     if pat is not None and wl.name in PATTERN_OF:
@@ -631,29 +709,227 @@ def config_entry(torch, wl: Workload, args, dev, pat, entry: str):
         mus = mix_us(torch, pat, wl, dev, args.steps)
         out["mix_us"] = round(mus, 3)
         out["kernel_vs_mix"] = round(mus / us, 4)
+        if wl.name == "cfg4":
+            # cfg 4's compute-free pattern streams faster with fewer workgroups per CU (capped by
+            # unused LDS) while the kernel, at four per CU by its registers, needs its waves to
+            # hide its arithmetic: the pattern at the kernel's occupancy and below it
+            caps = {}
+            for per_cu in (4, 3):
+                cu = pattern_us(torch, pat, p, wl.T, wl.H, nv, tpr, dev, args.steps,
+                                with_w=True, with_sm=True, lds=LDS_PER_CU // per_cu - 1024)
+                caps[f"{per_cu}_per_cu"] = {"us": round(cu, 3),
+                                            "kernel_vs_pattern": round(cu / us, 4)}
+            out["pattern_capped_occupancy"] = caps
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(wl, cpu, min(wl.T, 512), args.cpu_seconds / 3,
                                            m["first"])
     return out
 
 
-def decode_entry(torch, args, dev):
-    """cfg5 decode: us per call, eager (K back-to-back calls between events) and replayed from
-    a HIP graph, for T in DECODE_T at H = 5120; the C oracle on one thread beside it."""
+# Latency-bound calls are timed in fixed batches, independent of --steps: DECODE_CALLS calls per
+# batch, DECODE_BATCHES batches, the median batch reported with the fastest and slowest.
+DECODE_CALLS, DECODE_BATCHES = 500, 7
+
+
+def _batches(run_batch, batches=DECODE_BATCHES) -> dict:
+    """us per call over `batches` runs of run_batch(): median, min and max (3 decimals)."""
+    v = sorted(run_batch() for _ in range(batches))
+    return {"median": round(v[len(v) // 2], 3), "min": round(v[0], 3), "max": round(v[-1], 3)}
+
+
+def eager_batch(torch, launches, n=DECODE_CALLS):
+    """A batch of n back-to-back eager launches between two events; returns us per call."""
+    def run():
+        torch.cuda.synchronize()
+        e0, e1 = _ev(torch), _ev(torch)
+        e0.record()
+        for i in range(n):
+            launches[i % len(launches)]()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / n
+    return run
+
+
+def graph_batch(torch, launches, n=DECODE_CALLS):
+    """n launches captured into one HIP graph; each run replays it between two events and
+    returns us per call."""
+    g = torch.cuda.CUDAGraph()
+    s_cap = torch.cuda.Stream()
+    s_cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s_cap):
+        with torch.cuda.graph(g, stream=s_cap):
+            for i in range(n):
+                launches[i % len(launches)]()
+    torch.cuda.current_stream().wait_stream(s_cap)
+    g.replay()
+    torch.cuda.synchronize()
+
+    def run():
+        e0, e1 = _ev(torch), _ev(torch)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / n
+    run.graph = g  # keep the graph alive with the closure
+    return run
+
+
+def decode_floor_launches(torch, pat, T, H, dev, n_sets=3):
+    """Launchers of the decode floor kernels at the operator's exact-row launch shape (two
+    vectors a lane over H/16 lanes, one row per workgroup): the empty kernel (the launch floor)
+    and the compute-free add-norm-quant pattern in the exact-row form (loads of x, r, w; the
+    residual store; two row reductions; codes and scale stores)."""
+    nv, tpr = 2, H // 16
+    sets = []
+    for _ in range(n_sets):
+        sets.append({"x": torch.zeros(T, H, dtype=torch.bfloat16, device=dev),
+                     "r": torch.zeros(T, H, dtype=torch.bfloat16, device=dev),
+                     "w": torch.ones(H, dtype=torch.bfloat16, device=dev),
+                     "o0": torch.empty(T, H, dtype=torch.bfloat16, device=dev),
+                     "q": torch.empty(T, H, dtype=torch.uint8, device=dev),
+                     "s": torch.empty(T, dtype=torch.float32, device=dev)})
+    empty = [pat.launcher(torch, PATTERN_EMPTY, {}, T, H, nv, tpr)]
+    exact = [pat.launcher(torch, PATTERN_EXACT, d, T, H, nv, tpr) for d in sets]
+    return empty, exact, sets
+
+
+def decode_entry(torch, args, dev, pat):
+    """cfg5 decode, T in DECODE_T at H = 5120: us per call in fixed batches (eager: back-to-back
+    calls through the operator surface; graph: the same calls replayed from a HIP graph), next to
+    the floor of what one such call can cost on this GPU -- the empty kernel at the operator's
+    launch shape and the compute-free exact-row pattern of its loads, reductions and stores, both
+    graph-replayed the same way -- and the C oracle on one thread.  The batches of every shape and
+    kind are interleaved (round r runs batch r of each), so slow phases of the host affect every
+    figure alike rather than whichever shape was running."""
     out = {"entry": "mcoplib.op.rms_norm_dynamic_per_token_quant_custom with residual",
-           "hidden": 5120}
+           "hidden": 5120, "timing": f"{DECODE_BATCHES} interleaved batches of {DECODE_CALLS} "
+                                     "calls per figure, median batch (min, max) in us per call",
+           "launch_shape": "two 16-byte vectors a lane, 320 lanes, one row per workgroup"}
+    runs, keep = {}, []
     for t in DECODE_T:
         wl = WORKLOADS[f"cfg5-decode{t}"]
         cpu = config_inputs(wl.name)
-        m = measure(torch, wl, args, dev, cpu, check_rows=t, hot=False, warmup_s=0.3)
-        e = {"eager_us": round(m["ms"] * 1e3, 3), "graph_us": round(m["graph_us"], 3),
-             "algorithmic_bytes": wl.bytes}
+        sets = wl.device_sets(torch, dev, 3, cpu)
+        first = first_call_outputs(torch, wl, sets[0], t)
+        launches = [wl.launcher(torch, d) for d in sets]
+        for i in range(200):
+            launches[i % 3]()
+        runs[(t, "eager")] = eager_batch(torch, launches)
+        runs[(t, "graph")] = graph_batch(torch, launches)
+        if pat is not None:
+            empty, exact, psets = decode_floor_launches(torch, pat, t, wl.H, dev)
+            runs[(t, "floor")] = graph_batch(torch, empty)
+            runs[(t, "pattern")] = graph_batch(torch, exact)
+            keep.append(psets)
+        keep.append(sets)
+        e = {"algorithmic_bytes": wl.bytes}
         if not args.no_cpu:
-            cb = cpu_baseline(wl, cpu, t, 1.0, m["first"], threads=1)
+            cb = cpu_baseline(wl, cpu, t, 1.0, first, threads=1)
             e["cpu_us"] = cb["us_per_call"]
             e["cpu_cores"] = 1
             e["gpu_first_call_vs_oracle"] = cb["gpu_first_call_vs_oracle"]
         out[f"T{t}"] = e
+    got = {k: [] for k in runs}
+    for _ in range(DECODE_BATCHES):
+        for k, run in runs.items():
+            got[k].append(run())
+    for (t, kind), v in got.items():
+        v = sorted(v)
+        e = out[f"T{t}"]
+        e[f"{kind}_us"] = round(v[len(v) // 2], 3)
+        e[f"{kind}_us_min_max"] = [round(v[0], 3), round(v[-1], 3)]
+    for t in DECODE_T:
+        e = out[f"T{t}"]
+        if "floor_us" in e:
+            e["kernel_vs_floor"] = round(e["floor_us"] / e["graph_us"], 4)
+            e["kernel_vs_pattern"] = round(e["pattern_us"] / e["graph_us"], 4)
+    eagers = [out[f"T{t}"]["eager_us"] for t in DECODE_T]
+    out["eager_spread"] = round(max(eagers) / min(eagers) - 1, 4)
+    del runs, keep
+    torch.cuda.empty_cache()
+    return out
+
+
+# The reference's only published figure for this path: fused_add_rms_norm, T = 1024, H = 512,
+# fp16, "GPU time (cold)" on four MetaX C280 devices (56 SMs, 1843 GB/s bus peak), measured by
+# benchmark/fused_add_rms_norm_simple.py under its nvbench fork.
+PUBLISHED_H1 = {"device": "MetaX C280", "gpu_us_cold": [62.880, 55.262, 41.581, 41.773],
+                "bytes_per_call": 4195328,
+                "source": "mxbench/README_MXBENCH.md:162,167,172,177 (bytes: "
+                          "benchmark/fused_add_rms_norm_simple.py:57-61)"}
+
+
+def published_entry(torch, args, dev):
+    """torch.ops._C.fused_add_rms_norm at the reference's published shape (1024 x 512 fp16,
+    eps 1e-6), timed as nvbench times its samples: one launch between an event pair, with the
+    stream held busy while the host enqueues them (so the pair measures the GPU, not the host's
+    launch latency).  Cold: each sample follows a 512 MiB fill, which evicts the inputs from L2
+    and the 256 MB Infinity Cache (nvbench's cold samples flush the L2 the same way); hot: each
+    sample follows a clock-bounded spin kernel (torch.cuda._sleep) on inputs already in cache.
+    Also back to back and replayed from a HIP graph; GB/s on the reference's byte model; the
+    ratio of the reference's published GPU times to this cold median; the GPU's first call
+    against the C oracle."""
+    wl = WORKLOADS["published-h1"]
+    cpu = config_inputs(wl.name)
+    ref = oracle_call(wl, cpu) if not args.no_cpu else None
+    sets = wl.device_sets(torch, dev, 4, cpu)
+    first = first_call_outputs(torch, wl, sets[0], wl.T)
+    launches = [wl.launcher(torch, d) for d in sets]
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    for i in range(64):
+        launches[i % len(launches)]()
+    torch.cuda.synchronize()
+    n = 256
+
+    def samples(before):
+        ev = [(_ev(torch), _ev(torch)) for _ in range(n)]
+        for i in range(n):
+            before()
+            ev[i][0].record()
+            launches[i % len(launches)]()
+            ev[i][1].record()
+        torch.cuda.synchronize()
+        v = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
+        return {"median": round(v[n // 2], 3), "p10": round(v[n // 10], 3),
+                "p90": round(v[9 * n // 10], 3)}
+    cold = samples(lambda: flush.zero_())
+    hot = samples(lambda: torch.cuda._sleep(100000))
+    b2b = _batches(eager_batch(torch, launches, 1024), 5)
+    graph = _batches(graph_batch(torch, launches, 1024), 5)
+    props = torch.cuda.get_device_properties(0)
+    pub = PUBLISHED_H1["gpu_us_cold"]
+    out = {"entry": "torch.ops._C.fused_add_rms_norm (in place), fp16", "kernel": kernel_name(wl),
+           "shape": [wl.T, wl.H], "dtype": "fp16", "bytes_per_call": wl.bytes,
+           "device": f"{torch.cuda.get_device_name(0)} ({props.gcnArchName.split(':')[0]}, "
+                     f"{props.multi_processor_count} CUs)",
+           "cold_us": cold, "hot_us": hot,
+           "back_to_back_us": b2b["median"], "graph_us": graph["median"],
+           "GBs_cold": round(wl.bytes / (cold["median"] * 1e-6) / 1e9, 1),
+           "GBs_graph": round(wl.bytes / (graph["median"] * 1e-6) / 1e9, 1),
+           "published": PUBLISHED_H1,
+           "vs_published": {"what": "reference GPU time (cold) / this GPU's cold median, per "
+                                    "published device (higher = faster here); different GPUs "
+                                    "and vendors, so context rather than a like-for-like target",
+                            "ratios": [round(p / cold["median"], 2) for p in pub],
+                            "min": round(min(pub) / cold["median"], 2),
+                            "max": round(max(pub) / cold["median"], 2)},
+           "timing": f"{n} samples of one launch between an event pair (cold: after a 512 MiB "
+                     f"fill; hot: after a spin kernel); back-to-back and graph: median of 5 "
+                     f"batches of 1024 calls"}
+    if ref is not None:
+        diffs = {k: int((first[k].view(torch.int16) != ref[k].view(torch.int16)).sum())
+                 for k in ("x", "r")}
+        out["gpu_first_call_vs_oracle"] = {"rows": wl.T, "differing_values": diffs,
+                                           "bit_exact": all(v == 0 for v in diffs.values())}
+    prof = profile_summary(wl)
+    if prof:
+        out["profile"] = prof["file"]
+        out["rocprof_trace_mean_us"] = prof["trace_mean_us"]
+        out["profile_stale"] = prof["stale"]
+    del sets, launches, flush
+    torch.cuda.empty_cache()
     return out
 
 
@@ -709,6 +985,20 @@ def main() -> int:
         print("bench.py: cfg1 is measured on the CPU only (it is part of the default run's "
               "`configs`)", file=sys.stderr)
         return 2
+    if args.pattern is not None:
+        if wl.name not in PATTERN_OF:
+            print(f"bench.py: {wl.name} has no access-pattern kernel (those of "
+                  f"{sorted(PATTERN_OF)} do)", file=sys.stderr)
+            return 2
+        p, nv, tpr = PATTERN_OF[wl.name]
+        lds = 0 if args.pattern == "natural" else LDS_PER_CU // int(args.pattern) - 1024
+        pus = pattern_us(torch, Pattern(), p, wl.T, wl.H, nv, tpr, dev, args.steps, with_w=True,
+                         with_sm=wl.kind == "smooth_fp8", lds=lds)
+        print(json.dumps({"workload": wl.name, "pattern": p, "vectors_per_lane": nv,
+                          "lanes_per_row": tpr, "workgroups_per_cu": args.pattern,
+                          "lds_bytes": lds, "us": round(pus, 3),
+                          "GBs": round(wl.bytes / (pus * 1e-6) / 1e9, 1)}), flush=True)
+        return 0
 
     cpu = config_inputs(wl.name) if wl.seeded else None
     check_rows = min(wl.T, 1024) if (wl.seeded and not args.no_cpu) else 0
@@ -743,7 +1033,8 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic: seeded CPU inputs copied to the GPU, the same bits in every leg"
                 if wl.seeded else "synthetic: device-RNG inputs",
-        "config": {"workload": f"{wl.name}: {wl.kind} T={wl.T} H={wl.H} bf16 in"
+        "config": {"workload": f"{wl.name}: {wl.kind} T={wl.T} H={wl.H} "
+                               f"{'fp16' if wl.name == 'published-h1' else 'bf16'} in"
                                + ("" if wl.kind.startswith("ptq_") or wl.kind == "sdq" else f", eps={wl.eps}")
                                + (", 1% outlier channels x20" if wl.name == "cfg3" else ""),
                    "tokens": wl.T, "hidden": wl.H, "io": "bf16 -> int8/fp8 + fp32 scales",
@@ -757,12 +1048,9 @@ def main() -> int:
         "us_per_call": round(kernel_us, 3),
         "us_per_call_graph": None if "graph_us" not in m else round(m["graph_us"], 3),
     }
+    roof["profile_stale"] = prof["stale"] if prof else None
     if wl.name == "cfg3":
-        tr = roof["traffic_ratio"]
-        out["guard"] = {"frac_min": FRAC_GUARD, "traffic_ratio_max": TRAFFIC_GUARD,
-                        "frac": roof["frac"], "traffic_ratio": tr,
-                        "regressed": bool(roof["frac"] < FRAC_GUARD or tr is None
-                                          or tr > TRAFFIC_GUARD)}
+        out["guard"] = guard_of(roof["frac"], prof, wl.bytes)
     pat = None
     if not args.no_configs:
         pat = Pattern()
@@ -808,10 +1096,13 @@ def main() -> int:
         cfgs["cfg4"] = config_entry(torch, WORKLOADS["cfg4"], args, dev, pat,
                                     "mcoplib.op.rms_norm_dynamic_per_token_quant (SmoothQuant, "
                                     "fp8-e4m3fn, after_res + after_norm)")
-        cfgs["cfg5_decode"] = decode_entry(torch, args, dev)
+        cfgs["cfg5_decode"] = decode_entry(torch, args, dev, pat)
         cfgs["cfg5_large"] = config_entry(torch, WORKLOADS["cfg5-large"], args, dev, pat,
                                           "mcoplib.op.rms_norm_dynamic_per_token_quant_custom "
                                           "with residual")
+        # the reference's one published number sits on another GPU and another shape than the
+        # headline metric, so `vs_baseline` stays null; the comparison at its own shape is here
+        cfgs["published_h1"] = published_entry(torch, args, dev)
         out["configs"] = cfgs
     print(json.dumps(out), flush=True)
     return 0

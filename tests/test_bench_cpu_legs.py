@@ -65,3 +65,68 @@ def test_config_inputs_follow_the_recipe():
     # deterministic: the same bits every time
     assert torch.equal(bench.config_inputs("cfg5-decode4")["x"],
                        bench.config_inputs("cfg5-decode4")["x"])
+
+
+def _guard_tree(tmp_path):
+    """A copy of the sources the headline kernel's hash covers, with a profile summary of the
+    headline workload that records their current hash."""
+    import shutil
+    from pathlib import Path
+
+    src = Path(bench.ROOT)
+    (tmp_path / "mcoplib_amd").mkdir()
+    shutil.copytree(src / "mcoplib_amd" / "csrc", tmp_path / "mcoplib_amd" / "csrc")
+    shutil.copy(src / "mcoplib_amd" / "_build.py", tmp_path / "mcoplib_amd" / "_build.py")
+    (tmp_path / "profiles").mkdir()
+    wl = bench.WORKLOADS["cfg3"]
+    h = bench.kernel_source_hash("k_rms_norm_quant", tmp_path)
+    (tmp_path / "profiles" / "k_rms_norm_quant_cfg3.txt").write_text(
+        "# k_rms_norm_quant on cfg3\n"
+        f"kernel_source_sha16: {h}\n"
+        "timed legs (200 dispatches): mean 76.310 us, median 76.151 us\n"
+        f"hbm_bytes_per_dispatch: {int(wl.bytes * 1.0009)}\n")
+    return tmp_path, wl
+
+
+def test_guard_flags_a_profile_of_other_sources(tmp_path):
+    """The headline guard trusts the committed profile's traffic only while the kernel's sources
+    are the ones it was taken on: editing rms_norm_quant.hip (or a header every kernel shares, or
+    the compile flags) without re-profiling marks the profile stale and the run regressed."""
+    root, wl = _guard_tree(tmp_path)
+    prof = bench.profile_summary(wl, root)
+    assert prof["stale"] is False
+    g = bench.guard_of(0.7651, prof, wl.bytes)
+    assert g["regressed"] is False and g["profile_stale"] is False
+    assert g["traffic_ratio"] == 1.0009
+    # an edit to the kernel's own source
+    k = root / "mcoplib_amd" / "csrc" / "rms_norm_quant.hip"
+    k.write_text(k.read_text() + "\n// edited after the profile was taken\n")
+    prof = bench.profile_summary(wl, root)
+    assert prof["stale"] is True
+    g = bench.guard_of(0.7651, prof, wl.bytes)
+    assert g["regressed"] is True and g["profile_stale"] is True
+    # re-profiling (a summary recording the new hash) clears it; a shared header edit sets it
+    p = root / "profiles" / "k_rms_norm_quant_cfg3.txt"
+    p.write_text(p.read_text().replace(prof["source_sha16"], prof["current_source_sha16"]))
+    assert bench.profile_summary(wl, root)["stale"] is False
+    hdr = root / "mcoplib_amd" / "csrc" / "rowkern.h"
+    hdr.write_text(hdr.read_text() + "\n")
+    assert bench.profile_summary(wl, root)["stale"] is True
+    # an unrelated kernel's source does not touch the headline's hash
+    p.write_text(p.read_text().replace(
+        bench.profile_summary(wl, root)["source_sha16"],
+        bench.kernel_source_hash("k_rms_norm_quant", root)))
+    other = root / "mcoplib_amd" / "csrc" / "scale_dynamic_quant.hip"
+    other.write_text(other.read_text() + "\n")
+    assert bench.profile_summary(wl, root)["stale"] is False
+
+
+def test_guard_without_a_profile_or_below_the_bar():
+    wl = bench.WORKLOADS["cfg3"]
+    assert bench.guard_of(0.77, None, wl.bytes)["regressed"] is True
+    prof = {"hbm_bytes_per_dispatch": wl.bytes * 1.0009, "stale": False, "source_sha16": "x",
+            "current_source_sha16": "x"}
+    assert bench.guard_of(0.7499, prof, wl.bytes)["regressed"] is True
+    assert bench.guard_of(0.7501, prof, wl.bytes)["regressed"] is False
+    prof["hbm_bytes_per_dispatch"] = wl.bytes * 1.02
+    assert bench.guard_of(0.77, prof, wl.bytes)["regressed"] is True
