@@ -46,9 +46,11 @@ def _load() -> ctypes.CDLL:
     lib.mcop_rms_norm_dynamic_per_token_quant_custom.argtypes = [P, P, P, P, P, P, I64, I64, I,
                                                                   F, P]
     lib.mcop_debug_set_launch_override.argtypes = [I, I]
+    lib.mcop_debug_set_split_rows.argtypes = [I]
     for fn in ("mcop_fused_add_rms_norm", "mcop_rms_norm_dynamic_per_token_quant",
                "mcop_rms_norm_smooth_quant", "mcop_scale_dynamic_quant",
-               "mcop_fp8_e4m3fn_from_f32", "mcop_debug_set_launch_override", "mcop_abi_version",
+               "mcop_fp8_e4m3fn_from_f32", "mcop_debug_set_launch_override",
+               "mcop_debug_set_split_rows", "mcop_abi_version",
                "mcop_dynamic_scaled_int8_quant", "mcop_dynamic_per_token_scaled_fp8_quant",
                "mcop_fused_add_rms_norm_dynamic_per_token_quant_padding_output",
                "mcop_rms_norm_per_block_quant", "mcop_rms_norm", "mcop_head_rms_norm",
@@ -90,3 +92,10 @@ def set_launch_override(vectors_per_lane: int = 0, lanes_per_row: int = 0) -> No
     """Force the row kernels' launch shape for later calls from this thread (0, 0 = automatic;
     a debug hook for tests and tuning). Results do not change."""
     check(lib.mcop_debug_set_launch_override(int(vectors_per_lane), int(lanes_per_row)))
+
+
+def set_split_rows(enabled: bool = True) -> None:
+    """Whether rows too wide for one workgroup's registers may take the split-row kernels (the
+    default) or always the multi-pass kernels, for later calls from this thread (a debug hook
+    for tests and A/B timing). Results do not change."""
+    check(lib.mcop_debug_set_split_rows(1 if enabled else 0))

@@ -2,6 +2,7 @@
 // launch geometry, the (debug) launch-shape override.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -12,6 +13,7 @@
 #include "../../include/mcop_norm.h"
 #include "mcop_testing.h"
 #include "rowkern.h"
+#include "split_row.h"
 
 namespace mcop {
 
@@ -20,6 +22,8 @@ thread_local char g_err[512] = "";
 // launch-shape override of the calling thread (mcop_debug_set_launch_override)
 thread_local int g_over_nv = 0;
 thread_local int g_over_tpr = 0;
+// split-row kernels switched off for the calling thread (mcop_debug_set_split_rows)
+thread_local int g_no_split = 0;
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t round64(int64_t a) { return ceil_div(a, 64) * 64; }
@@ -150,6 +154,8 @@ bool row_fits(int64_t hidden, int vec, KernelOfNv kernels, int min_tpr) {
   return false;
 }
 
+bool split_rows_enabled() { return g_no_split == 0; }
+
 bool exact_form_ok(const void* ex_kernel) {
   const KernelInfo k = kernel_info(ex_kernel);
   if (k.ok && !k.spills) return true;
@@ -159,6 +165,79 @@ bool exact_form_ok(const void* ex_kernel) {
     fflush(stdout);
   }
   return false;
+}
+
+__global__ void __launch_bounds__(256) k_fill_u64(uint64_t* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+namespace {
+// The wall clock's rate of a device in kHz (cached), for the split-row kernels' wait bound.
+int wall_clock_khz(int dev) {
+  static std::mutex mu;
+  static int cache[64];
+  if (dev < 0 || dev >= 64) return 0;
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    if (cache[dev] > 0) return cache[dev];
+  }
+  int clk = 0;
+  if (hipDeviceGetAttribute(&clk, hipDeviceAttributeWallClockRate, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  cache[dev] = clk;
+  return clk;
+}
+}  // namespace
+
+bool split_plan(const void* kernel, int64_t rows, int64_t nvec, hipStream_t st, SplitPlan* p) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  if (cs != hipStreamCaptureStatusNone) return false;  // graphs take the multi-pass kernel
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  const int clk = wall_clock_khz(dev);
+  const int64_t slices = ceil_div(nvec, kSplitVecs);
+  if (clk <= 0 || slices < 2 || slices > kSplitMaxSlices) return false;
+  const int64_t slice_vecs = ceil_div(nvec, slices);
+  const int64_t lanes = round64(ceil_div(slice_vecs, kSplitNv));
+  if (blocks_per_cu(kernel, (int)lanes) < 1) return false;  // spills (or cannot launch)
+  p->slices = (int)slices;
+  p->slice_vecs = (int)slice_vecs;
+  p->lanes = (int)lanes;
+  p->chunk_rows = std::min<int64_t>(rows, (kSplitWsWords - 1) / (4 * slices));
+  p->ws_words = split_ws_words(p->chunk_rows, (int)slices);
+  p->timeout_ticks = (int64_t)clk * 250;  // 250 ms of the wall clock
+  return true;
+}
+
+int split_launch(const char* op, const void* kernel, void** args, const SplitPlan& p,
+                 int64_t rows, uint64_t* ws, hipStream_t st) {
+  const int64_t words = split_ws_words(rows, p.slices);
+  hipLaunchKernelGGL(k_fill_u64, dim3((unsigned)ceil_div(words, 256)), dim3(256), 0, st, ws,
+                     words);
+  if (int rc = check_launch(op)) return rc;
+  const hipError_t e = hipLaunchKernel(kernel, dim3((unsigned)(rows * p.slices)),
+                                       dim3((unsigned)p.lanes), args, 0, st);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(MCOP_E_LAUNCH, "%s: kernel launch failed: %s", op, hipGetErrorString(e));
+  }
+  if (trace_enabled()) {
+    fprintf(stdout, "[mcop] %s rows=%lld: split-row kernel, %d slices of %d vectors over %d "
+            "lanes\n", op, (long long)rows, p.slices, p.slice_vecs, p.lanes);
+    fflush(stdout);
+  }
+  return MCOP_OK;
 }
 
 bool wide_rows_ok(const char* op, int64_t rows) {
@@ -279,6 +358,11 @@ int mcop_debug_set_launch_override(int vectors_per_lane, int lanes_per_row) {
   }
   mcop::g_over_nv = vectors_per_lane;
   mcop::g_over_tpr = lanes_per_row;
+  return MCOP_OK;
+}
+
+int mcop_debug_set_split_rows(int enabled) {
+  mcop::g_no_split = enabled ? 0 : 1;
   return MCOP_OK;
 }
 

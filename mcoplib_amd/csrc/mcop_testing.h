@@ -27,6 +27,13 @@ int mcop_fp8_e4m3fn_from_f32(uint8_t* out, const float* in, int64_t n, float mul
  * the row does not fit falls back to automatic. Results do not change, only speed. */
 int mcop_debug_set_launch_override(int vectors_per_lane, int lanes_per_row);
 
+/* Whether later calls made BY THE CALLING THREAD may run rows too wide for one workgroup's
+ * registers on a split-row kernel (the row shared by several co-resident workgroups that
+ * exchange partial sums through a device workspace; the default, enabled = 1) or always on the
+ * operator's multi-pass kernel (enabled = 0), for the tests that check both kernels and for A/B
+ * timing. Results do not change, only speed. */
+int mcop_debug_set_split_rows(int enabled);
+
 #ifdef __cplusplus
 }
 #endif

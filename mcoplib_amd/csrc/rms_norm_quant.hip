@@ -26,11 +26,13 @@
 // written once (7*H + 4 bytes per bf16 row with residual).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cfloat>
 #include <type_traits>
 
 #include "../../include/mcop_norm.h"
 #include "rowkern.h"
+#include "split_row.h"
 
 namespace mcop {
 
@@ -354,6 +356,146 @@ k_rms_norm_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
   }
 }
 
+// Rows too wide for one workgroup's registers, read once: the row is split into `slices` slices
+// of `slice_vecs` vectors, one per workgroup -- workgroup b takes slice b % slices of row
+// b / slices -- each holding its slice in registers (NV vectors a lane, the lane mapping of the
+// register kernels within the slice).  The row's sum of squares and absmax are the slices'
+// partials combined through the workspace `ws` (split_row.h: split_sum in slice order,
+// split_max); every other step is the register kernel's, element by element.
+template <class E, int VEC, int NV, bool FP8, bool RES, int MODE>
+__global__ void __launch_bounds__(max_tpr(VEC, NV))
+k_rms_norm_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
+                       const typename E::S* __restrict__ x, const typename E::S* __restrict__ w,
+                       const float* __restrict__ scale_ub, typename E::S* __restrict__ res,
+                       int64_t rows, int hidden, int slices, int slice_vecs, float eps,
+                       uint64_t* __restrict__ ws, int64_t timeout_ticks) {
+  static_assert(MODE != QM_MC_7168, "7168-wide rows fit the register-resident kernel");
+  using S = typename E::S;
+  __shared__ double red_sum[16];
+  __shared__ float red_max[16];
+  __shared__ double x_sum;
+  __shared__ float x_max;
+  const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x;
+  const int lt = (int)threadIdx.x;
+  const int sl = (int)(blockIdx.x % (unsigned)slices);
+  const int64_t row = blockIdx.x / (unsigned)slices;
+  const int j0 = sl * slice_vecs;                   // the slice's first vector
+  const int jn = min(slice_vecs, nvec - j0);        // vectors in the slice
+  uint64_t* err = ws + split_ws_words(rows, slices) - 1;
+  const int64_t base = row * (int64_t)hidden;
+  // the lane's vector v: element offset in the row (lanes past the slice end re-read the
+  // slice's first vector, which does not count)
+  auto in_of = [&](int v) { return vec_index(v, tpr, lt) < jn; };
+  auto lj_of = [&](int v) {
+    return (int64_t)(j0 + (in_of(v) ? vec_index(v, tpr, lt) : 0)) * VEC;
+  };
+  Pack<S, VEC> xv[NV], rv[NV], wv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) wv[v] = ld<S, VEC>(w + lj_of(v));
+  shared_loads_first();
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    xv[v] = ld_nt<S, VEC>(x + base + lj_of(v));
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(res + base + lj_of(v));
+  }
+  float a[NV][VEC];
+  double ss = 0.0;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    double vs = 0.0;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float t = E::to_f(xv[v].v[e]);
+      if constexpr (RES) t += E::to_f(rv[v].v[e]);
+      a[v][e] = t;
+      const double d = (double)t;
+      vs = __builtin_fma(d, d, vs);
+    }
+    ss += in_of(v) ? vs : 0.0;
+    if constexpr (RES) {
+      if (in_of(v)) {
+        Pack<S, VEC> o;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(a[v][e]);
+        st_nt<S, VEC>(res + base + lj_of(v), o);
+      }
+    }
+  }
+  ss = row_reduce<true>(ss, red_sum, tpr, SumOp());
+  ss = split_sum(split_slots(ws, row, slices, 0), slices, sl, kSplitTag, ss, err, timeout_ticks,
+                 &x_sum);
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+  float amax = 0.0f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float y = rnd<E>(rnd<E>(a[v][e] * rho) * E::to_f(wv[v].v[e]));
+      a[v][e] = y;
+      amax = __builtin_fmaxf(amax, in_of(v) ? __builtin_fabsf(y) : 0.0f);
+    }
+  }
+  amax = row_reduce<true>(amax, red_max, tpr, MaxOp());
+  amax = split_max(split_slots(ws, row, slices, 1), slices, sl, kSplitTag, amax, err,
+                   timeout_ticks, &x_max);
+  float A;
+  const float s = row_scale<FP8, MODE>(amax, rho, scale_ub, &A);
+  if (sl == 0 && lt == 0) scales[row] = s;
+  const float inv = mcop_div_rn(1.0f, s);
+  const bool s_ok = mcop_divisor_ok(s);
+  const bool bounded = A == amax && s <= 0x1p100f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    if (in_of(v)) {
+      st_nt<uint8_t, VEC>(out + base + lj_of(v),
+                          row_codes<E, VEC, FP8, MODE>(a[v], rho, s, inv, s_ok, bounded,
+                                                       scale_ub != nullptr));
+    }
+  }
+}
+
+// Rows too wide for the register-resident kernels, vector path: the split-row kernel when it
+// applies (split_plan), in launches of at most chunk_rows rows, with its workspace from
+// `scratch` when given (the no-allocation entry point: kSplitWsWords words) or else from the
+// stream-ordered allocator, released on the same stream; MCOP_E_UNSUPPORTED (no message) when it
+// does not apply, so the caller runs the multi-pass kernel.
+template <class E, int VEC, bool FP8, bool RES, int MODE>
+static int launch_split(const char* name, void* out, float* scales, const void* x,
+                        const void* w, const float* scale_ub, void* res, int64_t rows,
+                        int hidden, float eps, uint64_t* scratch, hipStream_t st) {
+  using S = typename E::S;
+  const void* kernel =
+      reinterpret_cast<const void*>(&k_rms_norm_quant_split<E, VEC, kSplitNv, FP8, RES, MODE>);
+  SplitPlan p;
+  if (!split_plan(kernel, rows, hidden / VEC, st, &p)) return MCOP_E_UNSUPPORTED;
+  uint64_t* ws = scratch;
+  if (scratch == nullptr &&
+      hipMallocAsync(reinterpret_cast<void**>(&ws), (size_t)p.ws_words * 8, st) != hipSuccess) {
+    (void)hipGetLastError();
+    return MCOP_E_UNSUPPORTED;
+  }
+  int slices = p.slices, slice_vecs = p.slice_vecs;
+  int64_t timeout = p.timeout_ticks;
+  int rc = MCOP_OK;
+  for (int64_t r0 = 0; r0 < rows && rc == MCOP_OK; r0 += p.chunk_rows) {
+    int64_t n = std::min<int64_t>(p.chunk_rows, rows - r0);
+    auto* o = static_cast<uint8_t*>(out) + r0 * (int64_t)hidden;
+    float* sc = scales + r0;
+    auto* xp = static_cast<const S*>(x) + r0 * (int64_t)hidden;
+    auto* wp = static_cast<const S*>(w);
+    auto* rp = res == nullptr ? nullptr : static_cast<S*>(res) + r0 * (int64_t)hidden;
+    void* args[] = {&o, &sc, &xp, &wp, &scale_ub, &rp, &n, &hidden, &slices,
+                    &slice_vecs, &eps, &ws, &timeout};
+    rc = split_launch(name, kernel, args, p, n, ws, st);
+  }
+  if (scratch == nullptr && hipFreeAsync(ws, st) != hipSuccess) {
+    (void)hipGetLastError();
+    return rc != MCOP_OK ? rc : set_error(MCOP_E_LAUNCH, "%s: hipFreeAsync failed", name);
+  }
+  return rc;
+}
+
 template <class E, int VEC, bool FP8, bool RES, int MODE>
 static void launch_nv(const Geometry& g, void* out, float* scales, const void* x, const void* w,
                       const float* scale_ub, void* res, int64_t rows, int hidden, float eps,
@@ -409,10 +551,12 @@ static const void* kernel_of(int nv) {
   }
 }
 
+// `scratch`: the split-row kernel's workspace for the no-allocation entry point (NULL: the
+// stream-ordered allocator provides it).
 template <class E, bool FP8, int MODE>
 static int dispatch(const char* name, void* out, float* scales, const void* x, const void* w,
                     const float* scale_ub, void* res, int64_t rows, int64_t hidden, float eps,
-                    hipStream_t st) {
+                    hipStream_t st, uint64_t* scratch = nullptr) {
   constexpr int V = E::VEC;
   const bool vec_ok = hidden % V == 0 && aligned(16, x, w, res) && aligned(V, out);
   const KernelOfNv kernels =
@@ -420,6 +564,14 @@ static int dispatch(const char* name, void* out, float* scales, const void* x, c
              : (res ? &kernel_of<E, 1, FP8, true, MODE> : &kernel_of<E, 1, FP8, false, MODE>);
   if constexpr (MODE != QM_MC_7168) {
     if (!row_fits(hidden, vec_ok ? V : 1, kernels)) {
+      if (vec_ok && split_rows_enabled()) {
+        const int rc =
+            res ? launch_split<E, V, FP8, true, MODE>(name, out, scales, x, w, scale_ub, res,
+                                                      rows, (int)hidden, eps, scratch, st)
+                : launch_split<E, V, FP8, false, MODE>(name, out, scales, x, w, scale_ub, res,
+                                                       rows, (int)hidden, eps, scratch, st);
+        if (rc != MCOP_E_UNSUPPORTED) return rc;
+      }
       if (!wide_rows_ok(name, rows)) return MCOP_E_UNSUPPORTED;
       using S = typename E::S;
       auto* o = static_cast<uint8_t*>(out);

@@ -473,6 +473,11 @@ bool row_fits(int64_t hidden, int vec, KernelOfNv kernels, int min_tpr = 16);
 // generic form, which choose_geometry has already checked.
 bool exact_form_ok(const void* ex_kernel);
 
+// Whether rows too wide for the register-resident kernels may take a split-row kernel (rows
+// shared by several workgroups, split_row.h): on unless the calling thread switched it off with
+// mcop_debug_set_split_rows (then they take the multi-pass kernels, as graph captures do).
+bool split_rows_enabled();
+
 // Launch check of the multi-pass kernels for rows too wide for the register-resident ones
 // (one 1024-lane workgroup per row): false, with the message set, beyond 2^31 - 1 rows.
 bool wide_rows_ok(const char* op, int64_t rows);

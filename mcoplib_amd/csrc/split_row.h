@@ -1,0 +1,163 @@
+// split_row.h -- rows split over several workgroups: the device-side exchange of per-row
+// partial results between the workgroups that share a row, and the host-side plan of such a
+// launch.
+//
+// A row too wide for one workgroup's registers is cut into S slices of at most kSplitVecs
+// 16-byte vectors; S consecutive workgroups (a "group") hold one slice each in registers, so the
+// row is read from HBM once, as in the register-resident kernels.  Workgroup b takes slice b % S
+// of row b / S of the launch's rows.  Where the one-workgroup kernels reduce across the row's
+// waves through LDS, the group reduces across its workgroups through a small device workspace:
+//   - each workgroup reduces its slice (row_reduce) and publishes the result in tagged 64-bit
+//     words: the high half carries a tag, the low half 32 data bits; an fp64 partial takes two
+//     words.  Each word is written and read with one relaxed atomic access at agent scope
+//     (coherent across the XCDs' L2 caches), so a reader that sees the tag also sees the data in
+//     the same word, and no fence or cache write-back is needed;
+//   - one wave per workgroup polls the S words of its row until every tag is set, then combines
+//     them in slice order (so every workgroup of the row, and every launch shape, gets the same
+//     bits) and shares the result through LDS;
+//   - every row has its own slots, and the workspace is zeroed before each launch, so stale
+//     words never carry a tag; a launch covers at most as many rows as the workspace has slots
+//     for (kSplitWsWords), longer calls take several launches;
+//   - progress needs no co-residency of the grid: workgroups are dispatched in index order, so
+//     every workgroup of the lowest unfinished row has been dispatched, and a row's workgroups
+//     wait only for each other -- at most S - 1 waiting workgroups per launch hold resources
+//     (also with other kernels on the device);
+//   - every wait is bounded by the wall clock all the same: a wait that exceeds it sets the
+//     workspace's error word, and every later wait of the launch returns at once, so the grid
+//     always drains.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rowkern.h"
+
+namespace mcop {
+
+// Largest slice a workgroup holds: four 16-byte vectors a lane over 256 lanes (four waves: the
+// resident workgroups of a CU then fill its wave slots in steps of four).
+constexpr int kSplitNv = 4;
+constexpr int kSplitLanes = 256;
+constexpr int kSplitVecs = kSplitNv * kSplitLanes;
+// Most slices per row (one polling lane each).
+constexpr int kSplitMaxSlices = 64;
+
+// Workspace layout (64-bit words): for the launch's row r, phase f (0: the sum of squares, 1:
+// the absmax), slice s, word k: index ((r * 2 + f) * S + s) * 2 + k; the last word is the error
+// flag.  kSplitWsWords bounds a launch's workspace (2 MiB; the rows of one launch follow).
+constexpr int64_t kSplitWsWords = (int64_t)1 << 18;
+constexpr uint32_t kSplitTag = 1;
+
+__host__ __device__ constexpr int64_t split_ws_words(int64_t rows, int slices) {
+  return rows * 2 * slices * 2 + 1;
+}
+
+__device__ __forceinline__ uint64_t* split_slots(uint64_t* ws, int64_t row, int slices,
+                                                 int phase) {
+  return ws + ((row * 2 + phase) * slices) * 2;
+}
+
+__device__ __forceinline__ void ws_put(uint64_t* p, uint32_t tag, uint32_t data) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | data, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t ws_get(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wave 0 of the workgroup: waits until the `words` tagged words of each of the group's S slices
+// (at slots[s * 2 + k], k < words) carry `tag`; lane s < S returns its slice's words in w0, w1.
+// False when the wait timed out or an earlier wait of the launch did (error word set).
+__device__ __forceinline__ bool split_wait(const uint64_t* slots, int slices, int words,
+                                           uint32_t tag, uint64_t* err, int64_t timeout_ticks,
+                                           uint64_t* w0, uint64_t* w1) {
+  const int lane = (int)threadIdx.x & 63;
+  const int64_t t0 = wall_clock64();
+  while (true) {
+    bool ok = true;
+    if (lane < slices) {
+      *w0 = ws_get(slots + lane * 2);
+      *w1 = words > 1 ? ws_get(slots + lane * 2 + 1) : ((uint64_t)tag << 32);
+      ok = (uint32_t)(*w0 >> 32) == tag && (uint32_t)(*w1 >> 32) == tag;
+    }
+    if (__builtin_amdgcn_ballot_w64(!ok) == 0) return true;
+    if (ws_get(err) != 0) return false;
+    if (wall_clock64() - t0 > timeout_ticks) {
+      if (lane == 0) ws_put(err, 1, 1);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+// The group's sum of the slices' fp64 partials, in slice order; `part` is this workgroup's
+// partial (uniform), `sl` its slice.  Every thread of the workgroup calls it.
+__device__ __forceinline__ double split_sum(uint64_t* slots, int slices, int sl, uint32_t tag,
+                                            double part, uint64_t* err, int64_t timeout_ticks,
+                                            double* lds) {
+  if (threadIdx.x == 0) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, part);
+    ws_put(slots + sl * 2, tag, (uint32_t)b);
+    ws_put(slots + sl * 2 + 1, tag, (uint32_t)(b >> 32));
+  }
+  if (threadIdx.x < 64) {
+    uint64_t w0 = 0, w1 = 0;
+    split_wait(slots, slices, 2, tag, err, timeout_ticks, &w0, &w1);
+    const uint32_t lo = (uint32_t)w0, hi = (uint32_t)w1;
+    double total = 0.0;
+    for (int s = 0; s < slices; ++s) {
+      const uint64_t b = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)hi, s) << 32) |
+                         (uint32_t)__builtin_amdgcn_readlane((int)lo, s);
+      total += __builtin_bit_cast(double, b);
+    }
+    if (threadIdx.x == 0) *lds = total;
+  }
+  __syncthreads();
+  return *lds;
+}
+
+// The group's largest of the slices' (non-negative or NaN-free) fp32 maxima.
+__device__ __forceinline__ float split_max(uint64_t* slots, int slices, int sl, uint32_t tag,
+                                           float part, uint64_t* err, int64_t timeout_ticks,
+                                           float* lds) {
+  if (threadIdx.x == 0) ws_put(slots + sl * 2, tag, __builtin_bit_cast(uint32_t, part));
+  if (threadIdx.x < 64) {
+    uint64_t w0 = 0, w1 = 0;
+    split_wait(slots, slices, 1, tag, err, timeout_ticks, &w0, &w1);
+    float m = (int)(threadIdx.x & 63) < slices ? __builtin_bit_cast(float, (uint32_t)w0) : 0.0f;
+    m = wave_reduce(m, MaxOp());
+    if (threadIdx.x == 0) *lds = m;
+  }
+  __syncthreads();
+  return *lds;
+}
+
+__global__ void k_fill_u64(uint64_t* __restrict__ p, int64_t n);
+
+// Host side -------------------------------------------------------------------------------------
+
+// The launches of a split-row kernel: S slices of `slice_vecs` vectors (the last may be
+// shorter) over `lanes` lanes each, at most `chunk_rows` rows (chunk_rows * S workgroups) per
+// launch, a workspace of `ws_words` words.
+struct SplitPlan {
+  int slices;
+  int slice_vecs;
+  int lanes;
+  int64_t chunk_rows;
+  int64_t ws_words;
+  int64_t timeout_ticks;
+};
+
+// Plans the split-row launches of `kernel` (one slice per workgroup, kSplitNv vectors a lane) for
+// `rows` rows of `nvec` vectors: false (no message set) when they do not apply (the row fits
+// fewer than two slices or needs more than kSplitMaxSlices, the kernel spills, or the stream is
+// being captured into a graph), in which case the caller runs its multi-pass kernel instead.
+bool split_plan(const void* kernel, int64_t rows, int64_t nvec, hipStream_t st, SplitPlan* p);
+
+// Zeroes the launch's workspace (`rows` rows of the plan) and launches `kernel` with `args` (its
+// parameter list, as hipLaunchKernel takes it) over rows * S workgroups.
+int split_launch(const char* op, const void* kernel, void** args, const SplitPlan& p,
+                 int64_t rows, uint64_t* ws, hipStream_t st);
+
+}  // namespace mcop

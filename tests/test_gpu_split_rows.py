@@ -1,0 +1,239 @@
+"""Rows too wide for one workgroup's registers on the split-row kernels (H2 / H3: each row shared
+by several workgroups that exchange partial sums through a device workspace): bit for bit against
+the oracle and against the multi-pass kernels (forced with the library's test hook), over several
+row counts and a call that takes two launches, two streams at once, and a HIP graph capture
+(which takes the multi-pass kernel)."""
+
+import os
+import subprocess
+import sys
+import threading
+
+import pytest
+import torch
+
+import oracle
+import mcoplib_amd._C  # noqa: F401  (registers torch.ops._C.*)
+from conftest import ROOT
+from mcoplib_amd import _lib, custom_ops
+from gpu_util import DEV, assert_codes, assert_exact, assert_scales, gen, say
+
+pytestmark = pytest.mark.gpu
+
+
+def _x(T, H, seed, dtype, scale=1.0):
+    x = torch.randn(T, H, generator=gen(seed)) * scale
+    x[0, 7] = 40.0 * scale  # an outlier: the absmax row element
+    if T > 2:
+        x[2].zero_()
+    return x.to(dtype)
+
+
+def _w(H, seed, dtype):
+    return (1 + 0.1 * torch.randn(H, generator=gen(seed))).to(dtype)
+
+
+def _h2(x, w, r, qdt, ub):
+    """One vLLM-surface call on the GPU; returns (codes, scales, residual or None) on the CPU."""
+    q = torch.empty(x.shape, dtype=qdt, device=DEV)
+    s = torch.empty(x.shape[0], 1, device=DEV)
+    rd = None if r is None else r.to(DEV)
+    ubd = None if ub is None else torch.tensor([ub], device=DEV)
+    torch.ops._C.rms_norm_dynamic_per_token_quant(q, x.to(DEV), w.to(DEV), s, 1e-6, ubd, rd)
+    torch.cuda.synchronize()
+    return q.cpu(), s.cpu(), None if rd is None else rd.cpu()
+
+
+def _same(a, b, what):
+    if a is None:
+        assert b is None
+        return
+    assert torch.equal(a.view(torch.uint8) if a.element_size() == 1 else a,
+                       b.view(torch.uint8) if b.element_size() == 1 else b), what
+
+
+@pytest.mark.parametrize("dtype,H", [(torch.bfloat16, 65544), (torch.bfloat16, 131072),
+                                     (torch.bfloat16, 262144), (torch.float16, 65608),
+                                     (torch.float32, 32772), (torch.float32, 65536)])
+@pytest.mark.parametrize("qdt", [torch.int8, torch.float8_e4m3fn])
+def test_split_h2_against_oracle_and_multipass(dtype, H, qdt):
+    say(f"split H2 {dtype} H={H} {qdt}")
+    T = 5
+    x, r, w = _x(T, H, 60, dtype), _x(T, H, 61, dtype), _w(H, 62, dtype)
+    ubs = (None, 0.05) if qdt == torch.float8_e4m3fn else (None,)
+    for res in (None, r):
+        for ub in ubs:
+            tag = f"res={res is not None} ub={ub}"
+            q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant(x, w, 1e-6, qdt, ub, res)
+            got = _h2(x, w, res, qdt, ub)
+            assert_scales(got[1], s_ref, tag + " scales")
+            assert_codes(got[0], q_ref, tag + " codes")
+            if res is not None:
+                assert_exact(got[2], r_ref, tag + " residual")
+            _lib.set_split_rows(False)
+            try:
+                mp = _h2(x, w, res, qdt, ub)
+            finally:
+                _lib.set_split_rows(True)
+            for a, b, what in zip(got, mp, ("codes", "scales", "residual")):
+                _same(a, b, f"{tag} {what}: split-row and multi-pass kernels differ")
+
+
+@pytest.mark.parametrize("T", [1, 3, 250])
+def test_split_h3_row_counts(T):
+    """mcoplib's operator (1.5e-6 floor, +-127 codes) over a few row counts."""
+    H = 131072
+    say(f"split H3 T={T} H={H}")
+    x, r, w = _x(T, H, 63, torch.bfloat16), _x(T, H, 64, torch.bfloat16), _w(H, 65,
+                                                                               torch.bfloat16)
+    q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant_custom(x, w, 1e-6, residual=r)
+    rd = r.to(DEV)
+    q, s = custom_ops.rms_norm_dynamic_per_token_quant(x.to(DEV), w.to(DEV), 1e-6, torch.int8,
+                                                       residual=rd)
+    torch.cuda.synchronize()
+    assert_scales(s, s_ref, "scales")
+    assert_codes(q, q_ref, "codes")
+    assert_exact(rd, r_ref, "residual")
+
+
+def test_split_launches_in_chunks():
+    """More rows than one launch's workspace holds (1023 rows of 64 slices, 524288-wide bf16
+    rows): two launches, the second on the rows, residual and codes after the first's."""
+    T, H = 1025, 524288
+    say(f"split: {T}x{H} bf16 with a residual (two launches)")
+    x, r, w = _x(T, H, 83, torch.bfloat16), _x(T, H, 84, torch.bfloat16), _w(H, 85,
+                                                                               torch.bfloat16)
+    rd = r.to(DEV)
+    q = torch.empty(T, H, dtype=torch.int8, device=DEV)
+    s = torch.empty(T, 1, device=DEV)
+    torch.ops._C.rms_norm_dynamic_per_token_quant(q, x.to(DEV), w.to(DEV), s, 1e-6, None, rd)
+    torch.cuda.synchronize()
+    for b0 in (0, 1016, 1020):  # rows on both sides of the launch boundary (row 1023)
+        sel = slice(b0, b0 + 5)
+        q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant(x[sel], w, 1e-6,
+                                                                      torch.int8, None, r[sel])
+        assert_exact(rd[sel], r_ref, f"residual rows {b0}+")
+        assert_scales(s[sel], s_ref, f"scales rows {b0}+")
+        assert_codes(q[sel], q_ref, f"codes rows {b0}+")
+
+
+def test_split_wide_int8_workload_all_rows():
+    """The bench's wide-int8 workload, 2048 x 131072 bf16 with a residual, through the headline
+    surface: every row against the oracle (in blocks of 256 rows)."""
+    T, H = 2048, 131072
+    say(f"split: the wide-int8 workload {T}x{H}, all rows")
+    x, r, w = _x(T, H, 66, torch.bfloat16), _x(T, H, 67, torch.bfloat16), _w(H, 68,
+                                                                               torch.bfloat16)
+    rd = r.to(DEV)
+    q, s = custom_ops.rms_norm_dynamic_per_token_quant(x.to(DEV), w.to(DEV), 1e-6, torch.int8,
+                                                       residual=rd)
+    torch.cuda.synchronize()
+    B = 256
+    for b0 in range(0, T, B):
+        q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant_custom(
+            x[b0:b0 + B], w, 1e-6, residual=r[b0:b0 + B])
+        assert_exact(rd[b0:b0 + B], r_ref, f"residual rows {b0}+")
+        assert_scales(s[b0:b0 + B], s_ref, f"scales rows {b0}+")
+        assert_codes(q[b0:b0 + B], q_ref, f"codes rows {b0}+")
+
+
+def test_split_two_streams():
+    """Two host threads, each on its own stream, run wide rows (split-row launches) at the same
+    time, 20 calls each; every call matches the single-stream result."""
+    say("split: two threads, two streams, 20 wide calls each")
+    H = 131072
+    cases = []
+    for i, T in enumerate((40, 96)):
+        x, r, w = (_x(T, H, 70 + 3 * i, torch.bfloat16).to(DEV),
+                   _x(T, H, 71 + 3 * i, torch.bfloat16).to(DEV),
+                   _w(H, 72 + 3 * i, torch.bfloat16).to(DEV))
+        cases.append((x, r, w))
+
+    def run(x, r, w):
+        q = torch.empty(x.shape, dtype=torch.int8, device=DEV)
+        s = torch.empty(x.shape[0], 1, device=DEV)
+        rr = r.clone()
+        torch.ops._C.rms_norm_dynamic_per_token_quant(q, x, w, s, 1e-6, None, rr)
+        return q, s, rr
+    expected = [run(*c) for c in cases]
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(i):
+        try:
+            stream = torch.cuda.Stream()
+            with torch.cuda.stream(stream):
+                for _ in range(20):
+                    got = run(*cases[i])
+                    stream.synchronize()
+                    if not all(torch.equal(a, b) for a, b in zip(got, expected[i])):
+                        errors.append(f"thread {i}: result differs")
+                        return
+        except Exception as e:  # reported by the main thread
+            errors.append(f"thread {i}: {e!r}")
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads), "a thread did not finish"
+    assert not errors, errors
+
+
+def test_split_graph_capture_takes_the_multipass_kernel():
+    """A wide-row call captured into a HIP graph runs the multi-pass kernel (no cooperative
+    launch, no workspace in the graph); replays match the eager split-row result."""
+    say("split: graph capture of a wide-row call")
+    T, H = 6, 131072
+    x, r, w = (_x(T, H, 80, torch.bfloat16).to(DEV), _x(T, H, 81, torch.bfloat16).to(DEV),
+               _w(H, 82, torch.bfloat16).to(DEV))
+    q0 = torch.empty(T, H, dtype=torch.int8, device=DEV)
+    s0 = torch.empty(T, 1, device=DEV)
+    torch.ops._C.rms_norm_dynamic_per_token_quant(q0, x, w, s0, 1e-6, None, None)
+    q = torch.empty(T, H, dtype=torch.int8, device=DEV)
+    s = torch.empty(T, 1, device=DEV)
+    g = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(g, stream=cap):
+            torch.ops._C.rms_norm_dynamic_per_token_quant(q, x, w, s, 1e-6, None, None)
+    torch.cuda.current_stream().wait_stream(cap)
+    for i in range(3):
+        q.zero_()
+        s.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(q, q0) and torch.equal(s, s0), f"replay {i}"
+
+
+_TRACE_SCRIPT = r"""
+import sys, torch
+sys.path.insert(0, "tests")
+import mcoplib_amd._C
+from mcoplib_amd import _lib
+from gpu_util import DEV
+x = torch.randn(4, 131072, device=DEV).to(torch.bfloat16)
+w = torch.ones(131072, device=DEV, dtype=torch.bfloat16)
+q = torch.empty(4, 131072, dtype=torch.int8, device=DEV)
+s = torch.empty(4, 1, device=DEV)
+torch.ops._C.rms_norm_dynamic_per_token_quant(q, x, w, s, 1e-6, None, None)
+_lib.set_split_rows(False)
+torch.ops._C.rms_norm_dynamic_per_token_quant(q, x, w, s, 1e-6, None, None)
+torch.cuda.synchronize()
+print("child ok", flush=True)
+"""
+
+
+def test_split_launch_decisions_are_traced():
+    say("split: MCOP_DEBUG_TRACE names the split-row and the multi-pass launches")
+    env = dict(os.environ, MCOP_DEBUG_TRACE="1")
+    out = subprocess.run([sys.executable, "-c", _TRACE_SCRIPT], cwd=str(ROOT), env=env,
+                         capture_output=True, text=True, timeout=300)
+    say(out.stdout[-2000:])
+    assert out.returncode == 0, out.stderr[-3000:]
+    assert "child ok" in out.stdout
+    assert "rows=4: split-row kernel, 16 slices of 1024 vectors over 256 lanes" in out.stdout
+    assert "rows=4: multi-pass kernel" in out.stdout
