@@ -88,6 +88,23 @@ int mcop_rms_norm_dynamic_per_token_quant(void* out, mcop_dtype out_dtype, float
                                           int64_t num_tokens, int64_t hidden_size,
                                           mcop_dtype in_dtype, float epsilon, void* stream);
 
+/* mcop_rms_norm_dynamic_per_token_quant that allocates nothing, with the same arguments and
+ * results. It has no counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation). Where the allocating entry takes a stream-ordered workspace (rows too wide for
+ * one workgroup's registers, run split over several workgroups), this one uses a scratch array
+ * of 2 MiB that the library holds on each GPU it runs on until the process ends; long calls are
+ * cut into launches that fit it, and a launch that would not fit is refused with
+ * MCOP_E_UNSUPPORTED and a message. Every call on a GPU shares that GPU's array (zeroed by the
+ * call before use), so calls of this entry point that overlap on one GPU (other streams, other
+ * threads) race: serialize them. The first call on a device resolves the array's address there. */
+int mcop_rms_norm_dynamic_per_token_quant_noalloc(void* out, mcop_dtype out_dtype, float* scales,
+                                                  const void* input, const void* weight,
+                                                  const float* scale_ub, void* residual,
+                                                  int64_t num_tokens, int64_t hidden_size,
+                                                  mcop_dtype in_dtype, float epsilon,
+                                                  void* stream);
+
 /* H4. SmoothQuant (residual add +) RMSNorm + dynamic per-token quantization
  * (mcoplib.op.rms_norm_dynamic_per_token_quant, "fused_rms_norm_dq").
  *   a = input (+ residual, read only); after_res <- round(a)

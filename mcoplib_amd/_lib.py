@@ -30,6 +30,8 @@ def _load() -> ctypes.CDLL:
     P, I64, F, I, U32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int, ctypes.c_uint32
     lib.mcop_fused_add_rms_norm.argtypes = [P, I64, P, P, I64, I64, I, F, P]
     lib.mcop_rms_norm_dynamic_per_token_quant.argtypes = [P, I, P, P, P, P, P, I64, I64, I, F, P]
+    lib.mcop_rms_norm_dynamic_per_token_quant_noalloc.argtypes = [P, I, P, P, P, P, P, I64, I64,
+                                                                   I, F, P]
     lib.mcop_rms_norm_smooth_quant.argtypes = [P, I, P, P, P, I, P, I, P, P, P, I64, I64, I, F,
                                                U32, P]
     lib.mcop_scale_dynamic_quant.argtypes = [P, P, P, P, I64, I64, P]
@@ -48,6 +50,7 @@ def _load() -> ctypes.CDLL:
     lib.mcop_debug_set_launch_override.argtypes = [I, I]
     lib.mcop_debug_set_split_rows.argtypes = [I]
     for fn in ("mcop_fused_add_rms_norm", "mcop_rms_norm_dynamic_per_token_quant",
+               "mcop_rms_norm_dynamic_per_token_quant_noalloc",
                "mcop_rms_norm_smooth_quant", "mcop_scale_dynamic_quant",
                "mcop_fp8_e4m3fn_from_f32", "mcop_debug_set_launch_override",
                "mcop_debug_set_split_rows", "mcop_abi_version",

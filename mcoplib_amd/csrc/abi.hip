@@ -221,7 +221,7 @@ bool split_plan(const void* kernel, int64_t rows, int64_t nvec, hipStream_t st, 
 }
 
 int split_launch(const char* op, const void* kernel, void** args, const SplitPlan& p,
-                 int64_t rows, uint64_t* ws, hipStream_t st) {
+                 int64_t rows, uint64_t* ws, bool static_ws, hipStream_t st) {
   const int64_t words = split_ws_words(rows, p.slices);
   hipLaunchKernelGGL(k_fill_u64, dim3((unsigned)ceil_div(words, 256)), dim3(256), 0, st, ws,
                      words);
@@ -234,7 +234,8 @@ int split_launch(const char* op, const void* kernel, void** args, const SplitPla
   }
   if (trace_enabled()) {
     fprintf(stdout, "[mcop] %s rows=%lld: split-row kernel, %d slices of %d vectors over %d "
-            "lanes\n", op, (long long)rows, p.slices, p.slice_vecs, p.lanes);
+            "lanes, workspace %s\n", op, (long long)rows, p.slices, p.slice_vecs, p.lanes,
+            static_ws ? "in the no-allocation scratch" : "from the stream-ordered allocator");
     fflush(stdout);
   }
   return MCOP_OK;

@@ -28,6 +28,7 @@
 
 #include <algorithm>
 #include <cfloat>
+#include <mutex>
 #include <type_traits>
 
 #include "../../include/mcop_norm.h"
@@ -470,6 +471,11 @@ static int launch_split(const char* name, void* out, float* scales, const void* 
   SplitPlan p;
   if (!split_plan(kernel, rows, hidden / VEC, st, &p)) return MCOP_E_UNSUPPORTED;
   uint64_t* ws = scratch;
+  if (scratch != nullptr && p.ws_words > kSplitWsWords) {  // launches are sized to fit it
+    return set_error(MCOP_E_UNSUPPORTED, "%s: a launch needs %lld workspace words, more than "
+                     "the %lld of the no-allocation scratch", name, (long long)p.ws_words,
+                     (long long)kSplitWsWords);
+  }
   if (scratch == nullptr &&
       hipMallocAsync(reinterpret_cast<void**>(&ws), (size_t)p.ws_words * 8, st) != hipSuccess) {
     (void)hipGetLastError();
@@ -487,7 +493,7 @@ static int launch_split(const char* name, void* out, float* scales, const void* 
     auto* rp = res == nullptr ? nullptr : static_cast<S*>(res) + r0 * (int64_t)hidden;
     void* args[] = {&o, &sc, &xp, &wp, &scale_ub, &rp, &n, &hidden, &slices,
                     &slice_vecs, &eps, &ws, &timeout};
-    rc = split_launch(name, kernel, args, p, n, ws, st);
+    rc = split_launch(name, kernel, args, p, n, ws, scratch != nullptr, st);
   }
   if (scratch == nullptr && hipFreeAsync(ws, st) != hipSuccess) {
     (void)hipGetLastError();
@@ -619,16 +625,11 @@ static int check_args(const char* name, const void* out, const float* scales, co
   return MCOP_OK;
 }
 
-}  // namespace mcop
-
-extern "C" int mcop_rms_norm_dynamic_per_token_quant(void* out, mcop_dtype out_dtype,
-                                                     float* scales, const void* input,
-                                                     const void* weight, const float* scale_ub,
-                                                     void* residual, int64_t num_tokens,
-                                                     int64_t hidden_size, mcop_dtype in_dtype,
-                                                     float epsilon, void* stream) {
-  using namespace mcop;
-  const char* name = "rms_norm_dynamic_per_token_quant";
+// vLLM's operator (QM_VLLM), int8 or fp8 codes; `scratch` as for dispatch.
+static int h2_entry(const char* name, void* out, mcop_dtype out_dtype, float* scales,
+                    const void* input, const void* weight, const float* scale_ub, void* residual,
+                    int64_t num_tokens, int64_t hidden_size, mcop_dtype in_dtype, float epsilon,
+                    void* stream, uint64_t* scratch) {
   if (int rc = check_args(name, out, scales, input, weight, num_tokens, hidden_size)) return rc;
   if (num_tokens == 0) return MCOP_OK;
   if (out_dtype != MCOP_I8 && out_dtype != MCOP_FP8_E4M3FN) {
@@ -639,9 +640,11 @@ extern "C" int mcop_rms_norm_dynamic_per_token_quant(void* out, mcop_dtype out_d
   auto st = static_cast<hipStream_t>(stream);
 #define MCOP_CASE(E)                                                                         \
   return fp8 ? dispatch<E, true, QM_VLLM>(name, out, scales, input, weight, scale_ub,         \
-                                          residual, num_tokens, hidden_size, epsilon, st)     \
+                                          residual, num_tokens, hidden_size, epsilon, st,     \
+                                          scratch)                                            \
              : dispatch<E, false, QM_VLLM>(name, out, scales, input, weight, scale_ub,        \
-                                           residual, num_tokens, hidden_size, epsilon, st)
+                                           residual, num_tokens, hidden_size, epsilon, st,    \
+                                           scratch)
   switch (in_dtype) {
     case MCOP_BF16: MCOP_CASE(BF16);
     case MCOP_F16: MCOP_CASE(F16);
@@ -651,6 +654,65 @@ extern "C" int mcop_rms_norm_dynamic_per_token_quant(void* out, mcop_dtype out_d
                        (int)in_dtype);
   }
 #undef MCOP_CASE
+}
+
+// The no-allocation entry point's workspace for the split-row kernels: kSplitWsWords 64-bit
+// words (2 MiB) on every GPU the library runs on, held until the process ends.  In host code
+// the name is a stand-in, not a device address: scratch_address() resolves each device's copy.
+static __device__ __align__(256) uint64_t scratch[kSplitWsWords];
+
+// The device address of `scratch` on the current device: hipGetSymbolAddress once per device
+// (with that device current, on its first call there), then the kept address.  NULL, with the
+// message set, when the runtime cannot resolve it.
+static uint64_t* scratch_address(const char* name) {
+  static std::mutex mu;
+  static uint64_t* addr[64] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    set_error(MCOP_E_LAUNCH, "%s: no current device (or device %d beyond 63)", name, dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      set_error(MCOP_E_LAUNCH, "%s: hipGetSymbolAddress of the scratch array failed on device "
+                "%d: %s", name, dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    addr[dev] = static_cast<uint64_t*>(p);
+  }
+  return addr[dev];
+}
+
+}  // namespace mcop
+
+extern "C" int mcop_rms_norm_dynamic_per_token_quant(void* out, mcop_dtype out_dtype,
+                                                     float* scales, const void* input,
+                                                     const void* weight, const float* scale_ub,
+                                                     void* residual, int64_t num_tokens,
+                                                     int64_t hidden_size, mcop_dtype in_dtype,
+                                                     float epsilon, void* stream) {
+  return mcop::h2_entry("rms_norm_dynamic_per_token_quant", out, out_dtype, scales, input,
+                        weight, scale_ub, residual, num_tokens, hidden_size, in_dtype, epsilon,
+                        stream, nullptr);
+}
+
+extern "C" int mcop_rms_norm_dynamic_per_token_quant_noalloc(
+    void* out, mcop_dtype out_dtype, float* scales, const void* input, const void* weight,
+    const float* scale_ub, void* residual, int64_t num_tokens, int64_t hidden_size,
+    mcop_dtype in_dtype, float epsilon, void* stream) {
+  using namespace mcop;
+  const char* name = "rms_norm_dynamic_per_token_quant_noalloc";
+  if (int rc = check_args(name, out, scales, input, weight, num_tokens, hidden_size)) return rc;
+  if (num_tokens == 0) return MCOP_OK;
+  uint64_t* ws = scratch_address(name);
+  if (ws == nullptr) return MCOP_E_LAUNCH;
+  return h2_entry(name, out, out_dtype, scales, input, weight, scale_ub, residual, num_tokens,
+                  hidden_size, in_dtype, epsilon, stream, ws);
 }
 
 extern "C" int mcop_rms_norm_dynamic_per_token_quant_custom(

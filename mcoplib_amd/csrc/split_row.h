@@ -155,9 +155,10 @@ struct SplitPlan {
 // being captured into a graph), in which case the caller runs its multi-pass kernel instead.
 bool split_plan(const void* kernel, int64_t rows, int64_t nvec, hipStream_t st, SplitPlan* p);
 
-// Zeroes the launch's workspace (`rows` rows of the plan) and launches `kernel` with `args` (its
-// parameter list, as hipLaunchKernel takes it) over rows * S workgroups.
+// Zeroes the launch's workspace (`rows` rows of the plan) with a fill kernel and launches
+// `kernel` with `args` (its parameter list, as hipLaunchKernel takes it) over rows * S
+// workgroups; `static_ws` (the no-allocation scratch) only changes the trace line.
 int split_launch(const char* op, const void* kernel, void** args, const SplitPlan& p,
-                 int64_t rows, uint64_t* ws, hipStream_t st);
+                 int64_t rows, uint64_t* ws, bool static_ws, hipStream_t st);
 
 }  // namespace mcop

@@ -71,6 +71,11 @@ int main() {
                                                                                : (float*)dev(4),
                          res ? dev(5) : nullptr, T, H, in, 1e-6f, nullptr),
                      "rms_norm_dynamic_per_token_quant", T, H);
+              expect(mcop_rms_norm_dynamic_per_token_quant_noalloc(
+                         dev(0), out, (float*)dev(1), dev(2, mis), dev(3), res ? nullptr
+                                                                               : (float*)dev(4),
+                         res ? dev(5) : nullptr, T, H, in, 1e-6f, nullptr),
+                     "rms_norm_dynamic_per_token_quant_noalloc", T, H);
               for (mcop_dtype wd : kFloat) {
                 for (mcop_dtype sd : kFloat) {
                   expect(mcop_rms_norm_smooth_quant(
