@@ -193,7 +193,8 @@ int wall_clock_khz(int dev) {
 }
 }  // namespace
 
-bool split_plan(const void* kernel, int64_t rows, int64_t nvec, hipStream_t st, SplitPlan* p) {
+bool split_plan(const void* kernel, int nv, int64_t rows, int64_t nvec, hipStream_t st,
+                SplitPlan* p) {
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
     (void)hipGetLastError();
@@ -206,10 +207,10 @@ bool split_plan(const void* kernel, int64_t rows, int64_t nvec, hipStream_t st, 
     return false;
   }
   const int clk = wall_clock_khz(dev);
-  const int64_t slices = ceil_div(nvec, kSplitVecs);
+  const int64_t slices = ceil_div(nvec, (int64_t)nv * kSplitLanes);
   if (clk <= 0 || slices < 2 || slices > kSplitMaxSlices) return false;
   const int64_t slice_vecs = ceil_div(nvec, slices);
-  const int64_t lanes = round64(ceil_div(slice_vecs, kSplitNv));
+  const int64_t lanes = round64(ceil_div(slice_vecs, nv));
   if (blocks_per_cu(kernel, (int)lanes) < 1) return false;  // spills (or cannot launch)
   p->slices = (int)slices;
   p->slice_vecs = (int)slice_vecs;

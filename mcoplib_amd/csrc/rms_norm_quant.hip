@@ -423,9 +423,9 @@ k_rms_norm_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
       }
     }
   }
-  ss = row_reduce<true>(ss, red_sum, tpr, SumOp());
-  ss = split_sum(split_slots(ws, row, slices, 0), slices, sl, kSplitTag, ss, err, timeout_ticks,
-                 &x_sum);
+  SplitRowReduce red{red_sum, red_max, tpr, ws, row, slices, sl, err, timeout_ticks, &x_sum,
+                     &x_max};
+  ss = red.sum(ss);
   const float rho = mcop_inv_rms(ss, hidden, eps);
   float amax = 0.0f;
 #pragma unroll
@@ -437,9 +437,7 @@ k_rms_norm_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
       amax = __builtin_fmaxf(amax, in_of(v) ? __builtin_fabsf(y) : 0.0f);
     }
   }
-  amax = row_reduce<true>(amax, red_max, tpr, MaxOp());
-  amax = split_max(split_slots(ws, row, slices, 1), slices, sl, kSplitTag, amax, err,
-                   timeout_ticks, &x_max);
+  amax = red.max(amax);
   float A;
   const float s = row_scale<FP8, MODE>(amax, rho, scale_ub, &A);
   if (sl == 0 && lt == 0) scales[row] = s;
@@ -468,38 +466,21 @@ static int launch_split(const char* name, void* out, float* scales, const void* 
   using S = typename E::S;
   const void* kernel =
       reinterpret_cast<const void*>(&k_rms_norm_quant_split<E, VEC, kSplitNv, FP8, RES, MODE>);
-  SplitPlan p;
-  if (!split_plan(kernel, rows, hidden / VEC, st, &p)) return MCOP_E_UNSUPPORTED;
-  uint64_t* ws = scratch;
-  if (scratch != nullptr && p.ws_words > kSplitWsWords) {  // launches are sized to fit it
-    return set_error(MCOP_E_UNSUPPORTED, "%s: a launch needs %lld workspace words, more than "
-                     "the %lld of the no-allocation scratch", name, (long long)p.ws_words,
-                     (long long)kSplitWsWords);
-  }
-  if (scratch == nullptr &&
-      hipMallocAsync(reinterpret_cast<void**>(&ws), (size_t)p.ws_words * 8, st) != hipSuccess) {
-    (void)hipGetLastError();
-    return MCOP_E_UNSUPPORTED;
-  }
-  int slices = p.slices, slice_vecs = p.slice_vecs;
-  int64_t timeout = p.timeout_ticks;
-  int rc = MCOP_OK;
-  for (int64_t r0 = 0; r0 < rows && rc == MCOP_OK; r0 += p.chunk_rows) {
-    int64_t n = std::min<int64_t>(p.chunk_rows, rows - r0);
+  return split_run(name, kernel, kSplitNv, rows, hidden / VEC, scratch, st,
+                   [&](int64_t r0, int64_t n, uint64_t* ws, const SplitPlan& p, auto launch) {
     auto* o = static_cast<uint8_t*>(out) + r0 * (int64_t)hidden;
     float* sc = scales + r0;
     auto* xp = static_cast<const S*>(x) + r0 * (int64_t)hidden;
     auto* wp = static_cast<const S*>(w);
     auto* rp = res == nullptr ? nullptr : static_cast<S*>(res) + r0 * (int64_t)hidden;
-    void* args[] = {&o, &sc, &xp, &wp, &scale_ub, &rp, &n, &hidden, &slices,
-                    &slice_vecs, &eps, &ws, &timeout};
-    rc = split_launch(name, kernel, args, p, n, ws, scratch != nullptr, st);
-  }
-  if (scratch == nullptr && hipFreeAsync(ws, st) != hipSuccess) {
-    (void)hipGetLastError();
-    return rc != MCOP_OK ? rc : set_error(MCOP_E_LAUNCH, "%s: hipFreeAsync failed", name);
-  }
-  return rc;
+    int slices = p.slices, slice_vecs = p.slice_vecs;
+    int64_t timeout = p.timeout_ticks;
+    const float* ub = scale_ub;
+    int h = hidden;
+    float e = eps;
+    void* args[] = {&o, &sc, &xp, &wp, &ub, &rp, &n, &h, &slices, &slice_vecs, &e, &ws, &timeout};
+    return launch(args);
+  });
 }
 
 template <class E, int VEC, bool FP8, bool RES, int MODE>

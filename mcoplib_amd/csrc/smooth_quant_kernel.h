@@ -26,6 +26,7 @@
 
 #include "../../include/mcop_norm.h"
 #include "rowkern.h"
+#include "split_row.h"
 
 namespace mcop {
 
@@ -49,45 +50,58 @@ __device__ __forceinline__ Pack<uint8_t, VEC> sq_fp8_codes(const float* v, float
   return z;
 }
 
-// The lane's streamed vectors of one row: x (and the residual).
+// The lane's streamed vectors of one row's slice [j0, j0 + jn) (the whole row: 0, nvec): x
+// (and the residual); lanes past the slice end load its first vector.
 template <class E, int VEC, int NV, bool RES, bool EX>
-__device__ __forceinline__ void sq_load(const RowPos& p, const typename E::S* __restrict__ x,
+__device__ __forceinline__ void sq_load(const RowPos& p, int j0, int jn,
+                                        const typename E::S* __restrict__ x,
                                         const typename E::S* __restrict__ res, int hidden,
                                         int tpr, Pack<typename E::S, VEC>* xv,
                                         Pack<typename E::S, VEC>* rv) {
   using S = typename E::S;
-  const int nvec = hidden / VEC;
   const int64_t lbase = p.lrow * (int64_t)hidden;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int j = vec_index(v, tpr, p.lt);
-    const int64_t lj = (int64_t)(EX ? j : load_index(j, nvec)) * VEC;
+    const int k = vec_index(v, tpr, p.lt);
+    const int64_t lj = (int64_t)(j0 + (EX ? k : load_index(k, jn))) * VEC;
     xv[v] = ld_nt<S, VEC>(row_elem<EX>(x, lbase, lj));
     if constexpr (RES) rv[v] = ld_nt<S, VEC>(row_elem<EX>(res, lbase, lj));
   }
 }
 
-// One row (or, for tpr < blockDim, one of the workgroup's rows) given the lane's loaded vectors
-// of the row and its weight and smooth vectors.
-template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES, bool EX>
-__device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S, VEC>* xv,
+// The row reductions of the one-workgroup kernels: the row's waves combined through LDS.
+template <bool EX>
+struct WgRowReduce {
+  double* red_sum;
+  float* red_max;
+  int tpr;
+  __device__ __forceinline__ double sum(double v) { return row_reduce<EX>(v, red_sum, tpr, SumOp()); }
+  __device__ __forceinline__ float max(float v) { return row_reduce<EX>(v, red_max, tpr, MaxOp()); }
+};
+
+// One row (or, for tpr < blockDim, one of the workgroup's rows; or one slice [j0, j0 + jn) of a
+// row shared by several workgroups) given the lane's loaded vectors and its weight and smooth
+// vectors.  `red` combines the row's partial sum of squares and absmax (WgRowReduce, or the
+// split-row exchange).
+template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES, bool EX, class Red>
+__device__ __forceinline__ void sq_row(const RowPos& p, int j0, int jn,
+                                       const Pack<typename E::S, VEC>* xv,
                                        const Pack<typename E::S, VEC>* rv,
                                        const WVec<EW, VEC>* wv, const WVec<ES, VEC>* sv,
                                        uint8_t* __restrict__ out, float* __restrict__ scales,
                                        typename E::S* __restrict__ ares,
                                        typename E::S* __restrict__ anorm, int hidden, int tpr,
-                                       float eps, uint32_t flags, double* red_sum,
-                                       float* red_max) {
+                                       float eps, uint32_t flags, Red& red) {
   using S = typename E::S;
-  const int nvec = hidden / VEC;
   const int64_t base = p.row * (int64_t)hidden;
 
   float a[NV][VEC];
   double ss = 0.0;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int j = vec_index(v, tpr, p.lt);
-    const bool in = EX || j < nvec;
+    const int k = vec_index(v, tpr, p.lt);
+    const int j = j0 + k;
+    const bool in = EX || k < jn;
     Pack<S, VEC> o;
     double vs = 0.0;  // lanes past the row end (a copy of vector 0) do not count
 #pragma unroll
@@ -103,7 +117,7 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
     if (ares != nullptr && p.live && in) st_nt<S, VEC>(row_elem<EX>(ares, base, (int64_t)j * VEC), o);
   }
 
-  ss = row_reduce<EX>(ss, red_sum, tpr, SumOp());
+  ss = red.sum(ss);
   const float rho = mcop_inv_rms(ss, hidden, eps);
   const float inv_rho = mcop_div_rn(1.0f, rho);
   const bool rho_ok = mcop_divisor_ok(rho);
@@ -134,7 +148,8 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
   float amax = 0.0f;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int j = vec_index(v, tpr, p.lt);
+    const int k = vec_index(v, tpr, p.lt);
+    const int j = j0 + k;
     Pack<S, VEC> o;
     float n[VEC];
     if (standard) {
@@ -153,11 +168,11 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
       a[v][e] = vv;
       amax = __builtin_fmaxf(amax, __builtin_fabsf(vv));
     }
-    if (anorm != nullptr && p.live && (EX || j < nvec)) {
+    if (anorm != nullptr && p.live && (EX || k < jn)) {
       st_nt<S, VEC>(row_elem<EX>(anorm, base, (int64_t)j * VEC), o);
     }
   }
-  amax = row_reduce<EX>(amax, red_max, tpr, MaxOp());
+  amax = red.max(amax);
 
   const float s = mcop_div_rn(amax, FP8 ? 448.0f : 127.0f);
   if (p.live && p.lt == 0) scales[p.row] = s;
@@ -167,8 +182,9 @@ __device__ __forceinline__ void sq_row(const RowPos& p, const Pack<typename E::S
 
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int j = vec_index(v, tpr, p.lt);
-    if (p.live && (EX || j < nvec)) {
+    const int k = vec_index(v, tpr, p.lt);
+    const int j = j0 + k;
+    if (p.live && (EX || k < jn)) {
       Pack<uint8_t, VEC> q;
       if constexpr (FP8) {
         q = sq_fp8_codes<VEC>(a[v], amax, s, inv, s_ok, bounded);
@@ -212,9 +228,56 @@ k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   }
   shared_loads_first();
   Pack<typename E::S, VEC> xv[NV], rv[NV];
-  sq_load<E, VEC, NV, RES, EX>(p, x, res, hidden, tpr, xv, rv);
-  sq_row<E, EW, ES, VEC, NV, FP8, RES, EX>(p, xv, rv, wv, sv, out, scales, ares, anorm, hidden,
-                                            tpr, eps, flags, red_sum, red_max);
+  sq_load<E, VEC, NV, RES, EX>(p, 0, nvec, x, res, hidden, tpr, xv, rv);
+  WgRowReduce<EX> red{red_sum, red_max, tpr};
+  sq_row<E, EW, ES, VEC, NV, FP8, RES, EX>(p, 0, nvec, xv, rv, wv, sv, out, scales, ares, anorm,
+                                            hidden, tpr, eps, flags, red);
+}
+
+// Rows too wide for one workgroup's registers, read once (split_row.h): workgroup b takes slice
+// b % slices of row b / slices -- `slice_vecs` vectors, NV a lane -- and runs sq_row on it, the
+// row's partial sum of squares and absmax combined with the other slices' through the workspace
+// `ws`.  Every slice writes the row's scale (the same value).
+template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES>
+__global__ void __launch_bounds__(max_tpr(VEC, NV))
+k_rms_norm_smooth_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
+                              const typename E::S* __restrict__ x,
+                              const typename EW::S* __restrict__ w,
+                              const typename ES::S* __restrict__ sm,
+                              typename E::S* __restrict__ ares,
+                              typename E::S* __restrict__ anorm,
+                              const typename E::S* __restrict__ res, int64_t rows, int hidden,
+                              int slices, int slice_vecs, float eps, uint32_t flags,
+                              uint64_t* __restrict__ ws, int64_t timeout_ticks) {
+  __shared__ double red_sum[16];
+  __shared__ float red_max[16];
+  __shared__ double x_sum;
+  __shared__ float x_max;
+  const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x;
+  const int sl = (int)(blockIdx.x % (unsigned)slices);
+  RowPos p;
+  p.row = blockIdx.x / (unsigned)slices;
+  p.lrow = p.row;
+  p.lt = (int)threadIdx.x;
+  p.live = true;
+  const int j0 = sl * slice_vecs;
+  const int jn = min(slice_vecs, nvec - j0);
+  WVec<EW, VEC> wv[NV];
+  WVec<ES, VEC> sv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int64_t lj = (int64_t)(j0 + load_index(vec_index(v, tpr, p.lt), jn)) * VEC;
+    wv[v].p = ld<typename EW::S, VEC>(w + lj);
+    sv[v].p = ld<typename ES::S, VEC>(sm + lj);
+  }
+  shared_loads_first();
+  Pack<typename E::S, VEC> xv[NV], rv[NV];
+  sq_load<E, VEC, NV, RES, false>(p, j0, jn, x, res, hidden, tpr, xv, rv);
+  SplitRowReduce red{red_sum, red_max, tpr, ws, p.row, slices, sl,
+                     ws + split_ws_words(rows, slices) - 1, timeout_ticks, &x_sum, &x_max};
+  sq_row<E, EW, ES, VEC, NV, FP8, RES, false>(p, j0, jn, xv, rv, wv, sv, out, scales, ares, anorm,
+                                               hidden, tpr, eps, flags, red);
 }
 
 // Rows too wide for the registers: one 1024-lane workgroup per row and three passes over it --
@@ -463,6 +526,36 @@ static const void* kernel_of(int nv) {
   }
 }
 
+// Rows too wide for the register kernels, vector path: the split-row kernel when it applies, its
+// workspace from the stream-ordered allocator; MCOP_E_UNSUPPORTED when it does not.
+constexpr int kSqSplitNv = 4;
+
+template <class E, class EW, class ES, int VEC, bool FP8, bool RES>
+static int launch_split(const char* name, const Args& a, hipStream_t st) {
+  using S = typename E::S;
+  const void* kernel = reinterpret_cast<const void*>(
+      &k_rms_norm_smooth_quant_split<E, EW, ES, VEC, kSqSplitNv, FP8, RES>);
+  return split_run(name, kernel, kSqSplitNv, a.rows, a.hidden / VEC, nullptr, st,
+                   [&](int64_t r0, int64_t n, uint64_t* ws, const SplitPlan& p, auto launch) {
+    const int64_t off = r0 * (int64_t)a.hidden;
+    auto* o = static_cast<uint8_t*>(a.out) + off;
+    float* sc = a.scales + r0;
+    auto* xp = static_cast<const S*>(a.x) + off;
+    auto* wp = static_cast<const typename EW::S*>(a.w);
+    auto* sp = static_cast<const typename ES::S*>(a.sm);
+    auto* arp = a.ares == nullptr ? nullptr : static_cast<S*>(a.ares) + off;
+    auto* anp = a.anorm == nullptr ? nullptr : static_cast<S*>(a.anorm) + off;
+    auto* rp = a.res == nullptr ? nullptr : static_cast<const S*>(a.res) + off;
+    int h = a.hidden, slices = p.slices, slice_vecs = p.slice_vecs;
+    float e = a.eps;
+    uint32_t f = a.flags;
+    int64_t timeout = p.timeout_ticks;
+    void* args[] = {&o, &sc, &xp, &wp, &sp, &arp, &anp, &rp, &n, &h, &slices, &slice_vecs, &e,
+                    &f, &ws, &timeout};
+    return launch(args);
+  });
+}
+
 template <class E, class EW, class ES, bool FP8>
 static int dispatch(const Args& a, hipStream_t st) {
   constexpr int V = E::VEC;
@@ -475,6 +568,11 @@ static int dispatch(const Args& a, hipStream_t st) {
              : (r ? &kernel_of<E, EW, ES, 1, FP8, true> : &kernel_of<E, EW, ES, 1, FP8, false>);
   if (!row_fits(a.hidden, vec_ok ? V : 1, kernels)) {
     const char* name = "rms_norm_dynamic_per_token_quant (smooth)";
+    if (vec_ok && split_rows_enabled()) {
+      const int rc = r ? launch_split<E, EW, ES, V, FP8, true>(name, a, st)
+                       : launch_split<E, EW, ES, V, FP8, false>(name, a, st);
+      if (rc != MCOP_E_UNSUPPORTED) return rc;
+    }
     if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
     using S = typename E::S;
     auto* o = static_cast<uint8_t*>(a.out);

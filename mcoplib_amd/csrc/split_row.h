@@ -30,6 +30,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/mcop_norm.h"
 #include "rowkern.h"
 
 namespace mcop {
@@ -133,6 +134,32 @@ __device__ __forceinline__ float split_max(uint64_t* slots, int slices, int sl, 
   return *lds;
 }
 
+// The row reductions of a split-row kernel: the workgroup's waves through LDS (row_reduce),
+// then the row's workgroups through the workspace (split_sum, split_max).
+struct SplitRowReduce {
+  double* red_sum;
+  float* red_max;
+  int tpr;
+  uint64_t* ws;
+  int64_t row;
+  int slices;
+  int sl;
+  uint64_t* err;
+  int64_t timeout_ticks;
+  double* x_sum;
+  float* x_max;
+  __device__ __forceinline__ double sum(double v) {
+    v = row_reduce<true>(v, red_sum, tpr, SumOp());
+    return split_sum(split_slots(ws, row, slices, 0), slices, sl, kSplitTag, v, err,
+                     timeout_ticks, x_sum);
+  }
+  __device__ __forceinline__ float max(float v) {
+    v = row_reduce<true>(v, red_max, tpr, MaxOp());
+    return split_max(split_slots(ws, row, slices, 1), slices, sl, kSplitTag, v, err,
+                     timeout_ticks, x_max);
+  }
+};
+
 __global__ void k_fill_u64(uint64_t* __restrict__ p, int64_t n);
 
 // Host side -------------------------------------------------------------------------------------
@@ -149,16 +176,53 @@ struct SplitPlan {
   int64_t timeout_ticks;
 };
 
-// Plans the split-row launches of `kernel` (one slice per workgroup, kSplitNv vectors a lane) for
-// `rows` rows of `nvec` vectors: false (no message set) when they do not apply (the row fits
+// Plans the split-row launches of `kernel` (one slice per workgroup, `nv` vectors a lane, at most
+// kSplitLanes lanes) for `rows` rows of `nvec` vectors: false (no message set) when they do not apply (the row fits
 // fewer than two slices or needs more than kSplitMaxSlices, the kernel spills, or the stream is
 // being captured into a graph), in which case the caller runs its multi-pass kernel instead.
-bool split_plan(const void* kernel, int64_t rows, int64_t nvec, hipStream_t st, SplitPlan* p);
+bool split_plan(const void* kernel, int nv, int64_t rows, int64_t nvec, hipStream_t st,
+                SplitPlan* p);
 
 // Zeroes the launch's workspace (`rows` rows of the plan) with a fill kernel and launches
 // `kernel` with `args` (its parameter list, as hipLaunchKernel takes it) over rows * S
 // workgroups; `static_ws` (the no-allocation scratch) only changes the trace line.
 int split_launch(const char* op, const void* kernel, void** args, const SplitPlan& p,
                  int64_t rows, uint64_t* ws, bool static_ws, hipStream_t st);
+
+// Runs a split-row kernel (`nv` vectors a lane) over `rows` rows of `nvec` vectors: plans it, takes its workspace
+// (`scratch`, the no-allocation entry point's array, or else the stream-ordered allocator,
+// released on the same stream after the launches), and launches it over chunks of at most
+// plan.chunk_rows rows.  For each chunk, launch_chunk(r0, n, ws, plan, launch) builds the
+// kernel's parameter list for rows [r0, r0 + n) and returns launch(args).  MCOP_E_UNSUPPORTED
+// (no message) when the split does not apply: the caller runs its multi-pass kernel.
+template <class LaunchChunk>
+int split_run(const char* op, const void* kernel, int nv, int64_t rows, int64_t nvec,
+              uint64_t* scratch, hipStream_t st, LaunchChunk&& launch_chunk) {
+  SplitPlan p;
+  if (!split_plan(kernel, nv, rows, nvec, st, &p)) return MCOP_E_UNSUPPORTED;
+  uint64_t* ws = scratch;
+  if (scratch != nullptr && p.ws_words > kSplitWsWords) {  // launches are sized to fit it
+    return set_error(MCOP_E_UNSUPPORTED, "%s: a launch needs %lld workspace words, more than "
+                     "the %lld of the no-allocation scratch", op, (long long)p.ws_words,
+                     (long long)kSplitWsWords);
+  }
+  if (scratch == nullptr &&
+      hipMallocAsync(reinterpret_cast<void**>(&ws), (size_t)p.ws_words * 8, st) != hipSuccess) {
+    (void)hipGetLastError();
+    return MCOP_E_UNSUPPORTED;
+  }
+  int rc = MCOP_OK;
+  for (int64_t r0 = 0; r0 < rows && rc == MCOP_OK; r0 += p.chunk_rows) {
+    const int64_t n = rows - r0 < p.chunk_rows ? rows - r0 : p.chunk_rows;
+    rc = launch_chunk(r0, n, ws, p, [&](void** args) {
+      return split_launch(op, kernel, args, p, n, ws, scratch != nullptr, st);
+    });
+  }
+  if (scratch == nullptr && hipFreeAsync(ws, st) != hipSuccess) {
+    (void)hipGetLastError();
+    return rc != MCOP_OK ? rc : set_error(MCOP_E_LAUNCH, "%s: hipFreeAsync failed", op);
+  }
+  return rc;
+}
 
 }  // namespace mcop

@@ -1,8 +1,8 @@
-"""Rows too wide for one workgroup's registers on the split-row kernels (H2 / H3: each row shared
-by several workgroups that exchange partial sums through a device workspace): bit for bit against
-the oracle and against the multi-pass kernels (forced with the library's test hook), over several
-row counts and a call that takes two launches, two streams at once, and a HIP graph capture
-(which takes the multi-pass kernel)."""
+"""Rows too wide for one workgroup's registers on the split-row kernels (H2 / H3 / H4: each row
+shared by several workgroups that exchange partial sums through a device workspace): bit for bit
+against the oracle and against the multi-pass kernels (forced with the library's test hook), over
+several row counts and a call that takes two launches, two streams at once, and a HIP graph
+capture (which takes the multi-pass kernel)."""
 
 import os
 import subprocess
@@ -15,7 +15,7 @@ import torch
 import oracle
 import mcoplib_amd._C  # noqa: F401  (registers torch.ops._C.*)
 from conftest import ROOT
-from mcoplib_amd import _lib, custom_ops
+from mcoplib_amd import _lib, custom_ops, op
 from gpu_util import DEV, assert_codes, assert_exact, assert_scales, gen, say
 
 pytestmark = pytest.mark.gpu
@@ -77,6 +77,77 @@ def test_split_h2_against_oracle_and_multipass(dtype, H, qdt):
                 _lib.set_split_rows(True)
             for a, b, what in zip(got, mp, ("codes", "scales", "residual")):
                 _same(a, b, f"{tag} {what}: split-row and multi-pass kernels differ")
+
+
+def _h4(x, w, sm, r, qdt, standard):
+    """One fused_rms_norm_dq call on the GPU; returns (codes, scales, after_res, after_norm)."""
+    q = torch.empty(x.shape, dtype=qdt, device=DEV)
+    s = torch.empty(x.shape[0], device=DEV)
+    ar = torch.empty(x.shape, dtype=x.dtype, device=DEV)
+    an = torch.empty_like(ar)
+    op.rms_norm_dynamic_per_token_quant(q, x.to(DEV), w.to(DEV), sm.to(DEV), s, 1e-6, ar, an,
+                                        None if r is None else r.to(DEV),
+                                        standard_norm=standard)
+    torch.cuda.synchronize()
+    return q.cpu(), s.cpu(), ar.cpu(), an.cpu()
+
+
+@pytest.mark.parametrize("dtype,wdt,sdt,H", [
+    (torch.bfloat16, torch.bfloat16, torch.bfloat16, 65544),
+    (torch.bfloat16, torch.bfloat16, torch.float32, 131072),
+    (torch.bfloat16, torch.float32, torch.float32, 262144),
+    (torch.float16, torch.float16, torch.float16, 65608),
+    (torch.float32, torch.float32, torch.float32, 32772),
+])
+@pytest.mark.parametrize("qdt", [torch.int8, torch.float8_e4m3fn])
+def test_split_h4_against_oracle_and_multipass(dtype, wdt, sdt, H, qdt):
+    say(f"split H4 {dtype} w={wdt} s={sdt} H={H} {qdt}")
+    T = 4
+    x, r = _x(T, H, 90, dtype, 3.0), _x(T, H, 91, dtype, 3.0)
+    w = _w(H, 92, wdt)
+    sm = (0.5 + 1.5 * torch.rand(H, generator=gen(93))).to(sdt)
+    for res in (None, r):
+        for standard in (False, True):
+            tag = f"res={res is not None} std={standard}"
+            q_ref, s_ref, ar_ref, an_ref = oracle.rms_norm_smooth_quant(x, w, sm, 1e-6, qdt, res,
+                                                                        standard)
+            got = _h4(x, w, sm, res, qdt, standard)
+            assert_exact(got[2], ar_ref, tag + " after_res")
+            assert_exact(got[3], an_ref, tag + " after_norm")
+            assert_scales(got[1], s_ref, tag + " scales")
+            assert_codes(got[0], q_ref, tag + " codes")
+            _lib.set_split_rows(False)
+            try:
+                mp = _h4(x, w, sm, res, qdt, standard)
+            finally:
+                _lib.set_split_rows(True)
+            for a, b, what in zip(got, mp, ("codes", "scales", "after_res", "after_norm")):
+                _same(a, b, f"{tag} {what}: split-row and multi-pass kernels differ")
+
+
+def test_split_h4_wide_fp8_workload_rows():
+    """The bench's wide-fp8 workload, 2048 x 131072 bf16 SmoothQuant to fp8 (bf16 weight, fp32
+    smooth): blocks of rows at the start, the middle and the end against the oracle."""
+    T, H = 2048, 131072
+    say(f"split: the wide-fp8 workload {T}x{H}")
+    x = _x(T, H, 94, torch.bfloat16)
+    w = _w(H, 95, torch.bfloat16)
+    sm = (0.5 + 1.5 * torch.rand(H, generator=gen(96))).to(torch.float32)
+    q = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=DEV)
+    s = torch.empty(T, device=DEV)
+    ar = torch.empty(T, H, dtype=torch.bfloat16, device=DEV)
+    an = torch.empty_like(ar)
+    op.rms_norm_dynamic_per_token_quant(q, x.to(DEV), w.to(DEV), sm.to(DEV), s, 1e-6, ar, an,
+                                        None)
+    torch.cuda.synchronize()
+    for b0 in (0, 1000, 1984):
+        sel = slice(b0, b0 + 64)
+        q_ref, s_ref, ar_ref, an_ref = oracle.rms_norm_smooth_quant(x[sel], w, sm, 1e-6,
+                                                                    torch.float8_e4m3fn)
+        assert_exact(ar[sel], ar_ref, f"after_res rows {b0}+")
+        assert_exact(an[sel], an_ref, f"after_norm rows {b0}+")
+        assert_scales(s[sel], s_ref, f"scales rows {b0}+")
+        assert_codes(q[sel], q_ref, f"codes rows {b0}+")
 
 
 @pytest.mark.parametrize("T", [1, 3, 250])
