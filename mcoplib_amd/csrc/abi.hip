@@ -193,7 +193,7 @@ int wall_clock_khz(int dev) {
 }
 }  // namespace
 
-bool split_plan(const void* kernel, int nv, int64_t rows, int64_t nvec, hipStream_t st,
+bool split_plan(const SplitKernel* cands, int ncand, int64_t rows, int64_t nvec, hipStream_t st,
                 SplitPlan* p) {
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
@@ -207,27 +207,37 @@ bool split_plan(const void* kernel, int nv, int64_t rows, int64_t nvec, hipStrea
     return false;
   }
   const int clk = wall_clock_khz(dev);
-  const int64_t slices = ceil_div(nvec, (int64_t)nv * kSplitLanes);
-  if (clk <= 0 || slices < 2 || slices > kSplitMaxSlices) return false;
-  const int64_t slice_vecs = ceil_div(nvec, slices);
-  const int64_t lanes = round64(ceil_div(slice_vecs, nv));
-  if (blocks_per_cu(kernel, (int)lanes) < 1) return false;  // spills (or cannot launch)
-  p->slices = (int)slices;
-  p->slice_vecs = (int)slice_vecs;
-  p->lanes = (int)lanes;
-  p->chunk_rows = std::min<int64_t>(rows, (kSplitWsWords - 1) / (4 * slices));
-  p->ws_words = split_ws_words(p->chunk_rows, (int)slices);
+  if (clk <= 0) return false;
+  int64_t best = 0;
+  for (int c = 0; c < ncand; ++c) {
+    const int nv = cands[c].nv;
+    const int64_t slices = ceil_div(nvec, (int64_t)nv * kSplitLanes);
+    if (slices < 2 || slices > kSplitMaxSlices) continue;
+    const int64_t slice_vecs = ceil_div(nvec, slices);
+    const int64_t lanes = round64(ceil_div(slice_vecs, nv));
+    const int64_t resident = blocks_per_cu(cands[c].fn, (int)lanes) * lanes * nv;
+    if (resident <= best) continue;  // spills (or cannot launch), or keeps less resident
+    best = resident;
+    p->kernel = cands[c].fn;
+    p->nv = nv;
+    p->slices = (int)slices;
+    p->slice_vecs = (int)slice_vecs;
+    p->lanes = (int)lanes;
+  }
+  if (best == 0) return false;
+  p->chunk_rows = std::min<int64_t>(rows, (kSplitWsWords - 1) / (4 * p->slices));
+  p->ws_words = split_ws_words(p->chunk_rows, p->slices);
   p->timeout_ticks = (int64_t)clk * 250;  // 250 ms of the wall clock
   return true;
 }
 
-int split_launch(const char* op, const void* kernel, void** args, const SplitPlan& p,
-                 int64_t rows, uint64_t* ws, bool static_ws, hipStream_t st) {
+int split_launch(const char* op, void** args, const SplitPlan& p, int64_t rows, uint64_t* ws,
+                 bool static_ws, hipStream_t st) {
   const int64_t words = split_ws_words(rows, p.slices);
   hipLaunchKernelGGL(k_fill_u64, dim3((unsigned)ceil_div(words, 256)), dim3(256), 0, st, ws,
                      words);
   if (int rc = check_launch(op)) return rc;
-  const hipError_t e = hipLaunchKernel(kernel, dim3((unsigned)(rows * p.slices)),
+  const hipError_t e = hipLaunchKernel(p.kernel, dim3((unsigned)(rows * p.slices)),
                                        dim3((unsigned)p.lanes), args, 0, st);
   if (e != hipSuccess) {
     (void)hipGetLastError();

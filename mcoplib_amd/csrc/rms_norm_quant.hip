@@ -464,9 +464,10 @@ static int launch_split(const char* name, void* out, float* scales, const void* 
                         const void* w, const float* scale_ub, void* res, int64_t rows,
                         int hidden, float eps, uint64_t* scratch, hipStream_t st) {
   using S = typename E::S;
-  const void* kernel =
-      reinterpret_cast<const void*>(&k_rms_norm_quant_split<E, VEC, kSplitNv, FP8, RES, MODE>);
-  return split_run(name, kernel, kSplitNv, rows, hidden / VEC, scratch, st,
+  auto fn = [](auto k) { return reinterpret_cast<const void*>(k); };
+  const SplitKernel k8{fn(&k_rms_norm_quant_split<E, VEC, 8, FP8, RES, MODE>), 8};
+  const SplitKernel k4{fn(&k_rms_norm_quant_split<E, VEC, 4, FP8, RES, MODE>), 4};
+  return split_run(name, {k8, k4}, rows, hidden / VEC, scratch, st,
                    [&](int64_t r0, int64_t n, uint64_t* ws, const SplitPlan& p, auto launch) {
     auto* o = static_cast<uint8_t*>(out) + r0 * (int64_t)hidden;
     float* sc = scales + r0;

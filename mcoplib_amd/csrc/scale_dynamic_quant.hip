@@ -10,6 +10,7 @@
 
 #include "../../include/mcop_norm.h"
 #include "rowkern.h"
+#include "split_row.h"
 
 namespace mcop {
 
@@ -77,6 +78,65 @@ k_scale_dynamic_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
         for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(a[k][v][e] * inv);
         st_nt<uint8_t, VEC>(out + base + (int64_t)j * VEC, q);
       }
+    }
+  }
+}
+
+// Rows too wide for one workgroup's registers, read once (split_row.h): workgroup b takes slice
+// b % slices of row b / slices -- `slice_vecs` vectors, NV a lane -- and holds its products v in
+// registers; the slices' absmax values are combined through the workspace `ws` (split_max),
+// and every other step is the register kernel's, element by element.
+template <int VEC, int NV>
+__global__ void __launch_bounds__(max_tpr(VEC, NV))
+k_scale_dynamic_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
+                            const uint16_t* __restrict__ x, const float* __restrict__ sm,
+                            int64_t rows, int hidden, int slices, int slice_vecs,
+                            uint64_t* __restrict__ ws, int64_t timeout_ticks) {
+  __shared__ float red_max[16];
+  __shared__ float x_max;
+  const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x;
+  const int lt = (int)threadIdx.x;
+  const int sl = (int)(blockIdx.x % (unsigned)slices);
+  const int64_t row = blockIdx.x / (unsigned)slices;
+  const int j0 = sl * slice_vecs;
+  const int jn = min(slice_vecs, nvec - j0);
+  const int64_t base = row * (int64_t)hidden;
+  // Lanes past the slice end re-read the slice's first vector, which leaves the absmax unchanged.
+  auto in_of = [&](int v) { return vec_index(v, tpr, lt) < jn; };
+  auto lj_of = [&](int v) {
+    return (int64_t)(j0 + (in_of(v) ? vec_index(v, tpr, lt) : 0)) * VEC;
+  };
+  Pack<float, VEC> sv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) sv[v] = ld<float, VEC>(sm + lj_of(v));
+  shared_loads_first();
+  Pack<uint16_t, VEC> xv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) xv[v] = ld_nt<uint16_t, VEC>(x + base + lj_of(v));
+  float a[NV][VEC];
+  float amax = 0.0f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float t = BF16::to_f(xv[v].v[e]) * sv[v].v[e];
+      a[v][e] = t;
+      amax = __builtin_fmaxf(amax, __builtin_fabsf(t));
+    }
+  }
+  SplitRowReduce red{nullptr, red_max, tpr, ws, row, slices, sl,
+                     ws + split_ws_words(rows, slices) - 1, timeout_ticks, nullptr, &x_max};
+  amax = red.max(amax);
+  if (sl == 0 && lt == 0) scales[row] = amax * 0.00787401574803f;
+  const float inv = amax > 0.0f ? mcop_div_rn(127.0f, amax) : 0.0f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    if (in_of(v)) {
+      Pack<uint8_t, VEC> q;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(a[v][e] * inv);
+      st_nt<uint8_t, VEC>(out + base + lj_of(v), q);
     }
   }
 }
@@ -220,6 +280,26 @@ static const void* kernel_of(int nv) {
   }
 }
 
+// Rows too wide for the register kernels, vector path: the split-row kernel when it applies, its
+// workspace from the stream-ordered allocator; MCOP_E_UNSUPPORTED (no message) when it does not.
+static int launch_split(uint8_t* out, float* scales, const uint16_t* x, const float* sm,
+                        int64_t rows, int hidden, hipStream_t st) {
+  constexpr int V = BF16::VEC;
+  const SplitKernel k8{reinterpret_cast<const void*>(&k_scale_dynamic_quant_split<V, 8>), 8};
+  const SplitKernel k4{reinterpret_cast<const void*>(&k_scale_dynamic_quant_split<V, 4>), 4};
+  return split_run("scale_dynamic_quant", {k8, k4}, rows, hidden / V, nullptr, st,
+                   [&](int64_t r0, int64_t n, uint64_t* ws, const SplitPlan& p, auto launch) {
+    uint8_t* o = out + r0 * (int64_t)hidden;
+    float* sc = scales + r0;
+    const uint16_t* xp = x + r0 * (int64_t)hidden;
+    const float* sp = sm;
+    int h = hidden, slices = p.slices, slice_vecs = p.slice_vecs;
+    int64_t timeout = p.timeout_ticks;
+    void* args[] = {&o, &sc, &xp, &sp, &n, &h, &slices, &slice_vecs, &ws, &timeout};
+    return launch(args);
+  });
+}
+
 }  // namespace mcop
 
 extern "C" int mcop_scale_dynamic_quant(int8_t* out, float* scales, const void* input,
@@ -240,9 +320,13 @@ extern "C" int mcop_scale_dynamic_quant(int8_t* out, float* scales, const void* 
   auto st = static_cast<hipStream_t>(stream);
   const KernelOfNv kernels = vec_ok ? &kernel_of<V> : &kernel_of<1>;
   if (!row_fits(hidden_size, vec_ok ? V : 1, kernels)) {
-    if (!wide_rows_ok("scale_dynamic_quant", num_tokens)) return MCOP_E_UNSUPPORTED;
     auto* o = reinterpret_cast<uint8_t*>(out);
     auto* xp = static_cast<const uint16_t*>(input);
+    if (vec_ok && split_rows_enabled()) {
+      const int rc = launch_split(o, scales, xp, smooth, num_tokens, (int)hidden_size, st);
+      if (rc != MCOP_E_UNSUPPORTED) return rc;
+    }
+    if (!wide_rows_ok("scale_dynamic_quant", num_tokens)) return MCOP_E_UNSUPPORTED;
     if (vec_ok) {
       hipLaunchKernelGGL((k_scale_dynamic_quant_wide<V>), dim3((unsigned)num_tokens),
                          dim3(kWideLanes), 0, st, o, scales, xp, smooth, (int)hidden_size);

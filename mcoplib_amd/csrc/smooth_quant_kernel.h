@@ -528,14 +528,12 @@ static const void* kernel_of(int nv) {
 
 // Rows too wide for the register kernels, vector path: the split-row kernel when it applies, its
 // workspace from the stream-ordered allocator; MCOP_E_UNSUPPORTED when it does not.
-constexpr int kSqSplitNv = 4;
-
 template <class E, class EW, class ES, int VEC, bool FP8, bool RES>
 static int launch_split(const char* name, const Args& a, hipStream_t st) {
   using S = typename E::S;
-  const void* kernel = reinterpret_cast<const void*>(
-      &k_rms_norm_smooth_quant_split<E, EW, ES, VEC, kSqSplitNv, FP8, RES>);
-  return split_run(name, kernel, kSqSplitNv, a.rows, a.hidden / VEC, nullptr, st,
+  const SplitKernel k4{reinterpret_cast<const void*>(
+                           &k_rms_norm_smooth_quant_split<E, EW, ES, VEC, 4, FP8, RES>), 4};
+  return split_run(name, {k4}, a.rows, a.hidden / VEC, nullptr, st,
                    [&](int64_t r0, int64_t n, uint64_t* ws, const SplitPlan& p, auto launch) {
     const int64_t off = r0 * (int64_t)a.hidden;
     auto* o = static_cast<uint8_t*>(a.out) + off;

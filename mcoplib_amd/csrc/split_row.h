@@ -2,7 +2,7 @@
 // partial results between the workgroups that share a row, and the host-side plan of such a
 // launch.
 //
-// A row too wide for one workgroup's registers is cut into S slices of at most kSplitVecs
+// A row too wide for one workgroup's registers is cut into S slices of at most nv * kSplitLanes
 // 16-byte vectors; S consecutive workgroups (a "group") hold one slice each in registers, so the
 // row is read from HBM once, as in the register-resident kernels.  Workgroup b takes slice b % S
 // of row b / S of the launch's rows.  Where the one-workgroup kernels reduce across the row's
@@ -30,16 +30,16 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <initializer_list>
+
 #include "../../include/mcop_norm.h"
 #include "rowkern.h"
 
 namespace mcop {
 
-// Largest slice a workgroup holds: four 16-byte vectors a lane over 256 lanes (four waves: the
-// resident workgroups of a CU then fill its wave slots in steps of four).
-constexpr int kSplitNv = 4;
+// Slices are held by workgroups of at most 256 lanes (four waves: the resident workgroups of a
+// CU then fill its wave slots in steps of four), four or eight 16-byte vectors a lane.
 constexpr int kSplitLanes = 256;
-constexpr int kSplitVecs = kSplitNv * kSplitLanes;
 // Most slices per row (one polling lane each).
 constexpr int kSplitMaxSlices = 64;
 
@@ -168,6 +168,8 @@ __global__ void k_fill_u64(uint64_t* __restrict__ p, int64_t n);
 // shorter) over `lanes` lanes each, at most `chunk_rows` rows (chunk_rows * S workgroups) per
 // launch, a workspace of `ws_words` words.
 struct SplitPlan {
+  const void* kernel;
+  int nv;
   int slices;
   int slice_vecs;
   int lanes;
@@ -176,30 +178,41 @@ struct SplitPlan {
   int64_t timeout_ticks;
 };
 
-// Plans the split-row launches of `kernel` (one slice per workgroup, `nv` vectors a lane, at most
-// kSplitLanes lanes) for `rows` rows of `nvec` vectors: false (no message set) when they do not apply (the row fits
-// fewer than two slices or needs more than kSplitMaxSlices, the kernel spills, or the stream is
-// being captured into a graph), in which case the caller runs its multi-pass kernel instead.
-bool split_plan(const void* kernel, int nv, int64_t rows, int64_t nvec, hipStream_t st,
+// A split-row kernel instantiation and the vectors a lane it holds.
+struct SplitKernel {
+  const void* fn;
+  int nv;
+};
+
+// Plans the split-row launches (one slice per workgroup, at most kSplitLanes lanes) for `rows`
+// rows of `nvec` vectors, over the candidate kernels `cands`: the one that keeps the most row
+// vectors resident per CU (its workgroups per CU x lanes x nv, from its register use; the
+// workgroup's lifetime is mostly the exchanges' latency, so bytes resident set the bandwidth),
+// the earlier on a tie.  False (no message set) when none applies (the row fits fewer than two
+// slices or needs more than kSplitMaxSlices, the kernel spills, or the stream is being captured
+// into a graph), in which case the caller runs its multi-pass kernel instead.
+bool split_plan(const SplitKernel* cands, int ncand, int64_t rows, int64_t nvec, hipStream_t st,
                 SplitPlan* p);
 
-// Zeroes the launch's workspace (`rows` rows of the plan) with a fill kernel and launches
-// `kernel` with `args` (its parameter list, as hipLaunchKernel takes it) over rows * S
+// Zeroes the launch's workspace (`rows` rows of the plan) with a fill kernel and launches the
+// plan's kernel with `args` (its parameter list, as hipLaunchKernel takes it) over rows * S
 // workgroups; `static_ws` (the no-allocation scratch) only changes the trace line.
-int split_launch(const char* op, const void* kernel, void** args, const SplitPlan& p,
-                 int64_t rows, uint64_t* ws, bool static_ws, hipStream_t st);
+int split_launch(const char* op, void** args, const SplitPlan& p, int64_t rows, uint64_t* ws,
+                 bool static_ws, hipStream_t st);
 
-// Runs a split-row kernel (`nv` vectors a lane) over `rows` rows of `nvec` vectors: plans it, takes its workspace
+// Runs a split-row kernel (the planned one of `cands`) over `rows` rows of `nvec` vectors: plans it, takes its workspace
 // (`scratch`, the no-allocation entry point's array, or else the stream-ordered allocator,
 // released on the same stream after the launches), and launches it over chunks of at most
 // plan.chunk_rows rows.  For each chunk, launch_chunk(r0, n, ws, plan, launch) builds the
 // kernel's parameter list for rows [r0, r0 + n) and returns launch(args).  MCOP_E_UNSUPPORTED
 // (no message) when the split does not apply: the caller runs its multi-pass kernel.
 template <class LaunchChunk>
-int split_run(const char* op, const void* kernel, int nv, int64_t rows, int64_t nvec,
-              uint64_t* scratch, hipStream_t st, LaunchChunk&& launch_chunk) {
+int split_run(const char* op, std::initializer_list<SplitKernel> cands, int64_t rows,
+              int64_t nvec, uint64_t* scratch, hipStream_t st, LaunchChunk&& launch_chunk) {
   SplitPlan p;
-  if (!split_plan(kernel, nv, rows, nvec, st, &p)) return MCOP_E_UNSUPPORTED;
+  if (!split_plan(cands.begin(), (int)cands.size(), rows, nvec, st, &p)) {
+    return MCOP_E_UNSUPPORTED;
+  }
   uint64_t* ws = scratch;
   if (scratch != nullptr && p.ws_words > kSplitWsWords) {  // launches are sized to fit it
     return set_error(MCOP_E_UNSUPPORTED, "%s: a launch needs %lld workspace words, more than "
@@ -215,7 +228,7 @@ int split_run(const char* op, const void* kernel, int nv, int64_t rows, int64_t 
   for (int64_t r0 = 0; r0 < rows && rc == MCOP_OK; r0 += p.chunk_rows) {
     const int64_t n = rows - r0 < p.chunk_rows ? rows - r0 : p.chunk_rows;
     rc = launch_chunk(r0, n, ws, p, [&](void** args) {
-      return split_launch(op, kernel, args, p, n, ws, scratch != nullptr, st);
+      return split_launch(op, args, p, n, ws, scratch != nullptr, st);
     });
   }
   if (scratch == nullptr && hipFreeAsync(ws, st) != hipSuccess) {

@@ -1,10 +1,11 @@
-"""Rows too wide for one workgroup's registers on the split-row kernels (H2 / H3 / H4: each row
-shared by several workgroups that exchange partial sums through a device workspace): bit for bit
-against the oracle and against the multi-pass kernels (forced with the library's test hook), over
-several row counts and a call that takes two launches, two streams at once, and a HIP graph
-capture (which takes the multi-pass kernel)."""
+"""Rows too wide for one workgroup's registers on the split-row kernels (H2 / H3 / H4 / H5: each
+row shared by several workgroups that exchange partial sums through a device workspace): bit for
+bit against the oracle and against the multi-pass kernels (forced with the library's test hook),
+over several row counts and a call that takes several launches, two streams at once, and a HIP
+graph capture (which takes the multi-pass kernel)."""
 
 import os
+import re
 import subprocess
 import sys
 import threading
@@ -150,6 +151,47 @@ def test_split_h4_wide_fp8_workload_rows():
         assert_codes(q[sel], q_ref, f"codes rows {b0}+")
 
 
+def _h5(h, sm):
+    q, s = op.scale_dynamic_quant(h.to(DEV), sm.to(DEV), torch.int8)
+    torch.cuda.synchronize()
+    return q.cpu(), s.cpu().reshape(-1)
+
+
+@pytest.mark.parametrize("T,H", [(1, 65544), (5, 131072), (3, 262152), (130, 524288)])
+def test_split_h5_against_oracle_and_multipass(T, H):
+    say(f"split H5 {T}x{H}")
+    h = _x(T, H, 97, torch.bfloat16, 3.0)
+    sm = (0.5 + 1.5 * torch.rand(H, generator=gen(98))).to(torch.float32)
+    q_ref, s_ref = oracle.scale_dynamic_quant(h, sm)
+    got = _h5(h, sm)
+    assert_scales(got[1], s_ref, "scales")
+    assert_codes(got[0], q_ref, "codes")
+    _lib.set_split_rows(False)
+    try:
+        mp = _h5(h, sm)
+    finally:
+        _lib.set_split_rows(True)
+    for a, b, what in zip(got, mp, ("codes", "scales")):
+        _same(a, b, f"{what}: split-row and multi-pass kernels differ")
+
+
+def test_split_h5_wide_sdq_workload_rows():
+    """The bench's wide-sdq workload, 2048 x 131072 bf16 with fp32 smooth scales: blocks of rows
+    at the start, the middle and the end against the oracle."""
+    T, H = 2048, 131072
+    say(f"split: the wide-sdq workload {T}x{H}")
+    h = _x(T, H, 99, torch.bfloat16)
+    sm = (0.5 + 1.5 * torch.rand(H, generator=gen(100))).to(torch.float32)
+    q, s = op.scale_dynamic_quant(h.to(DEV), sm.to(DEV), torch.int8)
+    torch.cuda.synchronize()
+    s = s.reshape(-1)
+    for b0 in (0, 1000, 1984):
+        sel = slice(b0, b0 + 64)
+        q_ref, s_ref = oracle.scale_dynamic_quant(h[sel], sm)
+        assert_scales(s[sel], s_ref, f"scales rows {b0}+")
+        assert_codes(q[sel], q_ref, f"codes rows {b0}+")
+
+
 @pytest.mark.parametrize("T", [1, 3, 250])
 def test_split_h3_row_counts(T):
     """mcoplib's operator (1.5e-6 floor, +-127 codes) over a few row counts."""
@@ -168,24 +210,30 @@ def test_split_h3_row_counts(T):
 
 
 def test_split_launches_in_chunks():
-    """More rows than one launch's workspace holds (1023 rows of 64 slices, 524288-wide bf16
-    rows): two launches, the second on the rows, residual and codes after the first's."""
-    T, H = 1025, 524288
-    say(f"split: {T}x{H} bf16 with a residual (two launches)")
-    x, r, w = _x(T, H, 83, torch.bfloat16), _x(T, H, 84, torch.bfloat16), _w(H, 85,
-                                                                               torch.bfloat16)
-    rd = r.to(DEV)
+    """More rows than one launch's workspace holds (524288-wide bf16 rows with a residual: 1023
+    rows a launch at 64 slices of 1024 vectors, 2047 at 32 slices of 2048): several launches,
+    each later one on the rows, residual and codes after the one before.  Inputs are generated on
+    the GPU; rows on both sides of every launch boundary are checked against the oracle."""
+    T, H = 2050, 524288
+    say(f"split: {T}x{H} bf16 with a residual (several launches)")
+    g = torch.Generator(device=DEV).manual_seed(84)
+    x = torch.randn(T, H, device=DEV, generator=g).to(torch.bfloat16)
+    r = torch.randn(T, H, device=DEV, generator=g).to(torch.bfloat16)
+    w = _w(H, 85, torch.bfloat16)
+    sel = [slice(0, 3), slice(1020, 1027), slice(2044, 2050)]
+    x_rows = [x[s].cpu() for s in sel]
+    r_rows = [r[s].cpu() for s in sel]
     q = torch.empty(T, H, dtype=torch.int8, device=DEV)
-    s = torch.empty(T, 1, device=DEV)
-    torch.ops._C.rms_norm_dynamic_per_token_quant(q, x.to(DEV), w.to(DEV), s, 1e-6, None, rd)
+    s_all = torch.empty(T, 1, device=DEV)
+    torch.ops._C.rms_norm_dynamic_per_token_quant(q, x, w.to(DEV), s_all, 1e-6, None, r)
     torch.cuda.synchronize()
-    for b0 in (0, 1016, 1020):  # rows on both sides of the launch boundary (row 1023)
-        sel = slice(b0, b0 + 5)
-        q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant(x[sel], w, 1e-6,
-                                                                      torch.int8, None, r[sel])
-        assert_exact(rd[sel], r_ref, f"residual rows {b0}+")
-        assert_scales(s[sel], s_ref, f"scales rows {b0}+")
-        assert_codes(q[sel], q_ref, f"codes rows {b0}+")
+    for s, xs, rs in zip(sel, x_rows, r_rows):
+        q_ref, s_ref, r_ref = oracle.rms_norm_dynamic_per_token_quant(xs, w, 1e-6, torch.int8,
+                                                                      None, rs)
+        assert_exact(r[s], r_ref, f"residual rows {s.start}+")
+        assert_scales(s_all[s], s_ref, f"scales rows {s.start}+")
+        assert_codes(q[s], q_ref, f"codes rows {s.start}+")
+    del x, r, q
 
 
 def test_split_wide_int8_workload_all_rows():
@@ -306,5 +354,6 @@ def test_split_launch_decisions_are_traced():
     say(out.stdout[-2000:])
     assert out.returncode == 0, out.stderr[-3000:]
     assert "child ok" in out.stdout
-    assert "rows=4: split-row kernel, 16 slices of 1024 vectors over 256 lanes" in out.stdout
+    assert re.search(r"rows=4: split-row kernel, (8 slices of 2048|16 slices of 1024) vectors "
+                     r"over 256 lanes", out.stdout)
     assert "rows=4: multi-pass kernel" in out.stdout
