@@ -7,15 +7,17 @@
 //   x <- b(b(z * rho) * w)                            (:136-143: scale then weight multiply)
 // One pass over HBM: x, residual and weight are loaded once into VGPRs, residual is written
 // from registers before the reduction, x after it (8*H bytes per bf16 row, plus the weight).
-// Rows too wide for the registers take k_fused_add_rms_norm_wide: one 1024-lane workgroup per
-// row, the row's first 8 vectors a lane held in registers and (bf16, fp32) the next 8 in LDS
-// (one read of rows up to 131072 bf16 elements); beyond them two passes (sum of squares; then
-// residual and output), the second re-reading x and residual, which each lane then overwrites
-// at the same addresses.
+// Rows too wide for the registers take k_fused_add_rms_norm_split (the row split over several
+// workgroups, read once) or, under graph capture, on the scalar path and past 64 slices,
+// k_fused_add_rms_norm_wide: one 1024-lane workgroup per row, the row's first 8 vectors a lane
+// held in registers and (bf16, fp32) the next 8 in LDS (one read of rows up to 131072 bf16
+// elements); beyond them two passes (sum of squares; then residual and output), the second
+// re-reading x and residual, which each lane then overwrites at the same addresses.
 #include <hip/hip_runtime.h>
 
 #include "../../include/mcop_norm.h"
 #include "rowkern.h"
+#include "split_row.h"
 
 namespace mcop {
 
@@ -90,6 +92,72 @@ k_fused_add_rms_norm(typename E::S* __restrict__ x, int64_t x_stride,
         o.v[e] = E::from_f(rnd<E>(z[v][e] * rho) * E::to_f(wv[v].v[e]));
       }
       st_nt<S, VEC>(row_elem<EX>(x, xbase, (int64_t)j * VEC), o);
+    }
+  }
+}
+
+// Rows too wide for one workgroup's registers, read once (split_row.h): workgroup b takes slice
+// b % slices of row b / slices -- `slice_vecs` vectors, NV a lane -- holds its rounded sums z
+// in the dtype (packed) and its weight vectors, writes the residual, and combines the row's
+// sum of squares with the other slices' through the workspace `ws` (split_sum, in slice order)
+// before writing x.  The row index is uniform: scalar row bases, 32-bit offsets.
+template <class E, int VEC, int NV>
+__global__ void __launch_bounds__(max_tpr(VEC, NV))
+k_fused_add_rms_norm_split(typename E::S* __restrict__ x, int64_t x_stride,
+                           typename E::S* __restrict__ res, const typename E::S* __restrict__ w,
+                           int64_t rows, int hidden, int slices, int slice_vecs, float eps,
+                           uint64_t* __restrict__ ws, int64_t timeout_ticks) {
+  using S = typename E::S;
+  __shared__ double red_sum[16];
+  __shared__ double x_sum;
+  const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x;
+  const int lt = (int)threadIdx.x;
+  const int sl = (int)(blockIdx.x % (unsigned)slices);
+  const int64_t row = blockIdx.x / (unsigned)slices;
+  const int j0 = sl * slice_vecs;
+  const int jn = min(slice_vecs, nvec - j0);
+  const int64_t xbase = row * x_stride, rbase = row * (int64_t)hidden;
+  // Lanes past the slice end re-read the slice's first vector, which does not count.
+  auto in_of = [&](int v) { return vec_index(v, tpr, lt) < jn; };
+  auto lj_of = [&](int v) {
+    return (int64_t)(j0 + (in_of(v) ? vec_index(v, tpr, lt) : 0)) * VEC;
+  };
+  Pack<S, VEC> xv[NV], rv[NV], wv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) wv[v] = ld<S, VEC>(row_elem<true>(w, 0, lj_of(v)));
+  shared_loads_first();
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    xv[v] = ld_nt<S, VEC>(row_elem<true>(x, xbase, lj_of(v)));
+    rv[v] = ld_nt<S, VEC>(row_elem<true>(res, rbase, lj_of(v)));
+  }
+  double ss = 0.0;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    double vs = 0.0;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      xv[v].v[e] = E::from_f(E::to_f(xv[v].v[e]) + E::to_f(rv[v].v[e]));  // z
+      const double d = (double)E::to_f(xv[v].v[e]);
+      vs = __builtin_fma(d, d, vs);
+    }
+    ss += in_of(v) ? vs : 0.0;
+    if (in_of(v)) st_nt<S, VEC>(row_elem<true>(res, rbase, lj_of(v)), xv[v]);
+  }
+  SplitRowReduce red{red_sum, nullptr, tpr, ws, row, slices, sl,
+                     ws + split_ws_words(rows, slices) - 1, timeout_ticks, &x_sum, nullptr};
+  ss = red.sum(ss);
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    if (in_of(v)) {
+      Pack<S, VEC> o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        o.v[e] = E::from_f(rnd<E>(E::to_f(xv[v].v[e]) * rho) * E::to_f(wv[v].v[e]));
+      }
+      st_nt<S, VEC>(row_elem<true>(x, xbase, lj_of(v)), o);
     }
   }
 }
@@ -291,6 +359,29 @@ static const void* kernel_of(int nv) {
   }
 }
 
+// Rows too wide for the register kernels, vector path: the split-row kernel when it applies, its
+// workspace from the stream-ordered allocator; MCOP_E_UNSUPPORTED (no message) when it does not.
+template <class E, int VEC>
+static int launch_split(void* x, int64_t xs, void* res, const void* w, int64_t rows,
+                        int hidden, float eps, hipStream_t st) {
+  using S = typename E::S;
+  auto fn = [](auto k) { return reinterpret_cast<const void*>(k); };
+  const SplitKernel k8{fn(&k_fused_add_rms_norm_split<E, VEC, 8>), 8};
+  const SplitKernel k4{fn(&k_fused_add_rms_norm_split<E, VEC, 4>), 4};
+  return split_run("fused_add_rms_norm", {k8, k4}, rows, hidden / VEC, nullptr, st,
+                   [&](int64_t r0, int64_t n, uint64_t* ws, const SplitPlan& p, auto launch) {
+    S* xp = static_cast<S*>(x) + r0 * xs;
+    S* rp = static_cast<S*>(res) + r0 * (int64_t)hidden;
+    const S* wp = static_cast<const S*>(w);
+    int64_t stride = xs;
+    int h = hidden, slices = p.slices, slice_vecs = p.slice_vecs;
+    float e = eps;
+    int64_t timeout = p.timeout_ticks;
+    void* args[] = {&xp, &stride, &rp, &wp, &n, &h, &slices, &slice_vecs, &e, &ws, &timeout};
+    return launch(args);
+  });
+}
+
 template <class E>
 static int dispatch(void* x, int64_t xs, void* res, const void* w, int64_t rows, int64_t hidden,
                     float eps, hipStream_t st) {
@@ -298,6 +389,10 @@ static int dispatch(void* x, int64_t xs, void* res, const void* w, int64_t rows,
   const bool vec_ok = hidden % V == 0 && xs % V == 0 && aligned(16, x, res, w);
   const KernelOfNv kernels = vec_ok ? &kernel_of<E, V> : &kernel_of<E, 1>;
   if (!row_fits(hidden, vec_ok ? V : 1, kernels)) {
+    if (vec_ok && split_rows_enabled()) {
+      const int rc = launch_split<E, V>(x, xs, res, w, rows, (int)hidden, eps, st);
+      if (rc != MCOP_E_UNSUPPORTED) return rc;
+    }
     if (!wide_rows_ok("fused_add_rms_norm", rows)) return MCOP_E_UNSUPPORTED;
     using S = typename E::S;
     auto* xp = static_cast<S*>(x);

@@ -52,7 +52,7 @@ __device__ __forceinline__ Pack<uint8_t, VEC> sq_fp8_codes(const float* v, float
 
 // The lane's streamed vectors of one row's slice [j0, j0 + jn) (the whole row: 0, nvec): x
 // (and the residual); lanes past the slice end load its first vector.
-template <class E, int VEC, int NV, bool RES, bool EX>
+template <class E, int VEC, int NV, bool RES, bool EX, bool UA = EX>
 __device__ __forceinline__ void sq_load(const RowPos& p, int j0, int jn,
                                         const typename E::S* __restrict__ x,
                                         const typename E::S* __restrict__ res, int hidden,
@@ -64,8 +64,8 @@ __device__ __forceinline__ void sq_load(const RowPos& p, int j0, int jn,
   for (int v = 0; v < NV; ++v) {
     const int k = vec_index(v, tpr, p.lt);
     const int64_t lj = (int64_t)(j0 + (EX ? k : load_index(k, jn))) * VEC;
-    xv[v] = ld_nt<S, VEC>(row_elem<EX>(x, lbase, lj));
-    if constexpr (RES) rv[v] = ld_nt<S, VEC>(row_elem<EX>(res, lbase, lj));
+    xv[v] = ld_nt<S, VEC>(row_elem<UA>(x, lbase, lj));
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(row_elem<UA>(res, lbase, lj));
   }
 }
 
@@ -82,8 +82,10 @@ struct WgRowReduce {
 // One row (or, for tpr < blockDim, one of the workgroup's rows; or one slice [j0, j0 + jn) of a
 // row shared by several workgroups) given the lane's loaded vectors and its weight and smooth
 // vectors.  `red` combines the row's partial sum of squares and absmax (WgRowReduce, or the
-// split-row exchange).
-template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES, bool EX, class Red>
+// split-row exchange).  UA: the row index is uniform and the row's element offsets fit 32 bits
+// (scalar row base, one 32-bit offset per vector: row_elem<true>).
+template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES, bool EX, bool UA,
+          class Red>
 __device__ __forceinline__ void sq_row(const RowPos& p, int j0, int jn,
                                        const Pack<typename E::S, VEC>* xv,
                                        const Pack<typename E::S, VEC>* rv,
@@ -114,7 +116,7 @@ __device__ __forceinline__ void sq_row(const RowPos& p, int j0, int jn,
       a[v][e] = E::to_f(o.v[e]);  // b(a): what the later passes of the reference re-read
     }
     ss += in ? vs : 0.0;
-    if (ares != nullptr && p.live && in) st_nt<S, VEC>(row_elem<EX>(ares, base, (int64_t)j * VEC), o);
+    if (ares != nullptr && p.live && in) st_nt<S, VEC>(row_elem<UA>(ares, base, (int64_t)j * VEC), o);
   }
 
   ss = red.sum(ss);
@@ -169,7 +171,7 @@ __device__ __forceinline__ void sq_row(const RowPos& p, int j0, int jn,
       amax = __builtin_fmaxf(amax, __builtin_fabsf(vv));
     }
     if (anorm != nullptr && p.live && (EX || k < jn)) {
-      st_nt<S, VEC>(row_elem<EX>(anorm, base, (int64_t)j * VEC), o);
+      st_nt<S, VEC>(row_elem<UA>(anorm, base, (int64_t)j * VEC), o);
     }
   }
   amax = red.max(amax);
@@ -192,7 +194,7 @@ __device__ __forceinline__ void sq_row(const RowPos& p, int j0, int jn,
 #pragma unroll
         for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-127>(a[v][e] * inv);
       }
-      st_nt<uint8_t, VEC>(row_elem<EX>(out, base, (int64_t)j * VEC), q);
+      st_nt<uint8_t, VEC>(row_elem<UA>(out, base, (int64_t)j * VEC), q);
     }
   }
 }
@@ -230,8 +232,8 @@ k_rms_norm_smooth_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
   Pack<typename E::S, VEC> xv[NV], rv[NV];
   sq_load<E, VEC, NV, RES, EX>(p, 0, nvec, x, res, hidden, tpr, xv, rv);
   WgRowReduce<EX> red{red_sum, red_max, tpr};
-  sq_row<E, EW, ES, VEC, NV, FP8, RES, EX>(p, 0, nvec, xv, rv, wv, sv, out, scales, ares, anorm,
-                                            hidden, tpr, eps, flags, red);
+  sq_row<E, EW, ES, VEC, NV, FP8, RES, EX, EX>(p, 0, nvec, xv, rv, wv, sv, out, scales, ares,
+                                                anorm, hidden, tpr, eps, flags, red);
 }
 
 // Rows too wide for one workgroup's registers, read once (split_row.h): workgroup b takes slice
@@ -268,16 +270,16 @@ k_rms_norm_smooth_quant_split(uint8_t* __restrict__ out, float* __restrict__ sca
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int64_t lj = (int64_t)(j0 + load_index(vec_index(v, tpr, p.lt), jn)) * VEC;
-    wv[v].p = ld<typename EW::S, VEC>(w + lj);
-    sv[v].p = ld<typename ES::S, VEC>(sm + lj);
+    wv[v].p = ld<typename EW::S, VEC>(row_elem<true>(w, 0, lj));
+    sv[v].p = ld<typename ES::S, VEC>(row_elem<true>(sm, 0, lj));
   }
   shared_loads_first();
   Pack<typename E::S, VEC> xv[NV], rv[NV];
-  sq_load<E, VEC, NV, RES, false>(p, j0, jn, x, res, hidden, tpr, xv, rv);
+  sq_load<E, VEC, NV, RES, false, true>(p, j0, jn, x, res, hidden, tpr, xv, rv);
   SplitRowReduce red{red_sum, red_max, tpr, ws, p.row, slices, sl,
                      ws + split_ws_words(rows, slices) - 1, timeout_ticks, &x_sum, &x_max};
-  sq_row<E, EW, ES, VEC, NV, FP8, RES, false>(p, j0, jn, xv, rv, wv, sv, out, scales, ares, anorm,
-                                               hidden, tpr, eps, flags, red);
+  sq_row<E, EW, ES, VEC, NV, FP8, RES, false, true>(p, j0, jn, xv, rv, wv, sv, out, scales, ares,
+                                                     anorm, hidden, tpr, eps, flags, red);
 }
 
 // Rows too wide for the registers: one 1024-lane workgroup per row and three passes over it --

@@ -1,8 +1,8 @@
-"""Rows too wide for one workgroup's registers on the split-row kernels (H2 / H3 / H4 / H5: each
-row shared by several workgroups that exchange partial sums through a device workspace): bit for
-bit against the oracle and against the multi-pass kernels (forced with the library's test hook),
-over several row counts and a call that takes several launches, two streams at once, and a HIP
-graph capture (which takes the multi-pass kernel)."""
+"""Rows too wide for one workgroup's registers on the split-row kernels (H1 / H2 / H3 / H4 / H5:
+each row shared by several workgroups that exchange partial sums through a device workspace):
+bit for bit against the oracle and against the multi-pass kernels (forced with the library's
+test hook), over several row counts and a call that takes several launches, two streams at
+once, and a HIP graph capture (which takes the multi-pass kernel)."""
 
 import os
 import re
@@ -190,6 +190,59 @@ def test_split_h5_wide_sdq_workload_rows():
         q_ref, s_ref = oracle.scale_dynamic_quant(h[sel], sm)
         assert_scales(s[sel], s_ref, f"scales rows {b0}+")
         assert_codes(q[sel], q_ref, f"codes rows {b0}+")
+
+
+def _h1(x, r, w, pad):
+    """One vLLM fused_add_rms_norm call on the GPU (x a row-strided view when pad > 0); returns
+    (x, residual) on the CPU, and checks that the padding columns are untouched."""
+    T, H = x.shape
+    big = torch.randn(T, H + pad, generator=gen(101)).to(x.dtype)
+    big[:, :H] = x
+    bigd = big.to(DEV)
+    xd = bigd[:, :H]
+    rd = r.to(DEV)
+    torch.ops._C.fused_add_rms_norm(xd, rd, w.to(DEV), 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(bigd[:, H:].cpu(), big[:, H:]), "padding columns changed"
+    return xd.contiguous().cpu(), rd.cpu()
+
+
+@pytest.mark.parametrize("dtype,H", [(torch.bfloat16, 65544), (torch.bfloat16, 131072),
+                                     (torch.bfloat16, 524288), (torch.float16, 65608),
+                                     (torch.float32, 32772), (torch.float32, 65536)])
+@pytest.mark.parametrize("pad", [0, 24])
+def test_split_h1_against_oracle_and_multipass(dtype, H, pad):
+    say(f"split H1 {dtype} H={H} pad={pad}")
+    T = 4
+    x, r, w = _x(T, H, 102, dtype), _x(T, H, 103, dtype), _w(H, 104, dtype)
+    x_ref, r_ref = oracle.fused_add_rms_norm(x, r, w, 1e-6)
+    got = _h1(x, r, w, pad)
+    assert_exact(got[1], r_ref, "residual")
+    assert_exact(got[0], x_ref, "output")
+    _lib.set_split_rows(False)
+    try:
+        mp = _h1(x, r, w, pad)
+    finally:
+        _lib.set_split_rows(True)
+    for a, b, what in zip(got, mp, ("output", "residual")):
+        _same(a, b, f"{what}: split-row and multi-pass kernels differ")
+
+
+def test_split_h1_wide_fused_workload_rows():
+    """The bench's wide-fused workload, 2048 x 131072 bf16: blocks of rows at the start, the
+    middle and the end against the oracle."""
+    T, H = 2048, 131072
+    say(f"split: the wide-fused workload {T}x{H}")
+    x, r, w = _x(T, H, 105, torch.bfloat16), _x(T, H, 106, torch.bfloat16), _w(H, 107,
+                                                                                torch.bfloat16)
+    xd, rd = x.to(DEV), r.to(DEV)
+    torch.ops._C.fused_add_rms_norm(xd, rd, w.to(DEV), 1e-6)
+    torch.cuda.synchronize()
+    for b0 in (0, 1000, 1984):
+        sel = slice(b0, b0 + 64)
+        x_ref, r_ref = oracle.fused_add_rms_norm(x[sel], r[sel], w, 1e-6)
+        assert_exact(rd[sel], r_ref, f"residual rows {b0}+")
+        assert_exact(xd[sel], x_ref, f"output rows {b0}+")
 
 
 @pytest.mark.parametrize("T", [1, 3, 250])
