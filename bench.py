@@ -279,7 +279,8 @@ WORKLOADS = {
     "head-norm": Workload("head-norm", 65536 * 8, 128, 1e-6, "head_norm"),
     # the un-normed SmoothQuant sibling (scale_dynamic_quant) at SmoothQuant's shape
     "sdq": Workload("sdq", 16384, 7168, 0.0, "sdq"),
-    # rows wider than the registers hold: each operator's multi-pass kernel
+    # rows wider than the registers hold: the split-row kernels of H1, H2/H3, H4 and H5 (the row
+    # shared by several workgroups, read once), each other operator's multi-pass kernel
     "wide-int8": Workload("wide-int8", 2048, 131072, 1e-6, "add_norm_int8"),
     "wide-fused": Workload("wide-fused", 2048, 131072, 1e-6, "fused_add"),
     "wide-fp8": Workload("wide-fp8", 2048, 131072, 1e-6, "smooth_fp8"),
@@ -298,8 +299,14 @@ KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "norm_int8": "k_rms_norm_qua
                "sdq": "k_scale_dynamic_quant"}
 
 
+# kinds whose wide rows take a split-row kernel (the others a multi-pass kernel)
+SPLIT_KINDS = {"add_norm_int8", "fused_add", "smooth_fp8", "sdq"}
+
+
 def kernel_name(wl) -> str:
-    return KERNEL_NAME[wl.kind] + ("_wide" if wl.name.startswith("wide-") else "")
+    if not wl.name.startswith("wide-"):
+        return KERNEL_NAME[wl.kind]
+    return KERNEL_NAME[wl.kind] + ("_split" if wl.kind in SPLIT_KINDS else "_wide")
 
 
 # Compute-free kernels with a configuration's access pattern (bench_kernels/mcop_pattern.h), at the
@@ -330,16 +337,16 @@ KERNEL_SOURCES = {
     "k_rms_norm_group_quant": ["group_quant.hip"],
     "k_rms_norm": ["norm_kernel.h", "rms_norm.hip", "rms_norm_bf16.hip", "rms_norm_f16.hip"],
 }
-SHARED_SOURCES = ["rowkern.h", "numerics.h", "abi.hip"]
+SHARED_SOURCES = ["rowkern.h", "numerics.h", "abi.hip", "split_row.h"]
 
 
 def kernel_source_hash(kernel: str, root: Path = ROOT) -> str:
     """First 16 hex digits of the SHA-256 over a kernel's source files (name and text, in name
-    order) and the hipcc flags of mcoplib_amd/_build.py (`kernel` may carry the _wide suffix of
-    the multi-pass form, which lives in the same files)."""
+    order) and the hipcc flags of mcoplib_amd/_build.py (`kernel` may carry the _wide or _split
+    suffix of the multi-pass or split-row form, which live in the same files)."""
     import hashlib
 
-    base = kernel[:-len("_wide")] if kernel.endswith("_wide") else kernel
+    base = re.sub(r"_(wide|split)$", "", kernel)
     h = hashlib.sha256()
     for name in sorted(KERNEL_SOURCES[base] + SHARED_SOURCES):
         h.update(name.encode() + b"\0")

@@ -211,7 +211,7 @@ bool split_plan(const SplitKernel* cands, int ncand, int64_t rows, int64_t nvec,
   int64_t best = 0;
   for (int c = 0; c < ncand; ++c) {
     const int nv = cands[c].nv;
-    const int64_t slices = ceil_div(nvec, (int64_t)nv * kSplitLanes);
+    const int64_t slices = ceil_div(nvec, (int64_t)nv * cands[c].lanes);
     if (slices < 2 || slices > kSplitMaxSlices) continue;
     const int64_t slice_vecs = ceil_div(nvec, slices);
     const int64_t lanes = round64(ceil_div(slice_vecs, nv));

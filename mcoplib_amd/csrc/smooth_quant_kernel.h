@@ -533,8 +533,10 @@ static const void* kernel_of(int nv) {
 template <class E, class EW, class ES, int VEC, bool FP8, bool RES>
 static int launch_split(const char* name, const Args& a, hipStream_t st) {
   using S = typename E::S;
+  // 512-lane workgroups (half the slices, so half the exchanges per row for the same resident
+  // vectors per CU): 450 us against 469 us at 256 lanes for 2048 x 131072 bf16 fp8
   const SplitKernel k4{reinterpret_cast<const void*>(
-                           &k_rms_norm_smooth_quant_split<E, EW, ES, VEC, 4, FP8, RES>), 4};
+                           &k_rms_norm_smooth_quant_split<E, EW, ES, VEC, 4, FP8, RES>), 4, 512};
   return split_run(name, {k4}, a.rows, a.hidden / VEC, nullptr, st,
                    [&](int64_t r0, int64_t n, uint64_t* ws, const SplitPlan& p, auto launch) {
     const int64_t off = r0 * (int64_t)a.hidden;

@@ -37,8 +37,9 @@
 
 namespace mcop {
 
-// Slices are held by workgroups of at most 256 lanes (four waves: the resident workgroups of a
-// CU then fill its wave slots in steps of four), four or eight 16-byte vectors a lane.
+// Slices are held by workgroups of at most 256 lanes by default (four waves: the resident
+// workgroups of a CU then fill its wave slots in steps of four), four or eight 16-byte vectors
+// a lane.
 constexpr int kSplitLanes = 256;
 // Most slices per row (one polling lane each).
 constexpr int kSplitMaxSlices = 64;
@@ -178,15 +179,16 @@ struct SplitPlan {
   int64_t timeout_ticks;
 };
 
-// A split-row kernel instantiation and the vectors a lane it holds.
+// A split-row kernel instantiation, the vectors a lane it holds and its most lanes per
+// workgroup (at most its launch bound).
 struct SplitKernel {
   const void* fn;
   int nv;
+  int lanes = kSplitLanes;
 };
 
-// Plans the split-row launches (one slice per workgroup, at most kSplitLanes lanes) for `rows`
-// rows of `nvec` vectors, over the candidate kernels `cands`: the one that keeps the most row
-// vectors resident per CU (its workgroups per CU x lanes x nv, from its register use; the
+// Plans the split-row launches (one slice per workgroup) for `rows` rows of `nvec` vectors, over
+// the candidate kernels `cands`: the one that keeps the most row vectors resident per CU (its workgroups per CU x lanes x nv, from its register use; the
 // workgroup's lifetime is mostly the exchanges' latency, so bytes resident set the bandwidth),
 // the earlier on a tie.  False (no message set) when none applies (the row fits fewer than two
 // slices or needs more than kSplitMaxSlices, the kernel spills, or the stream is being captured
