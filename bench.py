@@ -71,6 +71,9 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run three 1 GiB device-to-device copies (a kernel of known "
                          "traffic, used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+    ap.add_argument("--multi-pass", action="store_true",
+                    help="run rows wider than the registers on the multi-pass kernels (the "
+                         "split-row kernels' fallback under graph capture), for comparison")
     ap.add_argument("--pattern", default=None, choices=["natural", "4", "3", "2"],
                     help="time only the workload's compute-free access-pattern kernel, at its "
                          "natural occupancy or capped to 4, 3 or 2 workgroups per CU (for "
@@ -299,14 +302,17 @@ KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "norm_int8": "k_rms_norm_qua
                "sdq": "k_scale_dynamic_quant"}
 
 
-# kinds whose wide rows take a split-row kernel (the others a multi-pass kernel)
+# kinds whose wide rows take a split-row kernel (the others a multi-pass kernel); --multi-pass
+# sends them to the multi-pass kernels too
 SPLIT_KINDS = {"add_norm_int8", "fused_add", "smooth_fp8", "sdq"}
+MULTI_PASS = False
 
 
 def kernel_name(wl) -> str:
     if not wl.name.startswith("wide-"):
         return KERNEL_NAME[wl.kind]
-    return KERNEL_NAME[wl.kind] + ("_split" if wl.kind in SPLIT_KINDS else "_wide")
+    split = wl.kind in SPLIT_KINDS and not MULTI_PASS
+    return KERNEL_NAME[wl.kind] + ("_split" if split else "_wide")
 
 
 # Compute-free kernels with a configuration's access pattern (bench_kernels/mcop_pattern.h), at the
@@ -978,6 +984,11 @@ def main() -> int:
     sys.path.insert(0, str(ROOT))
     import mcoplib  # noqa: F401  (fails loudly if libmcop_norm.so is missing)
 
+    if args.multi_pass:
+        global MULTI_PASS
+        from mcoplib_amd import _lib
+        _lib.set_split_rows(False)
+        MULTI_PASS = True
     dev = "cuda:0"
     torch.cuda.set_device(0)
     wl = WORKLOADS[args.workload]
