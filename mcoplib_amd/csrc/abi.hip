@@ -211,9 +211,12 @@ bool split_plan(const SplitKernel* cands, int ncand, int64_t rows, int64_t nvec,
   int64_t best = 0;
   for (int c = 0; c < ncand; ++c) {
     const int nv = cands[c].nv;
-    const int64_t slices = ceil_div(nvec, (int64_t)nv * cands[c].lanes);
+    const int64_t align = std::max(cands[c].align, 1);
+    // nv * lanes is a multiple of align (both powers of two), so the rounded slice still fits
+    const int64_t slice_vecs =
+        ceil_div(ceil_div(nvec, ceil_div(nvec, (int64_t)nv * cands[c].lanes)), align) * align;
+    const int64_t slices = ceil_div(nvec, slice_vecs);
     if (slices < 2 || slices > kSplitMaxSlices) continue;
-    const int64_t slice_vecs = ceil_div(nvec, slices);
     const int64_t lanes = round64(ceil_div(slice_vecs, nv));
     const int64_t resident = blocks_per_cu(cands[c].fn, (int)lanes) * lanes * nv;
     if (resident <= best) continue;  // spills (or cannot launch), or keeps less resident

@@ -25,6 +25,7 @@
 
 #include "../../include/mcop_norm.h"
 #include "rowkern.h"
+#include "split_row.h"
 
 namespace mcop {
 
@@ -182,6 +183,95 @@ k_rms_norm_group_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
       for (int e = 0; e < VEC; ++e) q.v[e] = q_i8_in_range(a[v][e], inv);
     }
     st_nt<uint8_t, VEC>(row_elem<EX>(out, base, (int64_t)j * VEC), q);
+  }
+}
+
+// Rows too wide for one workgroup's registers, read once (split_row.h): workgroup b takes slice
+// b % slices of row b / slices -- `slice_vecs` vectors, a multiple of the group's G / VEC
+// vectors, NV a lane -- and combines the row's sum of squares with the other slices' through
+// the workspace `ws` (split_sum, in slice order); groups lie inside one slice, in G / VEC
+// aligned lanes of one wave, so their absmax, scales and codes are the register kernel's.  The
+// row index is uniform: scalar row bases, 32-bit offsets.
+template <class E, int VEC, int NV, bool FP8, bool RES>
+__global__ void __launch_bounds__(max_tpr(VEC, NV))
+__attribute__((amdgpu_waves_per_eu(NV == 8 ? 4 : 1)))
+k_rms_norm_group_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
+                             const typename E::S* __restrict__ x,
+                             const typename E::S* __restrict__ w,
+                             const float* __restrict__ scale_ub, typename E::S* __restrict__ res,
+                             int64_t rows, int hidden, float eps, int group,
+                             int64_t scale_row_stride, int64_t scale_group_stride, int slices,
+                             int slice_vecs, uint64_t* __restrict__ ws, int64_t timeout_ticks) {
+  using S = typename E::S;
+  __shared__ double red_sum[16];
+  __shared__ double x_sum;
+  const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x;
+  const int lt = (int)threadIdx.x;
+  const int sl = (int)(blockIdx.x % (unsigned)slices);
+  const int64_t row = blockIdx.x / (unsigned)slices;
+  const int j0 = sl * slice_vecs;
+  const int jn = min(slice_vecs, nvec - j0);
+  const int64_t base = row * (int64_t)hidden;
+  // Lanes past the slice end (whole groups) re-read the slice's first vector and store nothing.
+  auto in_of = [&](int v) { return vec_index(v, tpr, lt) < jn; };
+  auto lj_of = [&](int v) {
+    return (int64_t)(j0 + (in_of(v) ? vec_index(v, tpr, lt) : 0)) * VEC;
+  };
+  Pack<S, VEC> xv[NV], rv[NV], wv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) wv[v] = ld<S, VEC>(row_elem<true>(w, 0, lj_of(v)));
+  shared_loads_first();
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    xv[v] = ld_nt<S, VEC>(row_elem<true>(x, base, lj_of(v)));
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(row_elem<true>(res, base, lj_of(v)));
+  }
+  float a[NV][VEC];
+  double ss = 0.0;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    double vs = 0.0;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float t = E::to_f(xv[v].v[e]);
+      if constexpr (RES) t += E::to_f(rv[v].v[e]);
+      a[v][e] = t;
+      const double d = (double)t;
+      vs = __builtin_fma(d, d, vs);
+    }
+    ss += in_of(v) ? vs : 0.0;
+    if constexpr (RES) {
+      if (in_of(v)) {
+        Pack<S, VEC> o;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(a[v][e]);
+        st_nt<S, VEC>(row_elem<true>(res, base, lj_of(v)), o);
+      }
+    }
+  }
+  SplitRowReduce red{red_sum, nullptr, tpr, ws, row, slices, sl,
+                     ws + split_ws_words(rows, slices) - 1, timeout_ticks, &x_sum, nullptr};
+  ss = red.sum(ss);
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+  const float ub = scale_ub != nullptr ? *scale_ub : 0.0f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    float m = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float y = rnd<E>(rnd<E>(a[v][e] * rho) * E::to_f(wv[v].v[e]));
+      a[v][e] = y;
+      m = __builtin_fmaxf(m, __builtin_fabsf(y));
+    }
+    m = group_max(m, group / VEC);
+    if (!in_of(v)) continue;
+    float s;
+    const Pack<uint8_t, VEC> q =
+        group_codes<E, VEC, FP8>(a[v], m, scale_ub != nullptr, ub, &s);
+    const int64_t o = lj_of(v);
+    if (o % group == 0) scales[row * scale_row_stride + (o / group) * scale_group_stride] = s;
+    st_nt<uint8_t, VEC>(row_elem<true>(out, base, o), q);
   }
 }
 
@@ -393,6 +483,36 @@ static void launch_nv(const Geometry& g, const GqArgs& a, hipStream_t st) {
 #undef MCOP_LAUNCH
 }
 
+// Rows too wide for the register kernels, vector path: the split-row kernel when it applies (its
+// slices whole groups), its workspace from the stream-ordered allocator; MCOP_E_UNSUPPORTED (no
+// message) when it does not.
+template <class E, int VEC, bool FP8, bool RES>
+static int launch_split(const char* name, const GqArgs& a, hipStream_t st) {
+  using S = typename E::S;
+  auto fn = [](auto k) { return reinterpret_cast<const void*>(k); };
+  const int gv = a.group / VEC;
+  const SplitKernel k8{fn(&k_rms_norm_group_quant_split<E, VEC, 8, FP8, RES>), 8, kSplitLanes,
+                       gv};
+  const SplitKernel k4{fn(&k_rms_norm_group_quant_split<E, VEC, 4, FP8, RES>), 4, kSplitLanes,
+                       gv};
+  return split_run(name, {k8, k4}, a.rows, a.hidden / VEC, nullptr, st,
+                   [&](int64_t r0, int64_t n, uint64_t* ws, const SplitPlan& p, auto launch) {
+    const int64_t off = r0 * (int64_t)a.hidden;
+    uint8_t* o = static_cast<uint8_t*>(a.out) + off;
+    float* sc = a.scales + r0 * a.srow;
+    const S* xp = static_cast<const S*>(a.x) + off;
+    const S* wp = static_cast<const S*>(a.w);
+    const float* ub = a.scale_ub;
+    S* rp = a.res == nullptr ? nullptr : static_cast<S*>(a.res) + off;
+    int h = a.hidden, grp = a.group, slices = p.slices, slice_vecs = p.slice_vecs;
+    float e = a.eps;
+    int64_t srow = a.srow, sgrp = a.sgrp, timeout = p.timeout_ticks;
+    void* args[] = {&o, &sc, &xp, &wp, &ub, &rp, &n, &h, &e, &grp, &srow, &sgrp, &slices,
+                    &slice_vecs, &ws, &timeout};
+    return launch(args);
+  });
+}
+
 template <class E, bool FP8>
 static int dispatch(const GqArgs& a, hipStream_t st) {
   const char* name = "rms_norm_per_block_quant";
@@ -402,6 +522,11 @@ static int dispatch(const GqArgs& a, hipStream_t st) {
       vec_ok ? (a.res ? &kernel_of<E, V, FP8, true> : &kernel_of<E, V, FP8, false>)
              : (a.res ? &kernel_of<E, 1, FP8, true> : &kernel_of<E, 1, FP8, false>);
   if (!row_fits(a.hidden, vec_ok ? V : 1, kernels, 64)) {
+    if (vec_ok && split_rows_enabled()) {
+      const int rc = a.res ? launch_split<E, V, FP8, true>(name, a, st)
+                           : launch_split<E, V, FP8, false>(name, a, st);
+      if (rc != MCOP_E_UNSUPPORTED) return rc;
+    }
     if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
     using S = typename E::S;
     auto* o = static_cast<uint8_t*>(a.out);

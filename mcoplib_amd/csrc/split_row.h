@@ -179,12 +179,14 @@ struct SplitPlan {
   int64_t timeout_ticks;
 };
 
-// A split-row kernel instantiation, the vectors a lane it holds and its most lanes per
-// workgroup (at most its launch bound).
+// A split-row kernel instantiation, the vectors a lane it holds, its most lanes per workgroup
+// (at most its launch bound) and the multiple of vectors every slice but the last holds (slices
+// start on it: whole quantization groups).
 struct SplitKernel {
   const void* fn;
   int nv;
   int lanes = kSplitLanes;
+  int align = 1;
 };
 
 // Plans the split-row launches (one slice per workgroup) for `rows` rows of `nvec` vectors, over

@@ -1,8 +1,8 @@
-"""Rows too wide for one workgroup's registers on the split-row kernels (H1 / H2 / H3 / H4 / H5:
-each row shared by several workgroups that exchange partial sums through a device workspace):
-bit for bit against the oracle and against the multi-pass kernels (forced with the library's
-test hook), over several row counts and a call that takes several launches, two streams at
-once, and a HIP graph capture (which takes the multi-pass kernel)."""
+"""Rows too wide for one workgroup's registers on the split-row kernels (H1 / H2 / H3 / H4 / H5
+and the per-block quant: each row shared by several workgroups that exchange partial sums
+through a device workspace): bit for bit against the oracle and against the multi-pass kernels
+(forced with the library's test hook), over several row counts and a call that takes several
+launches, two streams at once, and a HIP graph capture (which takes the multi-pass kernel)."""
 
 import os
 import re
@@ -243,6 +243,73 @@ def test_split_h1_wide_fused_workload_rows():
         x_ref, r_ref = oracle.fused_add_rms_norm(x[sel], r[sel], w, 1e-6)
         assert_exact(rd[sel], r_ref, f"residual rows {b0}+")
         assert_exact(xd[sel], x_ref, f"output rows {b0}+")
+
+
+def _per_block(x, w, r, qdt, G, ub, transposed):
+    """One vLLM rms_norm_per_block_quant call on the GPU; returns (codes, scales, residual)."""
+    T, H = x.shape
+    q = torch.empty(T, H, dtype=qdt, device=DEV)
+    s = torch.empty((H // G, T) if transposed else (T, H // G), device=DEV)
+    rd = None if r is None else r.to(DEV)
+    ubd = None if ub is None else torch.tensor([ub], device=DEV)
+    torch.ops._C.rms_norm_per_block_quant(q, x.to(DEV), w.to(DEV), s, 1e-6, ubd, rd, G,
+                                          transposed)
+    torch.cuda.synchronize()
+    return q.cpu(), s.cpu(), None if rd is None else rd.cpu()
+
+
+@pytest.mark.parametrize("dtype,H", [(torch.bfloat16, 65664), (torch.bfloat16, 131072),
+                                     (torch.float16, 65792), (torch.float32, 32896),
+                                     (torch.float32, 65536)])
+@pytest.mark.parametrize("qdt", [torch.int8, torch.float8_e4m3fn])
+def test_split_per_block_against_oracle_and_multipass(dtype, H, qdt):
+    """Slices hold whole groups (64 or 128 elements): every scale and code against the oracle,
+    and the split and multi-pass kernels bit for bit, row-major and transposed scales."""
+    say(f"split per-block {dtype} H={H} {qdt}")
+    T = 3
+    x, r = _x(T, H, 108, dtype, 0.01), _x(T, H, 109, dtype)
+    w = _w(H, 110, dtype)
+    for G in (64, 128):
+        for res, transposed, ub in ((None, False, None), (r, True, None), (r, False, 0.02)):
+            if ub is not None and qdt == torch.int8:
+                continue
+            tag = f"G={G} res={res is not None} tr={transposed} ub={ub}"
+            q_ref, s_ref, r_ref = oracle.rms_norm_per_block_quant(x, w, 1e-6, qdt, G, ub, res,
+                                                                  transposed)
+            got = _per_block(x, w, res, qdt, G, ub, transposed)
+            assert_scales(got[1], s_ref, tag + " scales")
+            assert_codes(got[0], q_ref, tag + " codes")
+            if res is not None:
+                assert_exact(got[2], r_ref, tag + " residual")
+            _lib.set_split_rows(False)
+            try:
+                mp = _per_block(x, w, res, qdt, G, ub, transposed)
+            finally:
+                _lib.set_split_rows(True)
+            for a, b, what in zip(got, mp, ("codes", "scales", "residual")):
+                _same(a, b, f"{tag} {what}: split-row and multi-pass kernels differ")
+
+
+def test_split_per_block_wide_block_workload_rows():
+    """The bench's wide-block workload, 2048 x 131072 bf16 to fp8 with G = 128 and a residual:
+    blocks of rows at the start, the middle and the end against the oracle."""
+    T, H, G = 2048, 131072, 128
+    say(f"split: the wide-block workload {T}x{H}")
+    x, r, w = _x(T, H, 111, torch.bfloat16), _x(T, H, 112, torch.bfloat16), _w(H, 113,
+                                                                                torch.bfloat16)
+    q = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=DEV)
+    s = torch.empty(T, H // G, device=DEV)
+    rd = r.to(DEV)
+    torch.ops._C.rms_norm_per_block_quant(q, x.to(DEV), w.to(DEV), s, 1e-6, None, rd, G, False)
+    torch.cuda.synchronize()
+    for b0 in (0, 1000, 1984):
+        sel = slice(b0, b0 + 64)
+        q_ref, s_ref, r_ref = oracle.rms_norm_per_block_quant(x[sel], w, 1e-6,
+                                                              torch.float8_e4m3fn, G, None,
+                                                              r[sel])
+        assert_exact(rd[sel], r_ref, f"residual rows {b0}+")
+        assert_scales(s[sel], s_ref, f"scales rows {b0}+")
+        assert_codes(q[sel], q_ref, f"codes rows {b0}+")
 
 
 @pytest.mark.parametrize("T", [1, 3, 250])
