@@ -28,6 +28,7 @@
 
 #include "../../include/mcop_norm.h"
 #include "rowkern.h"
+#include "split_row.h"
 
 namespace mcop {
 
@@ -216,6 +217,123 @@ k_rms_norm(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
       for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(n[e] * wv[v].at(e));
     }
     st_nt<S, VEC>(row_elem<EX>(out, out_base, (int64_t)j * VEC), o);
+  }
+}
+
+// Rows too wide for one workgroup's registers, read once (split_row.h): workgroup b takes slice
+// b % slices of row b / slices -- `slice_vecs` vectors, NV a lane -- and combines the row's sum
+// of squares with the other slices' through the workspace `ws` (split_sum, in slice order);
+// every other step is the register kernel's, element by element.  The launch covers rows
+// [row0, row0 + rows) of the row map.  The row index is uniform: scalar row bases, 32-bit offsets
+// within the row.
+template <class E, class EW, int VEC, int NV, bool RES>
+__global__ void __launch_bounds__(max_tpr(VEC, NV))
+k_rms_norm_split(typename E::S* __restrict__ out, typename E::S* __restrict__ ares,
+                 const typename E::S* __restrict__ x, const typename EW::S* __restrict__ w,
+                 const typename E::S* __restrict__ res, RowMap map, int64_t row0, int64_t rows,
+                 int hidden, float eps, int mode, int rms_div, int slices, int slice_vecs,
+                 uint64_t* __restrict__ ws, int64_t timeout_ticks) {
+  using S = typename E::S;
+  __shared__ double red_sum[16];
+  __shared__ double x_sum;
+  const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x;
+  const int lt = (int)threadIdx.x;
+  const int sl = (int)(blockIdx.x % (unsigned)slices);
+  const int64_t row = blockIdx.x / (unsigned)slices;
+  const int j0 = sl * slice_vecs;
+  const int jn = min(slice_vecs, nvec - j0);
+  const RowOffsets lo = row_offsets(map, row0 + row);
+  const int64_t rbase = (row0 + row) * (int64_t)hidden;
+  // Lanes past the slice end re-read the slice's first vector, which does not count.
+  auto in_of = [&](int v) { return vec_index(v, tpr, lt) < jn; };
+  auto lj_of = [&](int v) {
+    return (int64_t)(j0 + (in_of(v) ? vec_index(v, tpr, lt) : 0)) * VEC;
+  };
+  Pack<S, VEC> xv[NV], rv[NV];
+  NormW<EW, VEC> wv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    wv[v].p = ld<typename EW::S, VEC>(row_elem<true>(w, lo.w, lj_of(v)));
+  }
+  shared_loads_first();
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    xv[v] = ld_nt<S, VEC>(row_elem<true>(x, lo.in, lj_of(v)));
+    if constexpr (RES) rv[v] = ld_nt<S, VEC>(row_elem<true>(res, rbase, lj_of(v)));
+  }
+  // a, held in the dtype: x without a residual, b(x + r) with one (the element-wise chain's
+  // a~; the host sends the vectorized chain with a residual, whose a is unrounded, elsewhere)
+  double ss = 0.0;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    double vs = 0.0;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float t = E::to_f(xv[v].v[e]);
+      if constexpr (RES) {
+        t += E::to_f(rv[v].v[e]);
+        xv[v].v[e] = E::from_f(t);
+      }
+      const double d = (double)t;
+      vs = __builtin_fma(d, d, vs);
+    }
+    ss += in_of(v) ? vs : 0.0;
+    if constexpr (RES) {
+      if (in_of(v)) st_nt<S, VEC>(row_elem<true>(ares, rbase, lj_of(v)), xv[v]);
+    }
+  }
+  SplitRowReduce red{red_sum, nullptr, tpr, ws, row, slices, sl,
+                     ws + split_ws_words(rows, slices) - 1, timeout_ticks, &x_sum, nullptr};
+  ss = red.sum(ss);
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+  const float inv_rho = mcop_div_rn(1.0f, rho);
+  // the register kernel's choice of division form, per wave (both forms give the correctly
+  // rounded quotient)
+  constexpr bool kRoundOverflows = RES && sizeof(S) == 2 && !__is_same(E, BF16);
+  bool short_div = false;
+  if (mode != NORM_VLLM && mode != NORM_MC && rms_div) {
+    float amin = __builtin_inff();
+    float amx = 0.0f;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float t = __builtin_fabsf(E::to_f(xv[v].v[e]));
+        amin = __builtin_fminf(amin, t);
+        if constexpr (kRoundOverflows) amx = __builtin_fmaxf(amx, t);
+      }
+    }
+    const bool in_domain = div_domain_ok(amin, ss * (1.0 + 0x1p-6), inv_rho,
+                                         mcop_divisor_ok(rho)) &&
+                           (!kRoundOverflows || amx <= 0x1.fffffep127f);
+    short_div = __builtin_amdgcn_ballot_w64(!in_domain) == 0;
+  }
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    if (!in_of(v)) continue;
+    float av[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) av[e] = E::to_f(xv[v].v[e]);
+    Pack<S, VEC> o;
+    if (mode == NORM_VLLM) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(rnd<E>(av[e] * rho) * wv[v].at(e));
+    } else if (mode == NORM_MC || !rms_div) {
+      const float d = (mode == NORM_MC && rms_div) ? inv_rho : rho;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f((av[e] * d) * wv[v].at(e));
+    } else {
+      float n[VEC];
+      if (short_div) {
+        div_in_domain<VEC>(n, av, rho, inv_rho);
+      } else {
+        div_by_const<VEC>(n, av, rho, inv_rho, mcop_divisor_ok(rho));
+      }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o.v[e] = E::from_f(n[e] * wv[v].at(e));
+    }
+    st_nt<S, VEC>(row_elem<true>(out, lo.out, lj_of(v)), o);
   }
 }
 
@@ -408,6 +526,36 @@ static bool norm_vec_ok(const NormArgs& a) {
          aligned(WB, a.w);
 }
 
+// Rows too wide for the register kernels, vector path: the split-row kernel when it applies, its
+// workspace from the stream-ordered allocator; MCOP_E_UNSUPPORTED (no message) when it does not.
+template <class E, class EW, int VEC, bool RES>
+static int norm_launch_split(const char* name, const NormArgs& a, hipStream_t st) {
+  using S = typename E::S;
+  // the kernel holds a in the dtype, which the vectorized chain's unrounded x + r is not (that
+  // chain only runs on rows narrow enough for the register kernels)
+  if (RES && a.mode != NORM_MC_GENERIC) return MCOP_E_UNSUPPORTED;
+  auto fn = [](auto k) { return reinterpret_cast<const void*>(k); };
+  const SplitKernel k8{fn(&k_rms_norm_split<E, EW, VEC, 8, RES>), 8};
+  const SplitKernel k4{fn(&k_rms_norm_split<E, EW, VEC, 4, RES>), 4};
+  return split_run(name, {k8, k4}, a.rows, a.hidden / VEC, nullptr, st,
+                   [&](int64_t r0, int64_t n, uint64_t* ws, const SplitPlan& p, auto launch) {
+    S* o = static_cast<S*>(a.out);
+    S* arp = static_cast<S*>(a.ares);
+    const S* xp = static_cast<const S*>(a.x);
+    const typename EW::S* wp = static_cast<const typename EW::S*>(a.w);
+    const S* rp = static_cast<const S*>(a.res);
+    RowMap m = a.map;
+    int64_t row0 = r0;
+    int h = a.hidden, mode = a.mode, rms_div = a.rms_div, slices = p.slices,
+        slice_vecs = p.slice_vecs;
+    float e = a.eps;
+    int64_t timeout = p.timeout_ticks;
+    void* args[] = {&o, &arp, &xp, &wp, &rp, &m, &row0, &n, &h, &e, &mode, &rms_div, &slices,
+                    &slice_vecs, &ws, &timeout};
+    return launch(args);
+  });
+}
+
 template <class E, class EW>
 static int norm_dispatch(const char* name, const NormArgs& a, hipStream_t st) {
   constexpr int V = E::VEC;
@@ -417,6 +565,11 @@ static int norm_dispatch(const char* name, const NormArgs& a, hipStream_t st) {
       vec_ok ? (r ? &norm_kernel_of<E, EW, V, true> : &norm_kernel_of<E, EW, V, false>)
              : (r ? &norm_kernel_of<E, EW, 1, true> : &norm_kernel_of<E, EW, 1, false>);
   if (!row_fits(a.hidden, vec_ok ? V : 1, kernels)) {
+    if (vec_ok && split_rows_enabled()) {
+      const int rc = r ? norm_launch_split<E, EW, V, true>(name, a, st)
+                       : norm_launch_split<E, EW, V, false>(name, a, st);
+      if (rc != MCOP_E_UNSUPPORTED) return rc;
+    }
     if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
     using S = typename E::S;
     auto* o = static_cast<S*>(a.out);

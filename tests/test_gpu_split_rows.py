@@ -1,8 +1,9 @@
-"""Rows too wide for one workgroup's registers on the split-row kernels (H1 / H2 / H3 / H4 / H5
-and the per-block quant: each row shared by several workgroups that exchange partial sums
-through a device workspace): bit for bit against the oracle and against the multi-pass kernels
-(forced with the library's test hook), over several row counts and a call that takes several
-launches, two streams at once, and a HIP graph capture (which takes the multi-pass kernel)."""
+"""Rows too wide for one workgroup's registers on the split-row kernels (H1 / H2 / H3 / H4 / H5,
+the per-block quant and the norms: each row shared by several workgroups that exchange partial
+sums through a device workspace): bit for bit against the oracle and against the multi-pass
+kernels (forced with the library's test hook), over several row counts and calls that take
+several launches, two streams at once, and a HIP graph capture (which takes the multi-pass
+kernel)."""
 
 import os
 import re
@@ -310,6 +311,80 @@ def test_split_per_block_wide_block_workload_rows():
         assert_exact(rd[sel], r_ref, f"residual rows {b0}+")
         assert_scales(s[sel], s_ref, f"scales rows {b0}+")
         assert_codes(q[sel], q_ref, f"codes rows {b0}+")
+
+
+def _mc_norm(x, w, r, rms_div):
+    out = torch.empty(x.shape, dtype=x.dtype, device=DEV)
+    ares = None if r is None else torch.empty(x.shape, dtype=x.dtype, device=DEV)
+    op.rms_norm(out, x.to(DEV), w.to(DEV), 1e-6, ares, None if r is None else r.to(DEV),
+                rms_div)
+    torch.cuda.synchronize()
+    return out.cpu(), None if ares is None else ares.cpu()
+
+
+@pytest.mark.parametrize("dtype,wdtype,H", [(torch.bfloat16, torch.bfloat16, 65544),
+                                            (torch.bfloat16, torch.float32, 131072),
+                                            (torch.float16, torch.float16, 65608),
+                                            (torch.float32, torch.float32, 32772)])
+def test_split_norms_against_oracle_and_multipass(dtype, wdtype, H):
+    """mcoplib rms_norm (its element-wise chain at these widths, both rms_div forms, with and
+    without a residual), vLLM rms_norm on a strided 3-D view and head_rms_norm: against the
+    oracle and, bit for bit, against the multi-pass kernel."""
+    say(f"split norms {dtype} w={wdtype} H={H}")
+    x, r, w = _x(3, H, 114, dtype), _x(3, H, 115, dtype), _w(H, 116, wdtype)
+    for res in (None, r):
+        for rms_div in (True, False):
+            tag = f"res={res is not None} rms_div={rms_div}"
+            out_ref, ares_ref = oracle.rms_norm(x, w, 1e-6, residual=res, rms_div=rms_div)
+            got = _mc_norm(x, w, res, rms_div)
+            assert_exact(got[0], out_ref, tag + " out")
+            if res is not None:
+                assert_exact(got[1], ares_ref, tag + " after_res")
+            _lib.set_split_rows(False)
+            try:
+                mp = _mc_norm(x, w, res, rms_div)
+            finally:
+                _lib.set_split_rows(True)
+            for a, b, what in zip(got, mp, ("out", "after_res")):
+                _same(a, b, f"{tag} {what}: split-row and multi-pass kernels differ")
+    if dtype != torch.float16 and wdtype == dtype:
+        big = torch.randn(2, 3, H + 16, generator=gen(117)).to(dtype)
+        ref = oracle.vllm_rms_norm(big[:, :, :H].contiguous().view(6, H), w, 1e-6)
+        o = torch.empty(2, 3, H, dtype=dtype, device=DEV)
+        torch.ops._C.rms_norm(o, big.to(DEV)[:, :, :H], w.to(DEV), 1e-6)
+        torch.cuda.synchronize()
+        assert_exact(o.view(6, H), ref, "vLLM rms_norm 3-D strided")
+    if dtype == torch.bfloat16 and wdtype == dtype:
+        T, NH = 2, 3
+        hs = torch.randn(T, NH, H, generator=gen(118)).to(dtype)
+        hw = _w(NH * H, 119, dtype).view(NH, H)
+        base = torch.zeros_like(hs)
+        ref = oracle.head_rms_norm(base, hs, hw, 1e-6, 1, 2)
+        out = base.to(DEV)
+        op.head_rms_norm(out, hs.to(DEV), hw.to(DEV), 1e-6, 1, 2)
+        torch.cuda.synchronize()
+        assert_exact(out, ref, "head_rms_norm")
+
+
+def test_split_norm_strided_rows_over_several_launches():
+    """vLLM rms_norm over a strided 3-D view with more rows than one launch's workspace holds
+    (8400 rows of 131072 bf16: 4095 rows a launch at 16 slices, 8191 at 8): rows on both sides
+    of every launch boundary against the oracle, generated on the GPU."""
+    A, B, H = 2, 4200, 131072
+    say(f"split: vLLM rms_norm [{A}, {B}, {H}] strided (several launches)")
+    g = torch.Generator(device=DEV).manual_seed(120)
+    big = torch.randn(A, B, H + 16, device=DEV, generator=g).to(torch.bfloat16)
+    w = _w(H, 121, torch.bfloat16)
+    o = torch.empty(A, B, H, dtype=torch.bfloat16, device=DEV)
+    torch.ops._C.rms_norm(o, big[:, :, :H], w.to(DEV), 1e-6)
+    torch.cuda.synchronize()
+    xs = big[:, :, :H].reshape(A * B, H)
+    os_ = o.view(A * B, H)
+    for r0 in (0, 4090, 8186, A * B - 6):
+        sel = slice(r0, r0 + 6)
+        ref = oracle.vllm_rms_norm(xs[sel].cpu(), w, 1e-6)
+        assert_exact(os_[sel], ref, f"rows {r0}+")
+    del big, o
 
 
 @pytest.mark.parametrize("T", [1, 3, 250])
