@@ -11,11 +11,14 @@
 //   fp8 e4m3fn       op/vllm/quantization/fp8/common.cu:142-180
 //     A = max|v| (min with *scale_ub); s = max(A / 448, 1/(448*512)); q = e4m3fn(clamp(v / s))
 // The row is loaded once into VGPRs; one max reduction (two for the zero point form).  Rows too
-// wide for the registers take k_per_token_quant_wide (two passes, the row's head held on chip).
+// wide for the registers take k_per_token_quant_split (the row split over several workgroups,
+// read once) or, under graph capture, on the scalar path and past 64 slices,
+// k_per_token_quant_wide (two passes, the row's head held on chip).
 #include <hip/hip_runtime.h>
 
 #include "../../include/mcop_norm.h"
 #include "rowkern.h"
+#include "split_row.h"
 
 namespace mcop {
 
@@ -161,6 +164,71 @@ k_per_token_quant(uint8_t* __restrict__ out, float* __restrict__ scales, int32_t
   }
 }
 
+// Rows too wide for one workgroup's registers, read once (split_row.h): workgroup b takes slice
+// b % slices of row b / slices -- `slice_vecs` vectors, NV a lane, held in the input dtype --
+// and combines the row's max (and, with the zero point, the max of -v) with the other slices'
+// through the workspace `ws` in one exchange; every other step is the register kernel's.  The
+// row index is uniform: scalar row bases, 32-bit offsets within the row.
+template <class E, int VEC, int NV, int MODE>
+__global__ void __launch_bounds__(max_tpr(VEC, NV))
+k_per_token_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
+                        int32_t* __restrict__ azp, const typename E::S* __restrict__ x,
+                        const float* __restrict__ scale_ub, int64_t rows, int hidden,
+                        int64_t in_stride, int64_t out_stride, int slices, int slice_vecs,
+                        uint64_t* __restrict__ ws, int64_t timeout_ticks) {
+  using S = typename E::S;
+  __shared__ float red_a[16];
+  __shared__ float red_b[16];
+  __shared__ float x_max[2];
+  const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x;
+  const int lt = (int)threadIdx.x;
+  const int sl = (int)(blockIdx.x % (unsigned)slices);
+  const int64_t row = blockIdx.x / (unsigned)slices;
+  const int j0 = sl * slice_vecs;
+  const int jn = min(slice_vecs, nvec - j0);
+  // Lanes past the slice end re-read the slice's first vector (no effect on max or min).
+  auto in_of = [&](int v) { return vec_index(v, tpr, lt) < jn; };
+  auto lj_of = [&](int v) {
+    return (int64_t)(j0 + (in_of(v) ? vec_index(v, tpr, lt) : 0)) * VEC;
+  };
+  Pack<S, VEC> xv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) xv[v] = ld_nt<S, VEC>(row_elem<true>(x, row * in_stride, lj_of(v)));
+  float mx = MODE == PTQ_INT8_AZP ? -__builtin_inff() : 0.0f;
+  float nmn = -__builtin_inff();
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) ptq_fold<MODE>(E::to_f(xv[v].v[e]), mx, nmn);
+  }
+  uint64_t* err = ws + split_ws_words(rows, slices) - 1;
+  if constexpr (MODE == PTQ_INT8_AZP) {
+    mx = row_reduce<true>(mx, red_a, tpr, MaxOp());
+    nmn = row_reduce<true>(nmn, red_b, tpr, MaxOp());
+    split_max2(split_slots(ws, row, slices, 0), slices, sl, kSplitTag, &mx, &nmn, err,
+               timeout_ticks, x_max);
+  } else {
+    SplitRowReduce red{nullptr, red_a, tpr, ws, row, slices, sl, err, timeout_ticks, nullptr,
+                       x_max};
+    mx = red.max(mx);
+  }
+  const PtqRow r = ptq_row<MODE>(mx, nmn, scale_ub);
+  if (sl == 0 && lt == 0) {
+    scales[row] = r.s;
+    if constexpr (MODE == PTQ_INT8_AZP) azp[row] = r.zp;
+  }
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    if (!in_of(v)) continue;
+    float a[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) a[e] = E::to_f(xv[v].v[e]);
+    st_nt<uint8_t, VEC>(row_elem<true>(out, row * out_stride, lj_of(v)),
+                        ptq_codes<E, VEC, MODE>(a, r));
+  }
+}
+
 // Rows too wide for the registers: one 1024-lane workgroup per row, two passes (max / min;
 // codes).  The row's head stays on chip between the passes -- the first NC vectors of every
 // lane in registers, the next NL in lane-private LDS slots (vector c of lane t at [c][t], so no
@@ -295,6 +363,31 @@ static void launch_nv(const Geometry& g, const PtqArgs& a, hipStream_t st) {
 #undef MCOP_LAUNCH
 }
 
+// Rows too wide for the register kernels, vector path: the split-row kernel when it applies, its
+// workspace from the stream-ordered allocator; MCOP_E_UNSUPPORTED (no message) when it does not.
+template <class E, int VEC, int MODE>
+static int launch_split(const char* name, const PtqArgs& a, hipStream_t st) {
+  using S = typename E::S;
+  auto fn = [](auto k) { return reinterpret_cast<const void*>(k); };
+  // (a sixteen-vector candidate, chosen by residency at three waves per SIMD, ran slower: 134.3
+  // against 129.2 us for int8 and 154.8 against 133.8 us for fp8 at 2048 x 131072 bf16)
+  const SplitKernel k8{fn(&k_per_token_quant_split<E, VEC, 8, MODE>), 8};
+  const SplitKernel k4{fn(&k_per_token_quant_split<E, VEC, 4, MODE>), 4};
+  return split_run(name, {k8, k4}, a.rows, a.hidden / VEC, nullptr, st,
+                   [&](int64_t r0, int64_t n, uint64_t* ws, const SplitPlan& p, auto launch) {
+    uint8_t* o = static_cast<uint8_t*>(a.out) + r0 * a.out_stride;
+    float* sc = a.scales + r0;
+    int32_t* zp = a.azp == nullptr ? nullptr : a.azp + r0;
+    const S* xp = static_cast<const S*>(a.x) + r0 * a.in_stride;
+    const float* ub = a.scale_ub;
+    int h = a.hidden, slices = p.slices, slice_vecs = p.slice_vecs;
+    int64_t is = a.in_stride, os = a.out_stride, timeout = p.timeout_ticks;
+    void* args[] = {&o, &sc, &zp, &xp, &ub, &n, &h, &is, &os, &slices, &slice_vecs, &ws,
+                    &timeout};
+    return launch(args);
+  });
+}
+
 template <class E, int MODE>
 static int dispatch(const char* name, const PtqArgs& a, hipStream_t st) {
   constexpr int V = E::VEC;
@@ -302,6 +395,10 @@ static int dispatch(const char* name, const PtqArgs& a, hipStream_t st) {
                       aligned(16, a.x) && aligned(V, a.out);
   const KernelOfNv kernels = vec_ok ? &kernel_of<E, V, MODE> : &kernel_of<E, 1, MODE>;
   if (!row_fits(a.hidden, vec_ok ? V : 1, kernels)) {
+    if (vec_ok && split_rows_enabled()) {
+      const int rc = launch_split<E, V, MODE>(name, a, st);
+      if (rc != MCOP_E_UNSUPPORTED) return rc;
+    }
     if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
     using S = typename E::S;
     auto* o = static_cast<uint8_t*>(a.out);

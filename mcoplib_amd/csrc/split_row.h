@@ -135,6 +135,33 @@ __device__ __forceinline__ float split_max(uint64_t* slots, int slices, int sl, 
   return *lds;
 }
 
+// The group's largest of the slices' pairs of fp32 maxima (a, b), in one exchange: phase-0 slots,
+// one word each.  lds holds two floats.
+__device__ __forceinline__ void split_max2(uint64_t* slots, int slices, int sl, uint32_t tag,
+                                           float* a, float* b, uint64_t* err,
+                                           int64_t timeout_ticks, float* lds) {
+  if (threadIdx.x == 0) {
+    ws_put(slots + sl * 2, tag, __builtin_bit_cast(uint32_t, *a));
+    ws_put(slots + sl * 2 + 1, tag, __builtin_bit_cast(uint32_t, *b));
+  }
+  if (threadIdx.x < 64) {
+    uint64_t w0 = 0, w1 = 0;
+    split_wait(slots, slices, 2, tag, err, timeout_ticks, &w0, &w1);
+    const bool mine = (int)(threadIdx.x & 63) < slices;
+    float ma = mine ? __builtin_bit_cast(float, (uint32_t)w0) : -__builtin_inff();
+    float mb = mine ? __builtin_bit_cast(float, (uint32_t)w1) : -__builtin_inff();
+    ma = wave_reduce(ma, MaxOp());
+    mb = wave_reduce(mb, MaxOp());
+    if (threadIdx.x == 0) {
+      lds[0] = ma;
+      lds[1] = mb;
+    }
+  }
+  __syncthreads();
+  *a = lds[0];
+  *b = lds[1];
+}
+
 // The row reductions of a split-row kernel: the workgroup's waves through LDS (row_reduce),
 // then the row's workgroups through the workspace (split_sum, split_max).
 struct SplitRowReduce {

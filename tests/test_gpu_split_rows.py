@@ -1,9 +1,9 @@
 """Rows too wide for one workgroup's registers on the split-row kernels (H1 / H2 / H3 / H4 / H5,
-the per-block quant and the norms: each row shared by several workgroups that exchange partial
-sums through a device workspace): bit for bit against the oracle and against the multi-pass
-kernels (forced with the library's test hook), over several row counts and calls that take
-several launches, two streams at once, and a HIP graph capture (which takes the multi-pass
-kernel)."""
+the per-block quant, the norms and the quantizers: each row shared by several workgroups that
+exchange partial results through a device workspace): bit for bit against the oracle and against
+the multi-pass kernels (forced with the library's test hook), over several row counts and calls
+that take several launches, two streams at once, and a HIP graph capture (which takes the
+multi-pass kernel)."""
 
 import os
 import re
@@ -385,6 +385,85 @@ def test_split_norm_strided_rows_over_several_launches():
         ref = oracle.vllm_rms_norm(xs[sel].cpu(), w, 1e-6)
         assert_exact(os_[sel], ref, f"rows {r0}+")
     del big, o
+
+
+def _ptq_int8(x, use_azp):
+    T = x.shape[0]
+    q = torch.empty(x.shape, dtype=torch.int8, device=DEV)
+    s = torch.empty((T, 1), device=DEV)
+    zp = torch.empty((T, 1), dtype=torch.int32, device=DEV) if use_azp else None
+    torch.ops._C.dynamic_scaled_int8_quant(q, x.to(DEV), s, zp)
+    torch.cuda.synchronize()
+    return q.cpu(), s.cpu(), None if zp is None else zp.cpu()
+
+
+def _ptq_fp8(xd, ub):
+    T = xd.shape[0]
+    q = torch.empty(xd.shape, dtype=torch.float8_e4m3fn, device=DEV)
+    s = torch.empty((T, 1), device=DEV)
+    ubd = None if ub is None else torch.tensor([ub], device=DEV)
+    torch.ops._C.dynamic_per_token_scaled_fp8_quant(q, xd, s, ubd)
+    torch.cuda.synchronize()
+    return q.cpu(), s.cpu()
+
+
+def _mp(fn, *args):
+    _lib.set_split_rows(False)
+    try:
+        return fn(*args)
+    finally:
+        _lib.set_split_rows(True)
+
+
+@pytest.mark.parametrize("dtype,H", [(torch.bfloat16, 65544), (torch.bfloat16, 262144),
+                                     (torch.float16, 65608), (torch.float32, 32772),
+                                     (torch.float32, 131072)])
+def test_split_quantizers_against_oracle_and_multipass(dtype, H):
+    """int8 symmetric, int8 with zero points (the max and the min in one exchange) and fp8 (with
+    and without scale_ub, rows strided on the input side): against the oracle and, bit for bit,
+    against the multi-pass kernels."""
+    say(f"split quantizers {dtype} H={H}")
+    T = 4
+    x = _x(T, H, 122, dtype, 2.0)
+    x[1] += 3.0  # an all-positive-leaning row: the zero point moves
+    for use_azp in (False, True):
+        tag = f"int8 azp={use_azp}"
+        q_ref, s_ref, zp_ref = oracle.dynamic_scaled_int8_quant(x, use_azp=use_azp)
+        got = _ptq_int8(x, use_azp)
+        assert_scales(got[1], s_ref, tag + " scales")
+        assert_codes(got[0], q_ref, tag + " codes")
+        if use_azp:
+            assert_exact(got[2], zp_ref, tag + " azp")
+        for a, b, what in zip(got, _mp(_ptq_int8, x, use_azp), ("codes", "scales", "azp")):
+            _same(a, b, f"{tag} {what}: split-row and multi-pass kernels differ")
+    big = torch.randn(T, H + 64, generator=gen(123)).to(dtype)
+    xs = big.to(DEV)[:, :H]  # rows strided on the input side
+    for ub in (None, 0.05):
+        tag = f"fp8 ub={ub}"
+        q_ref, s_ref = oracle.dynamic_per_token_scaled_fp8_quant(big[:, :H].contiguous(),
+                                                                 scale_ub=ub)
+        got = _ptq_fp8(xs, ub)
+        assert_scales(got[1], s_ref, tag + " scales")
+        assert_codes(got[0], q_ref, tag + " codes")
+        for a, b, what in zip(got, _mp(_ptq_fp8, xs, ub), ("codes", "scales")):
+            _same(a, b, f"{tag} {what}: split-row and multi-pass kernels differ")
+
+
+def test_split_quantizer_wide_ptq_workload_rows():
+    """The bench's wide-ptq workload, 2048 x 131072 bf16 to int8: blocks of rows at the start,
+    the middle and the end against the oracle."""
+    T, H = 2048, 131072
+    say(f"split: the wide-ptq workload {T}x{H}")
+    x = _x(T, H, 124, torch.bfloat16)
+    q = torch.empty(T, H, dtype=torch.int8, device=DEV)
+    s = torch.empty((T, 1), device=DEV)
+    torch.ops._C.dynamic_scaled_int8_quant(q, x.to(DEV), s, None)
+    torch.cuda.synchronize()
+    for b0 in (0, 1000, 1984):
+        sel = slice(b0, b0 + 64)
+        q_ref, s_ref, _ = oracle.dynamic_scaled_int8_quant(x[sel])
+        assert_scales(s[sel], s_ref, f"scales rows {b0}+")
+        assert_codes(q[sel], q_ref, f"codes rows {b0}+")
 
 
 @pytest.mark.parametrize("T", [1, 3, 250])
