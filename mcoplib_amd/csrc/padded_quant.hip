@@ -24,6 +24,7 @@
 
 #include "../../include/mcop_norm.h"
 #include "rowkern.h"
+#include "split_row.h"
 
 namespace mcop {
 
@@ -136,6 +137,103 @@ k_add_rms_norm_quant_padded(uint8_t* __restrict__ padded, uint16_t* __restrict__
       st_nt<uint8_t, VEC>(row_elem<EX>(q_out, base, (int64_t)j * VEC), q);
       st_nt<uint8_t, VEC>(row_elem<EX>(padded, pbase, (int64_t)j * VEC), q);
     }
+  }
+}
+
+// Rows too wide for one workgroup's registers (the generic chain: 7168-wide rows always fit),
+// read once (split_row.h): workgroup b takes slice b % slices of row b / slices --
+// `slice_vecs` vectors, NV a lane -- holds z = b(x + r) and the weight in bf16, and combines
+// the row's sum of squares and absmax (which does not need rho) with the other slices' in one
+// exchange (split_sum_max); every other step is the register kernel's.  Slice 0 stores the
+// scale.  The row index is uniform: scalar row bases, 32-bit offsets within the row.
+template <int NV>
+__global__ void __launch_bounds__(max_tpr(8, NV))
+k_add_rms_norm_quant_padded_split(uint8_t* __restrict__ padded, uint16_t* __restrict__ rms,
+                                  uint8_t* __restrict__ q_out, float* __restrict__ scales,
+                                  const uint16_t* __restrict__ x, uint16_t* __restrict__ res,
+                                  const uint16_t* __restrict__ w, int64_t rows, int hidden,
+                                  int64_t pad_bytes, float eps, int slices, int slice_vecs,
+                                  uint64_t* __restrict__ ws, int64_t timeout_ticks) {
+  using E = BF16;
+  constexpr int VEC = 8;
+  __shared__ double red_sum[16];
+  __shared__ float red_max[16];
+  __shared__ double x_sum;
+  __shared__ float x_max;
+  const int nvec = hidden / VEC;
+  const int tpr = (int)blockDim.x;
+  const int lt = (int)threadIdx.x;
+  const int sl = (int)(blockIdx.x % (unsigned)slices);
+  const int64_t row = blockIdx.x / (unsigned)slices;
+  const int j0 = sl * slice_vecs;
+  const int jn = min(slice_vecs, nvec - j0);
+  const int64_t base = row * (int64_t)hidden;
+  const int64_t pbase = row * pad_bytes;
+  // Lanes past the slice end re-read the slice's first vector, which does not count.
+  auto in_of = [&](int v) { return vec_index(v, tpr, lt) < jn; };
+  auto lj_of = [&](int v) {
+    return (int64_t)(j0 + (in_of(v) ? vec_index(v, tpr, lt) : 0)) * VEC;
+  };
+  Pack<uint16_t, VEC> xv[NV], rv[NV], wv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) wv[v] = ld<uint16_t, VEC>(row_elem<true>(w, 0, lj_of(v)));
+  shared_loads_first();
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    xv[v] = ld_nt<uint16_t, VEC>(row_elem<true>(x, base, lj_of(v)));
+    rv[v] = ld_nt<uint16_t, VEC>(row_elem<true>(res, base, lj_of(v)));
+  }
+  double ss = 0.0;
+  float amax = 0.0f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    double vs = 0.0;
+    float vm = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float t = E::to_f(xv[v].v[e]) + E::to_f(rv[v].v[e]);
+      const double d = (double)t;
+      vs = __builtin_fma(d, d, vs);
+      xv[v].v[e] = E::from_f(t);  // z = b(a), the residual value the generic chain re-reads
+      vm = __builtin_fmaxf(vm, __builtin_fabsf(rnd<E>(E::to_f(xv[v].v[e]) *
+                                                      E::to_f(wv[v].v[e]))));
+    }
+    ss += in_of(v) ? vs : 0.0;
+    amax = __builtin_fmaxf(amax, in_of(v) ? vm : 0.0f);
+    if (in_of(v)) st_nt<uint16_t, VEC>(row_elem<true>(res, base, lj_of(v)), xv[v]);
+  }
+  ss = row_reduce<true>(ss, red_sum, tpr, SumOp());
+  amax = row_reduce<true>(amax, red_max, tpr, MaxOp());
+  split_sum_max(ws, row, slices, sl, kSplitTag, &ss, &amax, ws + split_ws_words(rows, slices) - 1,
+                timeout_ticks, &x_sum, &x_max);
+  const float rho = mcop_inv_rms(ss, hidden, eps);
+  const float s = __builtin_fmaxf(mcop_div_rn(amax * rho, 127.0f), FLT_EPSILON);
+  const float inv = mcop_div_rn(1.0f, s);
+  if (sl == 0 && lt == 0) {
+    scales[row] = s;
+    uint8_t* sp = padded + pbase + hidden;
+    if ((reinterpret_cast<uintptr_t>(sp) & 3) == 0) {
+      *reinterpret_cast<float*>(sp) = s;
+    } else {
+      const uint32_t b = __builtin_bit_cast(uint32_t, s);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sp[k] = (uint8_t)(b >> (8 * k));
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    if (!in_of(v)) continue;
+    Pack<uint16_t, VEC> o;
+    Pack<uint8_t, VEC> q;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      o.v[e] = E::from_f(rnd<E>(E::to_f(xv[v].v[e]) * rho) * E::to_f(wv[v].v[e]));
+      q.v[e] = q_i8<-127>(E::to_f(o.v[e]) * inv);
+    }
+    const int64_t lj = lj_of(v);
+    st_nt<uint16_t, VEC>(row_elem<true>(rms, base, lj), o);
+    st_nt<uint8_t, VEC>(row_elem<true>(q_out, base, lj), q);
+    st_nt<uint8_t, VEC>(row_elem<true>(padded, pbase, lj), q);
   }
 }
 
@@ -296,6 +394,31 @@ static void launch_nv(const Geometry& g, const PadArgs& a, hipStream_t st) {
 #undef MCOP_LAUNCH
 }
 
+// Rows too wide for the register kernels, vector path: the split-row kernel when it applies, its
+// workspace from the stream-ordered allocator; MCOP_E_UNSUPPORTED (no message) when it does not.
+static int launch_split(const char* name, const PadArgs& a, hipStream_t st) {
+  auto fn = [](auto k) { return reinterpret_cast<const void*>(k); };
+  const SplitKernel k8{fn(&k_add_rms_norm_quant_padded_split<8>), 8};
+  const SplitKernel k4{fn(&k_add_rms_norm_quant_padded_split<4>), 4};
+  return split_run(name, {k8, k4}, a.rows, a.hidden / 8, nullptr, st,
+                   [&](int64_t r0, int64_t n, uint64_t* ws, const SplitPlan& p, auto launch) {
+    const int64_t off = r0 * (int64_t)a.hidden;
+    uint8_t* pd = a.padded + r0 * a.pad_bytes;
+    uint16_t* rm = a.rms + off;
+    uint8_t* q = a.q + off;
+    float* sc = a.scales + r0;
+    const uint16_t* xp = a.x + off;
+    uint16_t* rp = a.res + off;
+    const uint16_t* wp = a.w;
+    int h = a.hidden, slices = p.slices, slice_vecs = p.slice_vecs;
+    int64_t pb = a.pad_bytes, timeout = p.timeout_ticks;
+    float e = a.eps;
+    void* args[] = {&pd, &rm, &q, &sc, &xp, &rp, &wp, &n, &h, &pb, &e, &slices, &slice_vecs,
+                    &ws, &timeout};
+    return launch(args);
+  });
+}
+
 template <bool OPT>
 static int dispatch(const PadArgs& a, hipStream_t st) {
   const char* name = "fused_add_rms_norm_dynamic_per_token_quant_padding_output";
@@ -303,6 +426,10 @@ static int dispatch(const PadArgs& a, hipStream_t st) {
                       aligned(16, a.x, a.res, a.w, a.rms) && aligned(8, a.q, a.padded);
   if constexpr (!OPT) {
     if (!row_fits(a.hidden, vec_ok ? 8 : 1, vec_ok ? &kernel_of<8, OPT> : &kernel_of<1, OPT>)) {
+      if (vec_ok && split_rows_enabled()) {
+        const int rc = launch_split(name, a, st);
+        if (rc != MCOP_E_UNSUPPORTED) return rc;
+      }
       if (!wide_rows_ok(name, a.rows)) return MCOP_E_UNSUPPORTED;
       const dim3 grid((unsigned)a.rows), block(kWideLanes);
       if (vec_ok) {

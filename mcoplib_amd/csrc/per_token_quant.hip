@@ -194,7 +194,9 @@ k_per_token_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
   };
   Pack<S, VEC> xv[NV];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) xv[v] = ld_nt<S, VEC>(row_elem<true>(x, row * in_stride, lj_of(v)));
+  for (int v = 0; v < NV; ++v) {
+    xv[v] = ld_nt<S, VEC>(row_elem<true>(x, row * in_stride, lj_of(v)));
+  }
   float mx = MODE == PTQ_INT8_AZP ? -__builtin_inff() : 0.0f;
   float nmn = -__builtin_inff();
 #pragma unroll

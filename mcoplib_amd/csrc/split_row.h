@@ -135,6 +135,44 @@ __device__ __forceinline__ float split_max(uint64_t* slots, int slices, int sl, 
   return *lds;
 }
 
+// The group's fp64 sum (in slice order) and fp32 maximum of the slices' partials, in one round:
+// both are published before either wait (the sum in the phase-0 slots, the maximum in the
+// phase-1 slots).  lds holds one double and one float.
+__device__ __forceinline__ void split_sum_max(uint64_t* ws, int64_t row, int slices, int sl,
+                                              uint32_t tag, double* sum, float* mx,
+                                              uint64_t* err, int64_t timeout_ticks,
+                                              double* lds_sum, float* lds_max) {
+  uint64_t* s0 = split_slots(ws, row, slices, 0);
+  uint64_t* s1 = split_slots(ws, row, slices, 1);
+  if (threadIdx.x == 0) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, *sum);
+    ws_put(s0 + sl * 2, tag, (uint32_t)b);
+    ws_put(s0 + sl * 2 + 1, tag, (uint32_t)(b >> 32));
+    ws_put(s1 + sl * 2, tag, __builtin_bit_cast(uint32_t, *mx));
+  }
+  if (threadIdx.x < 64) {
+    uint64_t w0 = 0, w1 = 0, m0 = 0, m1 = 0;
+    split_wait(s0, slices, 2, tag, err, timeout_ticks, &w0, &w1);
+    split_wait(s1, slices, 1, tag, err, timeout_ticks, &m0, &m1);
+    const uint32_t lo = (uint32_t)w0, hi = (uint32_t)w1;
+    double total = 0.0;
+    for (int s = 0; s < slices; ++s) {
+      const uint64_t b = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)hi, s) << 32) |
+                         (uint32_t)__builtin_amdgcn_readlane((int)lo, s);
+      total += __builtin_bit_cast(double, b);
+    }
+    float m = (int)(threadIdx.x & 63) < slices ? __builtin_bit_cast(float, (uint32_t)m0) : 0.0f;
+    m = wave_reduce(m, MaxOp());
+    if (threadIdx.x == 0) {
+      *lds_sum = total;
+      *lds_max = m;
+    }
+  }
+  __syncthreads();
+  *sum = *lds_sum;
+  *mx = *lds_max;
+}
+
 // The group's largest of the slices' pairs of fp32 maxima (a, b), in one exchange: phase-0 slots,
 // one word each.  lds holds two floats.
 __device__ __forceinline__ void split_max2(uint64_t* slots, int slices, int sl, uint32_t tag,

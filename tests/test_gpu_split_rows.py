@@ -1,9 +1,9 @@
 """Rows too wide for one workgroup's registers on the split-row kernels (H1 / H2 / H3 / H4 / H5,
-the per-block quant, the norms and the quantizers: each row shared by several workgroups that
-exchange partial results through a device workspace): bit for bit against the oracle and against
-the multi-pass kernels (forced with the library's test hook), over several row counts and calls
-that take several launches, two streams at once, and a HIP graph capture (which takes the
-multi-pass kernel)."""
+the per-block quant, the norms, the quantizers and the padded op: each row shared by several
+workgroups that exchange partial results through a device workspace): bit for bit against the
+oracle and against the multi-pass kernels (forced with the library's test hook), over several
+row counts and calls that take several launches, two streams at once, and a HIP graph capture
+(which takes the multi-pass kernel)."""
 
 import os
 import re
@@ -464,6 +464,60 @@ def test_split_quantizer_wide_ptq_workload_rows():
         q_ref, s_ref, _ = oracle.dynamic_scaled_int8_quant(x[sel])
         assert_scales(s[sel], s_ref, f"scales rows {b0}+")
         assert_codes(q[sel], q_ref, f"codes rows {b0}+")
+
+
+def _padded(x, r, w, pad):
+    T, H = x.shape
+    p = torch.zeros(T, 2 * pad, dtype=torch.int8, device=DEV)
+    rms = torch.empty(x.shape, dtype=torch.bfloat16, device=DEV)
+    q = torch.empty(x.shape, dtype=torch.int8, device=DEV)
+    s = torch.empty(T, 1, device=DEV)
+    rd = r.to(DEV)
+    op.fused_add_rms_norm_dynamic_per_token_quant_padding_output(p, rms, q, s, x.to(DEV), rd,
+                                                                  w.to(DEV), pad, 1e-6)
+    torch.cuda.synchronize()
+    return p.cpu(), rd.cpu(), rms.cpu(), q.cpu(), s.cpu()
+
+
+@pytest.mark.parametrize("H,extra", [(65544, 0), (131072, 64), (163848, 8)])
+def test_split_padded_against_oracle_and_multipass(H, extra):
+    """The padded wire-format op (its generic chain): every padded row byte, the residual,
+    output_rms, codes and scales against the oracle and, bit for bit, against the multi-pass
+    kernel; `extra` spare bytes after each row's scale stay untouched."""
+    say(f"split padded H={H} extra={extra}")
+    T = 3
+    pad = (H + 4 + extra + 1) // 2
+    x, r, w = _x(T, H, 125, torch.bfloat16), _x(T, H, 126, torch.bfloat16), _w(H, 127,
+                                                                                 torch.bfloat16)
+    refs = oracle.add_rms_norm_quant_padded(x, r, w, pad, 1e-6)
+    got = _padded(x, r, w, pad)
+    assert torch.equal(got[0].view(torch.uint8), refs[0]), "padded rows"
+    assert_exact(got[1], refs[1], "residual")
+    assert_exact(got[2], refs[2], "output_rms")
+    assert_codes(got[3], refs[3], "codes")
+    assert_scales(got[4], refs[4], "scales")
+    for a, b, what in zip(got, _mp(_padded, x, r, w, pad),
+                          ("padded", "residual", "output_rms", "codes", "scales")):
+        _same(a, b, f"{what}: split-row and multi-pass kernels differ")
+
+
+def test_split_padded_wide_padded_workload_rows():
+    """The bench's wide-padded workload, 2048 x 131072: blocks of rows at the start, the middle
+    and the end against the oracle, padded bytes included."""
+    T, H = 2048, 131072
+    pad = (H + 4 + 1) // 2
+    say(f"split: the wide-padded workload {T}x{H}")
+    x, r, w = _x(T, H, 128, torch.bfloat16), _x(T, H, 129, torch.bfloat16), _w(H, 130,
+                                                                                 torch.bfloat16)
+    p, rd, rms, q, s = _padded(x, r, w, pad)
+    for b0 in (0, 1000, 1984):
+        sel = slice(b0, b0 + 64)
+        refs = oracle.add_rms_norm_quant_padded(x[sel], r[sel], w, pad, 1e-6)
+        assert torch.equal(p[sel].view(torch.uint8), refs[0]), f"padded rows {b0}+"
+        assert_exact(rd[sel], refs[1], f"residual rows {b0}+")
+        assert_exact(rms[sel], refs[2], f"output_rms rows {b0}+")
+        assert_codes(q[sel], refs[3], f"codes rows {b0}+")
+        assert_scales(s[sel], refs[4], f"scales rows {b0}+")
 
 
 @pytest.mark.parametrize("T", [1, 3, 250])
