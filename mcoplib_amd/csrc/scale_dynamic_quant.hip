@@ -8,11 +8,16 @@
 // One pass: the row is loaded once into VGPRs, one max reduction, codes from registers.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "../../include/mcop_norm.h"
 #include "rowkern.h"
 #include "split_row.h"
 
 namespace mcop {
+
+// Rows a split-row workgroup takes when the call has at least two.
+constexpr int kSdqSplitRows = 2;
 
 // R rows per lane (1, or 2 for many rows): the lane's smooth vectors, loaded once, serve R rows.
 // The smooth scales are fp32, two loads per 16-byte input vector; even as cache hits they took
@@ -83,25 +88,35 @@ k_scale_dynamic_quant(uint8_t* __restrict__ out, float* __restrict__ scales,
 }
 
 // Rows too wide for one workgroup's registers, read once (split_row.h): workgroup b takes slice
-// b % slices of row b / slices -- `slice_vecs` vectors, NV a lane -- and holds its products v in
-// registers; the slices' absmax values are combined through the workspace `ws` (split_max),
-// and every other step is the register kernel's, element by element.
-template <int VEC, int NV>
-__global__ void __launch_bounds__(max_tpr(VEC, NV))
+// b % slices of the R rows of group b / slices -- `slice_vecs` vectors of each, NV a lane -- and
+// holds their products v in registers; the slice's smooth vectors, loaded once, serve the R rows
+// (they are fp32, twice the bytes of x).  The slices' absmax values are combined through the
+// workspace `ws` in one exchange (split_max, or split_max2 for two rows); every other step is
+// the register kernel's, element by element.  `rows` rows of the launch form `groups` groups;
+// a group's row past the end computes on a copy of its first row and stores nothing.
+template <int VEC, int NV, int R>
+__global__ void __launch_bounds__(max_tpr(VEC, NV * R))
 k_scale_dynamic_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
                             const uint16_t* __restrict__ x, const float* __restrict__ sm,
-                            int64_t rows, int hidden, int slices, int slice_vecs,
+                            int64_t groups, int64_t rows, int hidden, int slices, int slice_vecs,
                             uint64_t* __restrict__ ws, int64_t timeout_ticks) {
-  __shared__ float red_max[16];
-  __shared__ float x_max;
+  static_assert(R == 1 || R == 2, "one or two rows a workgroup");
+  __shared__ float red_max[16 * R];
+  __shared__ float x_max[2];
   const int nvec = hidden / VEC;
   const int tpr = (int)blockDim.x;
   const int lt = (int)threadIdx.x;
   const int sl = (int)(blockIdx.x % (unsigned)slices);
-  const int64_t row = blockIdx.x / (unsigned)slices;
+  const int64_t g = blockIdx.x / (unsigned)slices;
   const int j0 = sl * slice_vecs;
   const int jn = min(slice_vecs, nvec - j0);
-  const int64_t base = row * (int64_t)hidden;
+  int64_t row[R];
+  bool live[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    live[k] = g * R + k < rows;
+    row[k] = live[k] ? g * R + k : g * R;
+  }
   // Lanes past the slice end re-read the slice's first vector, which leaves the absmax unchanged.
   auto in_of = [&](int v) { return vec_index(v, tpr, lt) < jn; };
   auto lj_of = [&](int v) {
@@ -111,32 +126,53 @@ k_scale_dynamic_quant_split(uint8_t* __restrict__ out, float* __restrict__ scale
 #pragma unroll
   for (int v = 0; v < NV; ++v) sv[v] = ld<float, VEC>(sm + lj_of(v));
   shared_loads_first();
-  Pack<uint16_t, VEC> xv[NV];
+  Pack<uint16_t, VEC> xv[R][NV];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) xv[v] = ld_nt<uint16_t, VEC>(x + base + lj_of(v));
-  float a[NV][VEC];
-  float amax = 0.0f;
+  for (int k = 0; k < R; ++k) {
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const float t = BF16::to_f(xv[v].v[e]) * sv[v].v[e];
-      a[v][e] = t;
-      amax = __builtin_fmaxf(amax, __builtin_fabsf(t));
+    for (int v = 0; v < NV; ++v) {
+      xv[k][v] = ld_nt<uint16_t, VEC>(x + row[k] * (int64_t)hidden + lj_of(v));
     }
   }
-  SplitRowReduce red{nullptr, red_max, tpr, ws, row, slices, sl,
-                     ws + split_ws_words(rows, slices) - 1, timeout_ticks, nullptr, &x_max};
-  amax = red.max(amax);
-  if (sl == 0 && lt == 0) scales[row] = amax * 0.00787401574803f;
-  const float inv = amax > 0.0f ? mcop_div_rn(127.0f, amax) : 0.0f;
+  float a[R][NV][VEC];
+  float amax[R];
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    if (in_of(v)) {
-      Pack<uint8_t, VEC> q;
+  for (int k = 0; k < R; ++k) {
+    amax[k] = 0.0f;
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(a[v][e] * inv);
-      st_nt<uint8_t, VEC>(out + base + lj_of(v), q);
+    for (int v = 0; v < NV; ++v) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float t = BF16::to_f(xv[k][v].v[e]) * sv[v].v[e];
+        a[k][v][e] = t;
+        amax[k] = __builtin_fmaxf(amax[k], __builtin_fabsf(t));
+      }
+    }
+  }
+  uint64_t* err = ws + split_ws_words(groups, slices) - 1;
+  if constexpr (R == 1) {
+    SplitRowReduce red{nullptr, red_max, tpr, ws, g, slices, sl, err, timeout_ticks, nullptr,
+                       x_max};
+    amax[0] = red.max(amax[0]);
+  } else {
+    amax[0] = row_reduce<true>(amax[0], red_max, tpr, MaxOp());
+    amax[1] = row_reduce<true>(amax[1], red_max + 16, tpr, MaxOp());
+    split_max2(split_slots(ws, g, slices, 0), slices, sl, kSplitTag, &amax[0], &amax[1], err,
+               timeout_ticks, x_max);
+  }
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    if (!live[k]) continue;
+    if (sl == 0 && lt == 0) scales[row[k]] = amax[k] * 0.00787401574803f;
+    const float inv = amax[k] > 0.0f ? mcop_div_rn(127.0f, amax[k]) : 0.0f;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      if (in_of(v)) {
+        Pack<uint8_t, VEC> q;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-128>(a[k][v][e] * inv);
+        st_nt<uint8_t, VEC>(out + row[k] * (int64_t)hidden + lj_of(v), q);
+      }
     }
   }
 }
@@ -282,22 +318,33 @@ static const void* kernel_of(int nv) {
 
 // Rows too wide for the register kernels, vector path: the split-row kernel when it applies, its
 // workspace from the stream-ordered allocator; MCOP_E_UNSUPPORTED (no message) when it does not.
+// With at least two rows a workgroup takes two rows at four vectors a lane, sharing the smooth
+// vectors; a single row takes eight vectors a lane (or four).
 static int launch_split(uint8_t* out, float* scales, const uint16_t* x, const float* sm,
                         int64_t rows, int hidden, hipStream_t st) {
   constexpr int V = BF16::VEC;
-  const SplitKernel k8{reinterpret_cast<const void*>(&k_scale_dynamic_quant_split<V, 8>), 8};
-  const SplitKernel k4{reinterpret_cast<const void*>(&k_scale_dynamic_quant_split<V, 4>), 4};
-  return split_run("scale_dynamic_quant", {k8, k4}, rows, hidden / V, nullptr, st,
-                   [&](int64_t r0, int64_t n, uint64_t* ws, const SplitPlan& p, auto launch) {
-    uint8_t* o = out + r0 * (int64_t)hidden;
-    float* sc = scales + r0;
-    const uint16_t* xp = x + r0 * (int64_t)hidden;
+  auto fn = [](auto k) { return reinterpret_cast<const void*>(k); };
+  const int R = rows >= 2 ? kSdqSplitRows : 1;
+  const SplitKernel k8{fn(&k_scale_dynamic_quant_split<V, 8, 1>), 8};
+  const SplitKernel k4{fn(&k_scale_dynamic_quant_split<V, 4, 1>), 4};
+  const SplitKernel k4r2{fn(&k_scale_dynamic_quant_split<V, 4, 2>), 4};
+  auto chunk = [&](int64_t r0, int64_t n, uint64_t* ws, const SplitPlan& p, auto launch) {
+    // r0, n count groups of R rows
+    const int64_t row0 = r0 * R;
+    int64_t nrows = std::min<int64_t>(n * R, rows - row0);
+    uint8_t* o = out + row0 * (int64_t)hidden;
+    float* sc = scales + row0;
+    const uint16_t* xp = x + row0 * (int64_t)hidden;
     const float* sp = sm;
     int h = hidden, slices = p.slices, slice_vecs = p.slice_vecs;
     int64_t timeout = p.timeout_ticks;
-    void* args[] = {&o, &sc, &xp, &sp, &n, &h, &slices, &slice_vecs, &ws, &timeout};
+    void* args[] = {&o, &sc, &xp, &sp, &n, &nrows, &h, &slices, &slice_vecs, &ws, &timeout};
     return launch(args);
-  });
+  };
+  const char* name = "scale_dynamic_quant";
+  const int64_t groups = (rows + R - 1) / R;
+  if (R == 2) return split_run(name, {k4r2}, groups, hidden / V, nullptr, st, chunk);
+  return split_run(name, {k8, k4}, groups, hidden / V, nullptr, st, chunk);
 }
 
 }  // namespace mcop
