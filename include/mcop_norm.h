@@ -12,11 +12,9 @@
  *   - Return value: MCOP_OK (0) or a negative MCOP_E_* code. The message of the last failure on
  *     the calling thread is returned by mcop_last_error(). No state is kept between calls
  *     (apart from the calling thread's test hooks, mcoplib_amd/csrc/mcop_testing.h) and calls
- *     are re-entrant. Nothing is allocated, with one exception: rows too wide for one
- *     workgroup's registers (more than 65536 bf16/fp16 or 32768 fp32 elements for most
- *     operators, fewer where a kernel would spill) in mcop_fused_add_rms_norm,
- *     mcop_rms_norm_dynamic_per_token_quant, mcop_rms_norm_dynamic_per_token_quant_custom,
- *     mcop_rms_norm_smooth_quant and mcop_scale_dynamic_quant run split over several
+ *     are re-entrant. Nothing is allocated, with one exception: on the 16-byte vector path,
+ *     rows too wide for one workgroup's registers (more than 65536 bf16/fp16 or 32768 fp32
+ *     elements for most operators, fewer where a kernel would spill) run split over several
  *     workgroups, which exchange per-row partial results through a device workspace of at most
  *     2 MiB taken from the stream-ordered allocator (hipMallocAsync and hipFreeAsync on
  *     `stream`); under graph capture those rows take a multi-pass kernel that needs none.
