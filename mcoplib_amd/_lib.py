@@ -49,11 +49,12 @@ def _load() -> ctypes.CDLL:
                                                                   F, P]
     lib.mcop_debug_set_launch_override.argtypes = [I, I]
     lib.mcop_debug_set_split_rows.argtypes = [I]
+    lib.mcop_debug_fail_split_waits.argtypes = [I]
     for fn in ("mcop_fused_add_rms_norm", "mcop_rms_norm_dynamic_per_token_quant",
                "mcop_rms_norm_dynamic_per_token_quant_noalloc",
                "mcop_rms_norm_smooth_quant", "mcop_scale_dynamic_quant",
                "mcop_fp8_e4m3fn_from_f32", "mcop_debug_set_launch_override",
-               "mcop_debug_set_split_rows", "mcop_abi_version",
+               "mcop_debug_set_split_rows", "mcop_debug_fail_split_waits", "mcop_abi_version",
                "mcop_dynamic_scaled_int8_quant", "mcop_dynamic_per_token_scaled_fp8_quant",
                "mcop_fused_add_rms_norm_dynamic_per_token_quant_padding_output",
                "mcop_rms_norm_per_block_quant", "mcop_rms_norm", "mcop_head_rms_norm",
@@ -102,3 +103,10 @@ def set_split_rows(enabled: bool = True) -> None:
     default) or always the multi-pass kernels, for later calls from this thread (a debug hook
     for tests and A/B timing). Results do not change."""
     check(lib.mcop_debug_set_split_rows(1 if enabled else 0))
+
+
+def fail_split_waits(on: bool = True) -> None:
+    """Make the split-row launches of later calls from this thread fail every exchange at once
+    (their error word set before the kernel starts; a test hook for the failure path: such rows
+    get NaN scales, or NaN outputs for the norms); False restores normal launches."""
+    check(lib.mcop_debug_fail_split_waits(1 if on else 0))

@@ -24,6 +24,9 @@ thread_local int g_over_nv = 0;
 thread_local int g_over_tpr = 0;
 // split-row kernels switched off for the calling thread (mcop_debug_set_split_rows)
 thread_local int g_no_split = 0;
+// split-row launches of the calling thread start with their error word set, so every exchange
+// fails at once (mcop_debug_fail_split_waits)
+thread_local int g_fail_split_waits = 0;
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t round64(int64_t a) { return ceil_div(a, 64) * 64; }
@@ -167,9 +170,10 @@ bool exact_form_ok(const void* ex_kernel) {
   return false;
 }
 
-__global__ void __launch_bounds__(256) k_fill_u64(uint64_t* __restrict__ p, int64_t n) {
+__global__ void __launch_bounds__(256) k_fill_u64(uint64_t* __restrict__ p, int64_t n,
+                                                   uint64_t last) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
+  if (i < n) p[i] = i == n - 1 ? last : 0;
 }
 
 namespace {
@@ -230,7 +234,9 @@ bool split_plan(const SplitKernel* cands, int ncand, int64_t rows, int64_t nvec,
   if (best == 0) return false;
   p->chunk_rows = std::min<int64_t>(rows, (kSplitWsWords - 1) / (4 * p->slices));
   p->ws_words = split_ws_words(p->chunk_rows, p->slices);
-  p->timeout_ticks = (int64_t)clk * 250;  // 250 ms of the wall clock
+  // 2 s of the wall clock: the dispatch order already guarantees progress (split_row.h), so the
+  // bound only ends waits stalled from outside (the queue preempted for that long)
+  p->timeout_ticks = (int64_t)clk * 2000;
   return true;
 }
 
@@ -238,7 +244,7 @@ int split_launch(const char* op, void** args, const SplitPlan& p, int64_t rows, 
                  bool static_ws, hipStream_t st) {
   const int64_t words = split_ws_words(rows, p.slices);
   hipLaunchKernelGGL(k_fill_u64, dim3((unsigned)ceil_div(words, 256)), dim3(256), 0, st, ws,
-                     words);
+                     words, (uint64_t)(g_fail_split_waits ? 1 : 0));
   if (int rc = check_launch(op)) return rc;
   const hipError_t e = hipLaunchKernel(p.kernel, dim3((unsigned)(rows * p.slices)),
                                        dim3((unsigned)p.lanes), args, 0, st);
@@ -378,6 +384,11 @@ int mcop_debug_set_launch_override(int vectors_per_lane, int lanes_per_row) {
 
 int mcop_debug_set_split_rows(int enabled) {
   mcop::g_no_split = enabled ? 0 : 1;
+  return MCOP_OK;
+}
+
+int mcop_debug_fail_split_waits(int on) {
+  mcop::g_fail_split_waits = on ? 1 : 0;
   return MCOP_OK;
 }
 

@@ -205,6 +205,7 @@ k_rms_norm_group_quant_split(uint8_t* __restrict__ out, float* __restrict__ scal
   using S = typename E::S;
   __shared__ double red_sum[16];
   __shared__ double x_sum;
+  __shared__ int x_fail;
   const int nvec = hidden / VEC;
   const int tpr = (int)blockDim.x;
   const int lt = (int)threadIdx.x;
@@ -251,10 +252,12 @@ k_rms_norm_group_quant_split(uint8_t* __restrict__ out, float* __restrict__ scal
     }
   }
   SplitRowReduce red{red_sum, nullptr, tpr, ws, row, slices, sl,
-                     ws + split_ws_words(rows, slices) - 1, timeout_ticks, &x_sum, nullptr};
+                     ws + split_ws_words(rows, slices) - 1, timeout_ticks, &x_sum, nullptr,
+                     &x_fail};
   ss = red.sum(ss);
   const float rho = mcop_inv_rms(ss, hidden, eps);
   const float ub = scale_ub != nullptr ? *scale_ub : 0.0f;
+  const bool failed = red.failed();  // a failed exchange: NaN scales
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     float m = 0.0f;
@@ -270,7 +273,10 @@ k_rms_norm_group_quant_split(uint8_t* __restrict__ out, float* __restrict__ scal
     const Pack<uint8_t, VEC> q =
         group_codes<E, VEC, FP8>(a[v], m, scale_ub != nullptr, ub, &s);
     const int64_t o = lj_of(v);
-    if (o % group == 0) scales[row * scale_row_stride + (o / group) * scale_group_stride] = s;
+    if (o % group == 0) {
+      scales[row * scale_row_stride + (o / group) * scale_group_stride] =
+          failed ? __builtin_nanf("") : s;
+    }
     st_nt<uint8_t, VEC>(row_elem<true>(out, base, o), q);
   }
 }

@@ -34,6 +34,13 @@ int mcop_debug_set_launch_override(int vectors_per_lane, int lanes_per_row);
  * timing. Results do not change, only speed. */
 int mcop_debug_set_split_rows(int enabled);
 
+/* Makes the split-row launches of later calls made BY THE CALLING THREAD (on = 1) start with
+ * their workspace's error word already set, as a timed-out exchange leaves it, so that every
+ * exchange of the launch fails at once: the grid still drains, and every row's exchanged sum or
+ * maximum is NaN (NaN scales; NaN outputs for the norms). For the test of that failure path;
+ * on = 0 restores normal launches. Calls that take no split-row kernel are unaffected. */
+int mcop_debug_fail_split_waits(int on);
+
 #ifdef __cplusplus
 }
 #endif

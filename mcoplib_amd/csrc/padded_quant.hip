@@ -160,6 +160,7 @@ k_add_rms_norm_quant_padded_split(uint8_t* __restrict__ padded, uint16_t* __rest
   __shared__ float red_max[16];
   __shared__ double x_sum;
   __shared__ float x_max;
+  __shared__ int x_fail;
   const int nvec = hidden / VEC;
   const int tpr = (int)blockDim.x;
   const int lt = (int)threadIdx.x;
@@ -205,17 +206,19 @@ k_add_rms_norm_quant_padded_split(uint8_t* __restrict__ padded, uint16_t* __rest
   ss = row_reduce<true>(ss, red_sum, tpr, SumOp());
   amax = row_reduce<true>(amax, red_max, tpr, MaxOp());
   split_sum_max(ws, row, slices, sl, kSplitTag, &ss, &amax, ws + split_ws_words(rows, slices) - 1,
-                timeout_ticks, &x_sum, &x_max);
+                timeout_ticks, &x_sum, &x_max, &x_fail);
   const float rho = mcop_inv_rms(ss, hidden, eps);
   const float s = __builtin_fmaxf(mcop_div_rn(amax * rho, 127.0f), FLT_EPSILON);
   const float inv = mcop_div_rn(1.0f, s);
-  if (sl == 0 && lt == 0) {
-    scales[row] = s;
+  // slice 0 stores the scale; a slice whose exchange failed stores NaN (split_row.h)
+  if (lt == 0 && (sl == 0 || x_fail != 0)) {
+    const float s_out = x_fail != 0 ? __builtin_nanf("") : s;
+    scales[row] = s_out;
     uint8_t* sp = padded + pbase + hidden;
     if ((reinterpret_cast<uintptr_t>(sp) & 3) == 0) {
-      *reinterpret_cast<float*>(sp) = s;
+      *reinterpret_cast<float*>(sp) = s_out;
     } else {
-      const uint32_t b = __builtin_bit_cast(uint32_t, s);
+      const uint32_t b = __builtin_bit_cast(uint32_t, s_out);
 #pragma unroll
       for (int k = 0; k < 4; ++k) sp[k] = (uint8_t)(b >> (8 * k));
     }

@@ -16,6 +16,8 @@
 // k_per_token_quant_wide (two passes, the row's head held on chip).
 #include <hip/hip_runtime.h>
 
+#include <cfloat>
+
 #include "../../include/mcop_norm.h"
 #include "rowkern.h"
 #include "split_row.h"
@@ -30,9 +32,10 @@ struct PtqRow {
   float s;      // the stored scale
   float inv;    // the multiplier of the codes
   int zp;       // zero point (PTQ_INT8_AZP)
-  bool narrow;  // |zp| <= 2^29: the zero point sum fits int32 (PTQ_INT8_AZP)
+  bool narrow;  // |zp| <= 2^29 and inv finite: the zero point sum fits int32 (PTQ_INT8_AZP)
   bool s_ok;    // s inside the fast-quotient domain (PTQ_FP8)
   bool bounded; // no scale bound cut the row's absmax (PTQ_FP8)
+  bool in_range;  // inv is finite, so every |v * inv| <= 127 * (1 + 2^-23) (PTQ_INT8)
 };
 
 template <int MODE>
@@ -45,10 +48,15 @@ __device__ __forceinline__ PtqRow ptq_row(float mx, float nmn, const float* scal
     // zp = rne(-128 - mn / s) converted with saturation (it lies in [-128, 127] for s > 0)
     r.zp = degenerate ? -128 : cvt_rne_i32(-128.0f - mcop_div_rn(mn, r.s));
     r.inv = degenerate ? 0.0f : mcop_div_rn(1.0f, r.s);
-    r.narrow = r.zp >= -(1 << 29) && r.zp <= (1 << 29);
+    // a subnormal s (a row of tiny values) makes inv infinite, and the products infinite: the
+    // 64-bit sum then keeps -inf at -128 where an int32 sum would wrap
+    r.narrow = r.zp >= -(1 << 29) && r.zp <= (1 << 29) && r.inv <= FLT_MAX;
   } else if constexpr (MODE == PTQ_INT8) {
     r.s = mcop_div_rn(mx, 127.0f);
     r.inv = mx > 0.0f ? mcop_div_rn(127.0f, mx) : 0.0f;
+    // an absmax below 127 / FLT_MAX (tiny bf16 rows) makes inv infinite: the products of the
+    // row's nonzero values are then infinite and saturate, and 0 * inf = NaN codes 0
+    r.in_range = r.inv <= FLT_MAX;
   } else {
     float A = mx;
     if (scale_ub != nullptr) A = __builtin_fminf(A, *scale_ub);
@@ -68,7 +76,8 @@ __device__ __forceinline__ Pack<uint8_t, VEC> ptq_codes(const float* a, const Pt
     // float_to_int32_rn of the reference clamps with fmin/fmax before the saturating
     // conversion, so a NaN product becomes 2^31 -> INT32_MAX and codes 127.  Every finite v lies
     // in [mn, mx], so |v * inv| <= |mn / s| + 255 (to a relative 2^-21), and |zp| >= |mn / s| -
-    // 129.  With |zp| <= 2^29 (uniform over the row) the products stay below 2^30 in magnitude:
+    // 129.  With |zp| <= 2^29 and a finite inv (uniform over the row) the products stay below
+    // 2^30 in magnitude:
     // clamping NaN to 2^30 instead still codes 127, and the int32 sum with zp cannot overflow.
     // Otherwise the sum is formed in 64 bits.  The sum saturates to int8.
     if (r.narrow) {
@@ -85,8 +94,9 @@ __device__ __forceinline__ Pack<uint8_t, VEC> ptq_codes(const float* a, const Pt
       }
     }
   } else if constexpr (MODE == PTQ_INT8) {
-    if constexpr (std::is_same_v<E, F32>) {
-      // fp32 inputs can carry NaN payloads in the low byte: round, convert and saturate
+    if (std::is_same_v<E, F32> || !r.in_range) {
+      // fp32 inputs can carry NaN payloads in the low byte, and an infinite inv gives infinite
+      // products: round, convert and saturate
 #pragma unroll
       for (int e = 0; e < VEC; ++e) q.v[e] = q_i8<-127>(a[e] * r.inv);
     } else {
@@ -180,6 +190,7 @@ k_per_token_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
   __shared__ float red_a[16];
   __shared__ float red_b[16];
   __shared__ float x_max[2];
+  __shared__ int x_fail;
   const int nvec = hidden / VEC;
   const int tpr = (int)blockDim.x;
   const int lt = (int)threadIdx.x;
@@ -209,15 +220,16 @@ k_per_token_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
     mx = row_reduce<true>(mx, red_a, tpr, MaxOp());
     nmn = row_reduce<true>(nmn, red_b, tpr, MaxOp());
     split_max2(split_slots(ws, row, slices, 0), slices, sl, kSplitTag, &mx, &nmn, err,
-               timeout_ticks, x_max);
+               timeout_ticks, x_max, &x_fail);
   } else {
     SplitRowReduce red{nullptr, red_a, tpr, ws, row, slices, sl, err, timeout_ticks, nullptr,
-                       x_max};
+                       x_max, &x_fail};
     mx = red.max(mx);
   }
   const PtqRow r = ptq_row<MODE>(mx, nmn, scale_ub);
-  if (sl == 0 && lt == 0) {
-    scales[row] = r.s;
+  // slice 0 stores the scale; a slice whose exchange failed stores NaN (split_row.h)
+  if (lt == 0 && (sl == 0 || x_fail != 0)) {
+    scales[row] = x_fail != 0 ? __builtin_nanf("") : r.s;
     if constexpr (MODE == PTQ_INT8_AZP) azp[row] = r.zp;
   }
 #pragma unroll

@@ -376,6 +376,7 @@ k_rms_norm_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
   __shared__ float red_max[16];
   __shared__ double x_sum;
   __shared__ float x_max;
+  __shared__ int x_fail;
   const int nvec = hidden / VEC;
   const int tpr = (int)blockDim.x;
   const int lt = (int)threadIdx.x;
@@ -424,7 +425,7 @@ k_rms_norm_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
     }
   }
   SplitRowReduce red{red_sum, red_max, tpr, ws, row, slices, sl, err, timeout_ticks, &x_sum,
-                     &x_max};
+                     &x_max, &x_fail};
   ss = red.sum(ss);
   const float rho = mcop_inv_rms(ss, hidden, eps);
   float amax = 0.0f;
@@ -440,7 +441,9 @@ k_rms_norm_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
   amax = red.max(amax);
   float A;
   const float s = row_scale<FP8, MODE>(amax, rho, scale_ub, &A);
-  if (sl == 0 && lt == 0) scales[row] = s;
+  // slice 0 stores the scale; a slice whose exchange failed stores NaN (split_row.h)
+  const bool failed = red.failed();
+  if (lt == 0 && (sl == 0 || failed)) scales[row] = failed ? __builtin_nanf("") : s;
   const float inv = mcop_div_rn(1.0f, s);
   const bool s_ok = mcop_divisor_ok(s);
   const bool bounded = A == amax && s <= 0x1p100f;

@@ -103,6 +103,7 @@ k_scale_dynamic_quant_split(uint8_t* __restrict__ out, float* __restrict__ scale
   static_assert(R == 1 || R == 2, "one or two rows a workgroup");
   __shared__ float red_max[16 * R];
   __shared__ float x_max[2];
+  __shared__ int x_fail;
   const int nvec = hidden / VEC;
   const int tpr = (int)blockDim.x;
   const int lt = (int)threadIdx.x;
@@ -152,18 +153,19 @@ k_scale_dynamic_quant_split(uint8_t* __restrict__ out, float* __restrict__ scale
   uint64_t* err = ws + split_ws_words(groups, slices) - 1;
   if constexpr (R == 1) {
     SplitRowReduce red{nullptr, red_max, tpr, ws, g, slices, sl, err, timeout_ticks, nullptr,
-                       x_max};
+                       x_max, &x_fail};
     amax[0] = red.max(amax[0]);
   } else {
     amax[0] = row_reduce<true>(amax[0], red_max, tpr, MaxOp());
     amax[1] = row_reduce<true>(amax[1], red_max + 16, tpr, MaxOp());
     split_max2(split_slots(ws, g, slices, 0), slices, sl, kSplitTag, &amax[0], &amax[1], err,
-               timeout_ticks, x_max);
+               timeout_ticks, x_max, &x_fail);
   }
 #pragma unroll
   for (int k = 0; k < R; ++k) {
     if (!live[k]) continue;
-    if (sl == 0 && lt == 0) scales[row[k]] = amax[k] * 0.00787401574803f;
+    // slice 0 stores the scale; a slice whose exchange failed stores it too (NaN: split_row.h)
+    if (lt == 0 && (sl == 0 || x_fail != 0)) scales[row[k]] = amax[k] * 0.00787401574803f;
     const float inv = amax[k] > 0.0f ? mcop_div_rn(127.0f, amax[k]) : 0.0f;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {

@@ -80,24 +80,19 @@ struct WgRowReduce {
 };
 
 // One row (or, for tpr < blockDim, one of the workgroup's rows; or one slice [j0, j0 + jn) of a
-// row shared by several workgroups) given the lane's loaded vectors and its weight and smooth
-// vectors.  `red` combines the row's partial sum of squares and absmax (WgRowReduce, or the
-// split-row exchange).  UA: the row index is uniform and the row's element offsets fit 32 bits
-// (scalar row base, one 32-bit offset per vector: row_elem<true>).
-template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES, bool EX, bool UA,
-          class Red>
-__device__ __forceinline__ void sq_row(const RowPos& p, int j0, int jn,
-                                       const Pack<typename E::S, VEC>* xv,
-                                       const Pack<typename E::S, VEC>* rv,
-                                       const WVec<EW, VEC>* wv, const WVec<ES, VEC>* sv,
-                                       uint8_t* __restrict__ out, float* __restrict__ scales,
-                                       typename E::S* __restrict__ ares,
-                                       typename E::S* __restrict__ anorm, int hidden, int tpr,
-                                       float eps, uint32_t flags, Red& red) {
+// row shared by several workgroups) in three stages around its two reductions, given the lane's
+// loaded vectors and its weight and smooth vectors.  UA: the row index is uniform and the row's
+// element offsets fit 32 bits (scalar row base, one 32-bit offset per vector: row_elem<true>).
+//
+// Stage 1: a = b(x (+ r)) into `a`, after_res stored; returns the lane's sum of squares of the
+// unrounded x (+ r).
+template <class E, int VEC, int NV, bool RES, bool EX, bool UA>
+__device__ __forceinline__ double sq_stage1(const RowPos& p, int j0, int jn,
+                                            const Pack<typename E::S, VEC>* xv,
+                                            const Pack<typename E::S, VEC>* rv, float (*a)[VEC],
+                                            typename E::S* __restrict__ ares, int64_t base,
+                                            int tpr) {
   using S = typename E::S;
-  const int64_t base = p.row * (int64_t)hidden;
-
-  float a[NV][VEC];
   double ss = 0.0;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
@@ -118,8 +113,18 @@ __device__ __forceinline__ void sq_row(const RowPos& p, int j0, int jn,
     ss += in ? vs : 0.0;
     if (ares != nullptr && p.live && in) st_nt<S, VEC>(row_elem<UA>(ares, base, (int64_t)j * VEC), o);
   }
+  return ss;
+}
 
-  ss = red.sum(ss);
+// Stage 2, given the row's sum of squares ss: u = (a / rho) * w (or (a * rho) * w), after_norm
+// stored, a <- v = u * smooth; returns the lane's max |v|.
+template <class E, class EW, class ES, int VEC, int NV, bool RES, bool EX, bool UA>
+__device__ __forceinline__ float sq_stage2(const RowPos& p, int j0, int jn, float (*a)[VEC],
+                                           const WVec<EW, VEC>* wv, const WVec<ES, VEC>* sv,
+                                           typename E::S* __restrict__ anorm, int64_t base,
+                                           int hidden, int tpr, float eps, uint32_t flags,
+                                           double ss) {
+  using S = typename E::S;
   const float rho = mcop_inv_rms(ss, hidden, eps);
   const float inv_rho = mcop_div_rn(1.0f, rho);
   const bool rho_ok = mcop_divisor_ok(rho);
@@ -174,8 +179,15 @@ __device__ __forceinline__ void sq_row(const RowPos& p, int j0, int jn,
       st_nt<S, VEC>(row_elem<UA>(anorm, base, (int64_t)j * VEC), o);
     }
   }
-  amax = red.max(amax);
+  return amax;
+}
 
+// Stage 3, given the row's absmax: the scale (stored by the row's lane 0) and the codes of v.
+template <int VEC, int NV, bool FP8, bool EX, bool UA>
+__device__ __forceinline__ void sq_stage3(const RowPos& p, int j0, int jn, const float (*a)[VEC],
+                                          uint8_t* __restrict__ out,
+                                          float* __restrict__ scales, int64_t base, int tpr,
+                                          float amax) {
   const float s = mcop_div_rn(amax, FP8 ? 448.0f : 127.0f);
   if (p.live && p.lt == 0) scales[p.row] = s;
   const float inv = amax > 0.0f ? mcop_div_rn(1.0f, s) : 0.0f;
@@ -197,6 +209,28 @@ __device__ __forceinline__ void sq_row(const RowPos& p, int j0, int jn,
       st_nt<uint8_t, VEC>(row_elem<UA>(out, base, (int64_t)j * VEC), q);
     }
   }
+}
+
+// The three stages of one row with `red` (WgRowReduce, or the split-row exchange) combining
+// the row's partial sum of squares and absmax.
+template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES, bool EX, bool UA,
+          class Red>
+__device__ __forceinline__ void sq_row(const RowPos& p, int j0, int jn,
+                                       const Pack<typename E::S, VEC>* xv,
+                                       const Pack<typename E::S, VEC>* rv,
+                                       const WVec<EW, VEC>* wv, const WVec<ES, VEC>* sv,
+                                       uint8_t* __restrict__ out, float* __restrict__ scales,
+                                       typename E::S* __restrict__ ares,
+                                       typename E::S* __restrict__ anorm, int hidden, int tpr,
+                                       float eps, uint32_t flags, Red& red) {
+  const int64_t base = p.row * (int64_t)hidden;
+  float a[NV][VEC];
+  double ss = sq_stage1<E, VEC, NV, RES, EX, UA>(p, j0, jn, xv, rv, a, ares, base, tpr);
+  ss = red.sum(ss);
+  float amax = sq_stage2<E, EW, ES, VEC, NV, RES, EX, UA>(p, j0, jn, a, wv, sv, anorm, base,
+                                                         hidden, tpr, eps, flags, ss);
+  amax = red.max(amax);
+  sq_stage3<VEC, NV, FP8, EX, UA>(p, j0, jn, a, out, scales, base, tpr, amax);
 }
 
 // The weight and smooth vectors (L2-resident, shared by every row) are requested before the
@@ -255,6 +289,7 @@ k_rms_norm_smooth_quant_split(uint8_t* __restrict__ out, float* __restrict__ sca
   __shared__ float red_max[16];
   __shared__ double x_sum;
   __shared__ float x_max;
+  __shared__ int x_fail;
   const int nvec = hidden / VEC;
   const int tpr = (int)blockDim.x;
   const int sl = (int)(blockIdx.x % (unsigned)slices);
@@ -277,9 +312,11 @@ k_rms_norm_smooth_quant_split(uint8_t* __restrict__ out, float* __restrict__ sca
   Pack<typename E::S, VEC> xv[NV], rv[NV];
   sq_load<E, VEC, NV, RES, false, true>(p, j0, jn, x, res, hidden, tpr, xv, rv);
   SplitRowReduce red{red_sum, red_max, tpr, ws, p.row, slices, sl,
-                     ws + split_ws_words(rows, slices) - 1, timeout_ticks, &x_sum, &x_max};
+                     ws + split_ws_words(rows, slices) - 1, timeout_ticks, &x_sum, &x_max,
+                     &x_fail};
   sq_row<E, EW, ES, VEC, NV, FP8, RES, false, true>(p, j0, jn, xv, rv, wv, sv, out, scales, ares,
                                                      anorm, hidden, tpr, eps, flags, red);
+  if (red.failed() && p.lt == 0) scales[p.row] = __builtin_nanf("");
 }
 
 // Rows too wide for the registers: one 1024-lane workgroup per row and three passes over it --

@@ -24,7 +24,9 @@
 //     (also with other kernels on the device);
 //   - every wait is bounded by the wall clock all the same: a wait that exceeds it sets the
 //     workspace's error word, and every later wait of the launch returns at once, so the grid
-//     always drains.
+//     always drains.  A row whose exchange failed this way gets NaN for the exchanged sum or
+//     maximum, so its scale (or, for the norms, its output) is NaN: the failure is visible in
+//     the results instead of leaving partial sums in them.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -70,7 +72,9 @@ __device__ __forceinline__ uint64_t ws_get(const uint64_t* p) {
 
 // Wave 0 of the workgroup: waits until the `words` tagged words of each of the group's S slices
 // (at slots[s * 2 + k], k < words) carry `tag`; lane s < S returns its slice's words in w0, w1.
-// False when the wait timed out or an earlier wait of the launch did (error word set).
+// False when the wait timed out or another wait of the launch did before (error word set): the
+// error word is read with every poll of the slots and decides first, so once it is set every
+// later exchange of the launch fails, also one whose slots are complete.
 __device__ __forceinline__ bool split_wait(const uint64_t* slots, int slices, int words,
                                            uint32_t tag, uint64_t* err, int64_t timeout_ticks,
                                            uint64_t* w0, uint64_t* w1) {
@@ -81,10 +85,11 @@ __device__ __forceinline__ bool split_wait(const uint64_t* slots, int slices, in
     if (lane < slices) {
       *w0 = ws_get(slots + lane * 2);
       *w1 = words > 1 ? ws_get(slots + lane * 2 + 1) : ((uint64_t)tag << 32);
-      ok = (uint32_t)(*w0 >> 32) == tag && (uint32_t)(*w1 >> 32) == tag;
     }
+    const uint64_t e = ws_get(err);  // requested with the slot words, not after them
+    if (lane < slices) ok = (uint32_t)(*w0 >> 32) == tag && (uint32_t)(*w1 >> 32) == tag;
+    if (e != 0) return false;
     if (__builtin_amdgcn_ballot_w64(!ok) == 0) return true;
-    if (ws_get(err) != 0) return false;
     if (wall_clock64() - t0 > timeout_ticks) {
       if (lane == 0) ws_put(err, 1, 1);
       return false;
@@ -93,11 +98,26 @@ __device__ __forceinline__ bool split_wait(const uint64_t* slots, int slices, in
   }
 }
 
+// Wave 0, after split_wait of a two-word fp64 exchange: the sum of the S slices' partials (lane
+// s holds slice s's low word in w0, its high word in w1), in slice order.
+__device__ __forceinline__ double slice_sum(uint64_t w0, uint64_t w1, int slices) {
+  const uint32_t lo = (uint32_t)w0, hi = (uint32_t)w1;
+  double total = 0.0;
+  for (int s = 0; s < slices; ++s) {
+    const uint64_t b = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)hi, s) << 32) |
+                       (uint32_t)__builtin_amdgcn_readlane((int)lo, s);
+    total += __builtin_bit_cast(double, b);
+  }
+  return total;
+}
+
 // The group's sum of the slices' fp64 partials, in slice order; `part` is this workgroup's
-// partial (uniform), `sl` its slice.  Every thread of the workgroup calls it.
+// partial (uniform), `sl` its slice.  Every thread of the workgroup calls it.  After a failed
+// wait the sum is NaN and *lds_fail (when given) is 1, else 0; the same holds for the maxima of
+// split_max, split_sum_max and split_max2 below.
 __device__ __forceinline__ double split_sum(uint64_t* slots, int slices, int sl, uint32_t tag,
                                             double part, uint64_t* err, int64_t timeout_ticks,
-                                            double* lds) {
+                                            double* lds, int* lds_fail) {
   if (threadIdx.x == 0) {
     const uint64_t b = __builtin_bit_cast(uint64_t, part);
     ws_put(slots + sl * 2, tag, (uint32_t)b);
@@ -105,15 +125,12 @@ __device__ __forceinline__ double split_sum(uint64_t* slots, int slices, int sl,
   }
   if (threadIdx.x < 64) {
     uint64_t w0 = 0, w1 = 0;
-    split_wait(slots, slices, 2, tag, err, timeout_ticks, &w0, &w1);
-    const uint32_t lo = (uint32_t)w0, hi = (uint32_t)w1;
-    double total = 0.0;
-    for (int s = 0; s < slices; ++s) {
-      const uint64_t b = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)hi, s) << 32) |
-                         (uint32_t)__builtin_amdgcn_readlane((int)lo, s);
-      total += __builtin_bit_cast(double, b);
+    const bool ok = split_wait(slots, slices, 2, tag, err, timeout_ticks, &w0, &w1);
+    const double total = ok ? slice_sum(w0, w1, slices) : __builtin_nan("");
+    if (threadIdx.x == 0) {
+      *lds = total;
+      if (lds_fail != nullptr) *lds_fail = ok ? 0 : 1;
     }
-    if (threadIdx.x == 0) *lds = total;
   }
   __syncthreads();
   return *lds;
@@ -122,14 +139,17 @@ __device__ __forceinline__ double split_sum(uint64_t* slots, int slices, int sl,
 // The group's largest of the slices' (non-negative or NaN-free) fp32 maxima.
 __device__ __forceinline__ float split_max(uint64_t* slots, int slices, int sl, uint32_t tag,
                                            float part, uint64_t* err, int64_t timeout_ticks,
-                                           float* lds) {
+                                           float* lds, int* lds_fail) {
   if (threadIdx.x == 0) ws_put(slots + sl * 2, tag, __builtin_bit_cast(uint32_t, part));
   if (threadIdx.x < 64) {
     uint64_t w0 = 0, w1 = 0;
-    split_wait(slots, slices, 1, tag, err, timeout_ticks, &w0, &w1);
+    const bool ok = split_wait(slots, slices, 1, tag, err, timeout_ticks, &w0, &w1);
     float m = (int)(threadIdx.x & 63) < slices ? __builtin_bit_cast(float, (uint32_t)w0) : 0.0f;
     m = wave_reduce(m, MaxOp());
-    if (threadIdx.x == 0) *lds = m;
+    if (threadIdx.x == 0) {
+      *lds = ok ? m : __builtin_nanf("");
+      if (lds_fail != nullptr) *lds_fail = ok ? 0 : 1;
+    }
   }
   __syncthreads();
   return *lds;
@@ -141,7 +161,7 @@ __device__ __forceinline__ float split_max(uint64_t* slots, int slices, int sl, 
 __device__ __forceinline__ void split_sum_max(uint64_t* ws, int64_t row, int slices, int sl,
                                               uint32_t tag, double* sum, float* mx,
                                               uint64_t* err, int64_t timeout_ticks,
-                                              double* lds_sum, float* lds_max) {
+                                              double* lds_sum, float* lds_max, int* lds_fail) {
   uint64_t* s0 = split_slots(ws, row, slices, 0);
   uint64_t* s1 = split_slots(ws, row, slices, 1);
   if (threadIdx.x == 0) {
@@ -152,20 +172,15 @@ __device__ __forceinline__ void split_sum_max(uint64_t* ws, int64_t row, int sli
   }
   if (threadIdx.x < 64) {
     uint64_t w0 = 0, w1 = 0, m0 = 0, m1 = 0;
-    split_wait(s0, slices, 2, tag, err, timeout_ticks, &w0, &w1);
-    split_wait(s1, slices, 1, tag, err, timeout_ticks, &m0, &m1);
-    const uint32_t lo = (uint32_t)w0, hi = (uint32_t)w1;
-    double total = 0.0;
-    for (int s = 0; s < slices; ++s) {
-      const uint64_t b = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)hi, s) << 32) |
-                         (uint32_t)__builtin_amdgcn_readlane((int)lo, s);
-      total += __builtin_bit_cast(double, b);
-    }
+    bool ok = split_wait(s0, slices, 2, tag, err, timeout_ticks, &w0, &w1);
+    ok = split_wait(s1, slices, 1, tag, err, timeout_ticks, &m0, &m1) && ok;
+    const double total = ok ? slice_sum(w0, w1, slices) : __builtin_nan("");
     float m = (int)(threadIdx.x & 63) < slices ? __builtin_bit_cast(float, (uint32_t)m0) : 0.0f;
     m = wave_reduce(m, MaxOp());
     if (threadIdx.x == 0) {
       *lds_sum = total;
-      *lds_max = m;
+      *lds_max = ok ? m : __builtin_nanf("");
+      *lds_fail = ok ? 0 : 1;
     }
   }
   __syncthreads();
@@ -177,22 +192,23 @@ __device__ __forceinline__ void split_sum_max(uint64_t* ws, int64_t row, int sli
 // one word each.  lds holds two floats.
 __device__ __forceinline__ void split_max2(uint64_t* slots, int slices, int sl, uint32_t tag,
                                            float* a, float* b, uint64_t* err,
-                                           int64_t timeout_ticks, float* lds) {
+                                           int64_t timeout_ticks, float* lds, int* lds_fail) {
   if (threadIdx.x == 0) {
     ws_put(slots + sl * 2, tag, __builtin_bit_cast(uint32_t, *a));
     ws_put(slots + sl * 2 + 1, tag, __builtin_bit_cast(uint32_t, *b));
   }
   if (threadIdx.x < 64) {
     uint64_t w0 = 0, w1 = 0;
-    split_wait(slots, slices, 2, tag, err, timeout_ticks, &w0, &w1);
+    const bool ok = split_wait(slots, slices, 2, tag, err, timeout_ticks, &w0, &w1);
     const bool mine = (int)(threadIdx.x & 63) < slices;
     float ma = mine ? __builtin_bit_cast(float, (uint32_t)w0) : -__builtin_inff();
     float mb = mine ? __builtin_bit_cast(float, (uint32_t)w1) : -__builtin_inff();
     ma = wave_reduce(ma, MaxOp());
     mb = wave_reduce(mb, MaxOp());
     if (threadIdx.x == 0) {
-      lds[0] = ma;
-      lds[1] = mb;
+      lds[0] = ok ? ma : __builtin_nanf("");
+      lds[1] = ok ? mb : __builtin_nanf("");
+      *lds_fail = ok ? 0 : 1;
     }
   }
   __syncthreads();
@@ -214,19 +230,25 @@ struct SplitRowReduce {
   int64_t timeout_ticks;
   double* x_sum;
   float* x_max;
+  int* x_fail = nullptr;  // LDS: 1 after an exchange that failed (nullptr: not recorded)
   __device__ __forceinline__ double sum(double v) {
     v = row_reduce<true>(v, red_sum, tpr, SumOp());
     return split_sum(split_slots(ws, row, slices, 0), slices, sl, kSplitTag, v, err,
-                     timeout_ticks, x_sum);
+                     timeout_ticks, x_sum, x_fail);
   }
   __device__ __forceinline__ float max(float v) {
     v = row_reduce<true>(v, red_max, tpr, MaxOp());
     return split_max(split_slots(ws, row, slices, 1), slices, sl, kSplitTag, v, err,
-                     timeout_ticks, x_max);
+                     timeout_ticks, x_max, x_fail);
   }
+  // After the row's last exchange, in every thread: whether it failed (then every later
+  // exchange of the launch failed too; the kernel writes NaN scales for the row).
+  __device__ __forceinline__ bool failed() const { return x_fail != nullptr && *x_fail != 0; }
 };
 
-__global__ void k_fill_u64(uint64_t* __restrict__ p, int64_t n);
+// Zeroes the n words of a launch's workspace and writes `last` into its last word (the error
+// word: 0, or nonzero to fail every wait of the launch at once, a test hook's forced failure).
+__global__ void k_fill_u64(uint64_t* __restrict__ p, int64_t n, uint64_t last);
 
 // Host side -------------------------------------------------------------------------------------
 

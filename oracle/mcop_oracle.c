@@ -451,8 +451,11 @@ void oracle_dynamic_scaled_int8_quant(int8_t* out, float* scales, const void* x,
 /* vLLM dynamic_scaled_int8_quant with azp (asymmetric), int8_quant_kernels.cu:370-422:
      s = (max x - min x) / 255; zp = (int32) nearbyint(-128 - min x / s); inv = 1 / s;
      q = sat[-128,127](float_to_int32_rn(x * inv) + zp)  (int32_to_int8, :37-46);
-   a NaN element therefore codes 127.  The integer sum is formed in 64 bits (the reference's
-   int32 sum overflows only for a NaN element with zp > 0, where saturation gives 127 too).
+   a NaN element therefore codes 127.  The integer sum is formed in 64 bits, so it saturates
+   instead of overflowing: the reference's int32 sum overflows, which C leaves undefined, for a
+   NaN element or a product of +inf with zp > 0, and for a product of -inf with zp < 0 (inv =
+   1 / s is infinite when s is subnormal, a row of tiny values); here those code 127, 127 and
+   -128, the codes of the clamped values.
    A constant row (s == 0) has no zero point -- the reference converts NaN / inf to int there,
    which has no defined result; this restatement writes s = 0, zp = -128 and q = -128. */
 void oracle_dynamic_scaled_int8_azp_quant(int8_t* out, float* scales, int32_t* azp,

@@ -154,8 +154,9 @@ def test_misaligned_views_take_the_scalar_path():
 def test_special_values():
     say("special values: zero, constant, inf, nan, huge, tiny rows")
     H = 512
+    # the 1e-38 row's absmax lies below 127 / FLT_MAX in bf16 and fp32: 127 / A is infinite
     rows = [torch.zeros(H), torch.full((H,), 2.5), torch.full((H,), -7.0), torch.randn(H) * 1e-30,
-            torch.randn(H).clamp(-3, 3) * 1e38]
+            torch.randn(H).clamp(-3, 3) * 1e38, torch.randn(H) * 1e-38]
     r = torch.randn(H)
     r[7] = float("inf")
     rows.append(r)

@@ -483,10 +483,11 @@ def _padded(x, r, w, pad):
 def test_split_padded_against_oracle_and_multipass(H, extra):
     """The padded wire-format op (its generic chain): every padded row byte, the residual,
     output_rms, codes and scales against the oracle and, bit for bit, against the multi-pass
-    kernel; `extra` spare bytes after each row's scale stay untouched."""
+    kernel; the spare bytes (at least `extra`) after each row's scale stay untouched."""
     say(f"split padded H={H} extra={extra}")
     T = 3
-    pad = (H + 4 + extra + 1) // 2
+    # whole 8-byte units a padded row (the vector path, hence the split-row kernel, needs them)
+    pad = (H + 4 + extra + 7) // 8 * 4
     x, r, w = _x(T, H, 125, torch.bfloat16), _x(T, H, 126, torch.bfloat16), _w(H, 127,
                                                                                  torch.bfloat16)
     refs = oracle.add_rms_norm_quant_padded(x, r, w, pad, 1e-6)
@@ -505,7 +506,7 @@ def test_split_padded_wide_padded_workload_rows():
     """The bench's wide-padded workload, 2048 x 131072: blocks of rows at the start, the middle
     and the end against the oracle, padded bytes included."""
     T, H = 2048, 131072
-    pad = (H + 4 + 1) // 2
+    pad = (H + 4 + 63) // 64 * 32  # the bench's padded rows
     say(f"split: the wide-padded workload {T}x{H}")
     x, r, w = _x(T, H, 128, torch.bfloat16), _x(T, H, 129, torch.bfloat16), _w(H, 130,
                                                                                  torch.bfloat16)

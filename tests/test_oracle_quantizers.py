@@ -46,6 +46,19 @@ def test_int8_zero_and_inf_rows_give_zero_codes():
     assert torch.count_nonzero(q) == 0
 
 
+def test_int8_tiny_row_has_an_infinite_inverse():
+    """A row whose absmax lies below 127 / FLT_MAX (bf16 and fp32 reach it; fp16 cannot): the
+    binary32 quotient 127 / A overflows to inf, so every nonzero element's product is infinite
+    and saturates to +-127, and 0 * inf = NaN converts to 0 -- not the codes of the exact
+    quotient, which would round these elements to +-127 and +-64."""
+    x = torch.tensor([[2e-38, -2e-38, 1e-38, 0.0, -1e-38]], dtype=torch.bfloat16)
+    A = np.float32(x.float().abs().max().item())
+    assert np.isinf(np.float32(127.0) / A)  # the premise: the binary32 quotient overflows
+    q, s, _ = oracle.dynamic_scaled_int8_quant(x)
+    assert q.tolist() == [[127, -127, 127, 0, -127]]
+    assert s.item() == float(A / np.float32(127.0))
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_int8_torch_restatement(dtype):
     x = (torch.randn(128, 1031, generator=_gen(1)) * 3).to(dtype)
@@ -103,6 +116,23 @@ def test_azp_all_positive_row_has_large_zero_point():
     assert azp.item() == -255128
     # 1/s rounds to 254.99998, so the middle value lands at 255127.48 -> 255127 -> -1
     assert q.tolist() == [[-128, -1, 127]]
+
+
+def test_azp_tiny_row_saturates_infinite_products():
+    """A row of tiny values: s = (max - min) / 255 is subnormal, so inv = 1 / s is infinite and
+    every nonzero product is +-inf.  float_to_int32_rn clamps them to +-2^31, i.e. INT32_MAX /
+    INT32_MIN, and the zero point is negative here, so the int32 sum of the reference would
+    wrap for -inf; the restatement saturates instead: -inf codes -128 (not 127), +inf 127, and
+    0 * inf = NaN 127 like any NaN product."""
+    x = torch.tensor([[4e-39, -2e-39, 0.0]], dtype=torch.float32)
+    mx, mn = np.float32(x[0, 0].item()), np.float32(x[0, 1].item())
+    s32 = (mx - mn) / np.float32(255.0)
+    assert np.isinf(np.float32(1.0) / s32)  # the premise: inv overflows
+    zp = int(np.rint(np.float32(-128.0) - mn / s32))
+    assert zp < 0
+    q, s, azp = oracle.dynamic_scaled_int8_quant(x, use_azp=True)
+    assert s.item() == float(s32) and azp.item() == zp
+    assert q.tolist() == [[127, -128, 127]]
 
 
 def test_azp_nan_element_codes_like_the_fmin_clamp():
