@@ -304,7 +304,8 @@ KERNEL_NAME = {"add_norm_int8": "k_rms_norm_quant", "norm_int8": "k_rms_norm_qua
 
 # kinds whose wide rows take a split-row kernel (the others a multi-pass kernel); --multi-pass
 # sends them to the multi-pass kernels too
-SPLIT_KINDS = {"add_norm_int8", "fused_add", "smooth_fp8", "sdq"}
+SPLIT_KINDS = {"add_norm_int8", "fused_add", "smooth_fp8", "sdq", "norm_res", "vllm_norm",
+               "ptq_int8", "ptq_int8_azp", "ptq_fp8", "padded", "block_fp8"}
 MULTI_PASS = False
 
 

@@ -51,6 +51,7 @@ COMPILE_FLAGS = [
 FOUR_WAVE_KERNELS = (
     r"^void mcop::k_rms_norm_quant<mcop::BF16, 8, 8, false, (true|false), [0-9], (true|false)>\(",
     r"^void mcop::k_fused_add_rms_norm<mcop::BF16, 8, 8, (true|false)>\(",
+    r"^void mcop::k_rms_norm_quant_split<mcop::BF16, 8, 8, false, (true|false), [0-9]>\(",
 )
 RESOURCES = "resource_usage.json"
 

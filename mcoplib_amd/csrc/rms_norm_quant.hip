@@ -363,8 +363,11 @@ k_rms_norm_quant_wide(uint8_t* __restrict__ out, float* __restrict__ scales,
 // register kernels within the slice).  The row's sum of squares and absmax are the slices'
 // partials combined through the workspace `ws` (split_row.h: split_sum in slice order,
 // split_max); every other step is the register kernel's, element by element.
+// The bf16 int8 form at eight vectors a lane asks for four waves per SIMD, as the register
+// kernel does (left free it took 129 VGPRs and three: 348 against 308 us at 2048 x 131072).
 template <class E, int VEC, int NV, bool FP8, bool RES, int MODE>
 __global__ void __launch_bounds__(max_tpr(VEC, NV))
+__attribute__((amdgpu_waves_per_eu(NV == 8 && !FP8 && std::is_same<E, BF16>::value ? 4 : 1)))
 k_rms_norm_quant_split(uint8_t* __restrict__ out, float* __restrict__ scales,
                        const typename E::S* __restrict__ x, const typename E::S* __restrict__ w,
                        const float* __restrict__ scale_ub, typename E::S* __restrict__ res,

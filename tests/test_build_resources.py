@@ -47,12 +47,17 @@ def test_resource_check_catches_spills():
                          "false>(...)", "mangled": "x", "scratch": 0, "occupancy": 4}
     ok_h1 = {"kernel": "void mcop::k_fused_add_rms_norm<mcop::BF16, 8, 8, false>(...)",
              "mangled": "y", "scratch": 0, "occupancy": 4}
-    assert b.check_resources([ok_four, ok_h1]) == []
+    ok_split = {"kernel": "void mcop::k_rms_norm_quant_split<mcop::BF16, 8, 8, false, true, "
+                          "0>(...)", "mangled": "s", "scratch": 0, "occupancy": 4}
+    oks = [ok_four, ok_h1, ok_split]
+    assert b.check_resources(oks) == []
     wide = {"kernel": "void mcop::k_rms_norm_quant_wide<mcop::F16, 8, true, false, 0>(...)",
             "mangled": "z", "scratch": 16, "occupancy": 4}
-    assert any("multi-pass" in p for p in b.check_resources([ok_four, ok_h1, wide]))
+    assert any("multi-pass" in p for p in b.check_resources(oks + [wide]))
     spilled = dict(ok_four, scratch=20)
-    assert any("four-waves" in p for p in b.check_resources([spilled, ok_h1]))
+    assert any("four-waves" in p for p in b.check_resources([spilled, ok_h1, ok_split]))
     three = dict(ok_h1, occupancy=3)
-    assert any("four-waves" in p for p in b.check_resources([ok_four, three]))
+    assert any("four-waves" in p for p in b.check_resources([ok_four, three, ok_split]))
+    three_split = dict(ok_split, occupancy=3)
+    assert any("four-waves" in p for p in b.check_resources([ok_four, ok_h1, three_split]))
     assert any("no kernel matches" in p for p in b.check_resources([ok_four]))
