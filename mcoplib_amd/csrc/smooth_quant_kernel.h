@@ -80,19 +80,24 @@ struct WgRowReduce {
 };
 
 // One row (or, for tpr < blockDim, one of the workgroup's rows; or one slice [j0, j0 + jn) of a
-// row shared by several workgroups) in three stages around its two reductions, given the lane's
-// loaded vectors and its weight and smooth vectors.  UA: the row index is uniform and the row's
-// element offsets fit 32 bits (scalar row base, one 32-bit offset per vector: row_elem<true>).
-//
-// Stage 1: a = b(x (+ r)) into `a`, after_res stored; returns the lane's sum of squares of the
-// unrounded x (+ r).
-template <class E, int VEC, int NV, bool RES, bool EX, bool UA>
-__device__ __forceinline__ double sq_stage1(const RowPos& p, int j0, int jn,
-                                            const Pack<typename E::S, VEC>* xv,
-                                            const Pack<typename E::S, VEC>* rv, float (*a)[VEC],
-                                            typename E::S* __restrict__ ares, int64_t base,
-                                            int tpr) {
+// row shared by several workgroups) given the lane's loaded vectors and its weight and smooth
+// vectors.  `red` combines the row's partial sum of squares and absmax (WgRowReduce, or the
+// split-row exchange).  UA: the row index is uniform and the row's element offsets fit 32 bits
+// (scalar row base, one 32-bit offset per vector: row_elem<true>).
+template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES, bool EX, bool UA,
+          class Red>
+__device__ __forceinline__ void sq_row(const RowPos& p, int j0, int jn,
+                                       const Pack<typename E::S, VEC>* xv,
+                                       const Pack<typename E::S, VEC>* rv,
+                                       const WVec<EW, VEC>* wv, const WVec<ES, VEC>* sv,
+                                       uint8_t* __restrict__ out, float* __restrict__ scales,
+                                       typename E::S* __restrict__ ares,
+                                       typename E::S* __restrict__ anorm, int hidden, int tpr,
+                                       float eps, uint32_t flags, Red& red) {
   using S = typename E::S;
+  const int64_t base = p.row * (int64_t)hidden;
+
+  float a[NV][VEC];
   double ss = 0.0;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
@@ -113,18 +118,8 @@ __device__ __forceinline__ double sq_stage1(const RowPos& p, int j0, int jn,
     ss += in ? vs : 0.0;
     if (ares != nullptr && p.live && in) st_nt<S, VEC>(row_elem<UA>(ares, base, (int64_t)j * VEC), o);
   }
-  return ss;
-}
 
-// Stage 2, given the row's sum of squares ss: u = (a / rho) * w (or (a * rho) * w), after_norm
-// stored, a <- v = u * smooth; returns the lane's max |v|.
-template <class E, class EW, class ES, int VEC, int NV, bool RES, bool EX, bool UA>
-__device__ __forceinline__ float sq_stage2(const RowPos& p, int j0, int jn, float (*a)[VEC],
-                                           const WVec<EW, VEC>* wv, const WVec<ES, VEC>* sv,
-                                           typename E::S* __restrict__ anorm, int64_t base,
-                                           int hidden, int tpr, float eps, uint32_t flags,
-                                           double ss) {
-  using S = typename E::S;
+  ss = red.sum(ss);
   const float rho = mcop_inv_rms(ss, hidden, eps);
   const float inv_rho = mcop_div_rn(1.0f, rho);
   const bool rho_ok = mcop_divisor_ok(rho);
@@ -179,15 +174,8 @@ __device__ __forceinline__ float sq_stage2(const RowPos& p, int j0, int jn, floa
       st_nt<S, VEC>(row_elem<UA>(anorm, base, (int64_t)j * VEC), o);
     }
   }
-  return amax;
-}
+  amax = red.max(amax);
 
-// Stage 3, given the row's absmax: the scale (stored by the row's lane 0) and the codes of v.
-template <int VEC, int NV, bool FP8, bool EX, bool UA>
-__device__ __forceinline__ void sq_stage3(const RowPos& p, int j0, int jn, const float (*a)[VEC],
-                                          uint8_t* __restrict__ out,
-                                          float* __restrict__ scales, int64_t base, int tpr,
-                                          float amax) {
   const float s = mcop_div_rn(amax, FP8 ? 448.0f : 127.0f);
   if (p.live && p.lt == 0) scales[p.row] = s;
   const float inv = amax > 0.0f ? mcop_div_rn(1.0f, s) : 0.0f;
@@ -209,28 +197,6 @@ __device__ __forceinline__ void sq_stage3(const RowPos& p, int j0, int jn, const
       st_nt<uint8_t, VEC>(row_elem<UA>(out, base, (int64_t)j * VEC), q);
     }
   }
-}
-
-// The three stages of one row with `red` (WgRowReduce, or the split-row exchange) combining
-// the row's partial sum of squares and absmax.
-template <class E, class EW, class ES, int VEC, int NV, bool FP8, bool RES, bool EX, bool UA,
-          class Red>
-__device__ __forceinline__ void sq_row(const RowPos& p, int j0, int jn,
-                                       const Pack<typename E::S, VEC>* xv,
-                                       const Pack<typename E::S, VEC>* rv,
-                                       const WVec<EW, VEC>* wv, const WVec<ES, VEC>* sv,
-                                       uint8_t* __restrict__ out, float* __restrict__ scales,
-                                       typename E::S* __restrict__ ares,
-                                       typename E::S* __restrict__ anorm, int hidden, int tpr,
-                                       float eps, uint32_t flags, Red& red) {
-  const int64_t base = p.row * (int64_t)hidden;
-  float a[NV][VEC];
-  double ss = sq_stage1<E, VEC, NV, RES, EX, UA>(p, j0, jn, xv, rv, a, ares, base, tpr);
-  ss = red.sum(ss);
-  float amax = sq_stage2<E, EW, ES, VEC, NV, RES, EX, UA>(p, j0, jn, a, wv, sv, anorm, base,
-                                                         hidden, tpr, eps, flags, ss);
-  amax = red.max(amax);
-  sq_stage3<VEC, NV, FP8, EX, UA>(p, j0, jn, a, out, scales, base, tpr, amax);
 }
 
 // The weight and smooth vectors (L2-resident, shared by every row) are requested before the
