@@ -130,3 +130,25 @@ def test_guard_without_a_profile_or_below_the_bar():
     assert bench.guard_of(0.7501, prof, wl.bytes)["regressed"] is False
     prof["hbm_bytes_per_dispatch"] = wl.bytes * 1.02
     assert bench.guard_of(0.77, prof, wl.bytes)["regressed"] is True
+
+
+def test_every_benched_workload_names_a_profiled_kernel():
+    """Each bandwidth workload's kernel name (the split-row kernel for the wide workloads of
+    every operator that has one, the multi-pass kernel under --multi-pass) has its committed
+    rocprofv3 summary, so the bench never attributes a workload to a kernel that does not run.
+    (Whether a summary is current is the bench's own guard: profile_stale.)"""
+    from pathlib import Path
+    missing = []
+    for name, wl in bench.WORKLOADS.items():
+        if name.startswith("cfg5-decode") or name == "cfg1":
+            continue
+        for mp in ((False, True) if name.startswith("wide-") else (False,)):
+            bench.MULTI_PASS = mp
+            try:
+                kn = bench.kernel_name(wl)
+            finally:
+                bench.MULTI_PASS = False
+            p = Path(bench.ROOT) / "profiles" / f"{kn}_{name}.txt"
+            if not p.exists():
+                missing.append(str(p.name))
+    assert not missing, missing
