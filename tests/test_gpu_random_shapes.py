@@ -56,6 +56,36 @@ def test_random_shape(seed):
     T, H = _shape(rng)
     dtype = rng.choice(DTYPES)
     say(f"random seed={seed}: {name} T={T} H={H} {dtype}")
+    _check(seed, rng, name, T, H, dtype)
+
+
+def _wide_shape(rng: random.Random):
+    """Rows past the register-resident kernels: mostly whole 16-byte vectors (the split-row
+    kernels, 2 to 64 slices), a few odd widths (the element-wise multi-pass kernels)."""
+    kind = rng.random()
+    if kind < 0.85:
+        H = 8 * rng.randint(8193, 48000)
+    elif kind < 0.95:
+        H = rng.choice([65544, 131072, 262144, 393216])
+    else:
+        H = rng.randint(65537, 140000) | 1
+    T = rng.choice([1, 2, 3, 5, 9, rng.randint(1, 24)])
+    return T, H
+
+
+@pytest.mark.parametrize("seed", range(1000, 1096))
+def test_random_wide_shape(seed):
+    """Seeded random rows wider than one workgroup's registers through every operator."""
+    rng = random.Random(seed)
+    name = OPS[seed % len(OPS)]
+    T, H = _wide_shape(rng)
+    dtype = rng.choice(DTYPES)
+    say(f"random wide seed={seed}: {name} T={T} H={H} {dtype}")
+    _check(seed, rng, name, T, H, dtype)
+
+
+def _check(seed, rng, name, T, H, dtype):
+    """One seeded case of operator `name` at [T, H] in `dtype` against the oracle."""
     eps = rng.choice([1e-6, 1e-5])
     if name == "h1":
         x, r, w = _x(T, H, seed, dtype), _x(T, H, seed + 1, dtype), _w(H, seed + 2, dtype)
